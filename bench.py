@@ -1,0 +1,249 @@
+"""bench.py — Q4_K decode matvec throughput on one MI355X (BASELINE metric).
+
+A "step" is one pass of the hot path over one batch of synthetic input: the
+seven batch-1 projections of one Llama-3-8B layer (Q 4096x4096, K and V
+1024x4096, O 4096x4096, gate and up 14336x4096, down 4096x14336) in Q4_K,
+each a `quantized_matmul` over raw GGUF blocks.
+Steps cycle through `--copies` distinct copies of the layer (8 x 122.7 MB by
+default) so no step re-reads weights left in the 256 MB last-level cache;
+all inputs are resident in HBM before the timed region.  Timing: HIP events
+recorded on the backend stream around a HIP graph holding exactly K steps,
+bracketed by device synchronisation.
+
+value = algorithmic bytes of K steps (weights + x + y of every projection)
+/ elapsed seconds, in GB/s.  Extra fields report the per-matrix rates, the
+Q6_K/Q8_0 layers, the TinyLlama-shape sweep, the roofline of
+the dominant kernel (Q4_K 14336x4096) and the CPU baseline: the oracle's
+restatement of Yule's AVX2 qmv (oracle/cpu_avx2.c) timed on the host cores.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--copies C] [--quick]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+from yule_amd import DType, matrix_bytes, synth  # noqa: E402
+
+METRIC = "Q4_K matvec HBM GB/s (% of 8 TB/s peak); Q4_K_M decode tokens/sec, 1 GPU"
+HBM_PEAK_GBS = 8000.0
+
+# Llama-3-8B per-layer projections (n_rows, n_cols)
+LLAMA3_LAYER = [("attn_q", 4096, 4096), ("attn_k", 1024, 4096), ("attn_v", 1024, 4096),
+                ("attn_output", 4096, 4096), ("ffn_gate", 14336, 4096), ("ffn_up", 14336, 4096),
+                ("ffn_down", 4096, 14336)]
+LLAMA3_LM_HEAD = ("output", 128256, 4096)
+# TinyLlama-1.1B projections
+TINY_SWEEP = [("q_o", 2048, 2048, DType.Q4_K), ("k_v", 256, 2048, DType.Q4_K), ("gate_up", 5632, 2048, DType.Q4_K),
+              ("down", 2048, 5632, DType.Q4_K), ("lm_head", 32000, 2048, DType.Q6_K)]
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def algo_bytes(dt, n_rows, n_cols) -> int:
+    """Algorithmic bytes of one matvec: the weight blocks + f32 x + f32 y."""
+    return matrix_bytes(dt, n_rows, n_cols) + 4 * n_cols + 4 * n_rows
+
+
+class Layer:
+    """`copies` device copies of one layer's projections in one format."""
+
+    def __init__(self, hip, dt, shapes, copies, seed):
+        self.hip, self.dt, self.shapes = hip, dt, shapes
+        self.host = {}
+        self.w = {}
+        self.x = {}
+        self.y = {}
+        for i, (name, r, c) in enumerate(shapes):
+            t0 = time.time()
+            self.host[name] = synth.gen_quant(dt, seed + i, r, c)
+            self.w[name] = [hip.upload(self.host[name]) for _ in range(copies)]
+            if c not in self.x:
+                xs = synth.gauss(seed + 1000 + c, c)
+                self.host[f"x{c}"] = xs
+                self.x[c] = hip.upload(xs)
+            self.y[name] = [hip.allocate(4 * r) for _ in range(copies)]
+            log(f"  {dt.name} {name} {r}x{c}: {matrix_bytes(dt, r, c) / 1e6:.1f} MB x{copies} ({time.time() - t0:.1f}s)")
+        self.copies = copies
+        self.step_bytes = sum(algo_bytes(dt, r, c) for _, r, c in shapes)
+
+    def ops_for_step(self, s):
+        c = s % self.copies
+        return [(self.w[n][c], self.x[cols], self.y[n][c], r, cols, self.dt) for n, r, cols in self.shapes]
+
+    def ops_for_matrix(self, name, n):
+        _, r, cols = next(s for s in self.shapes if s[0] == name)
+        return [(self.w[name][i % self.copies], self.x[cols], self.y[name][i % self.copies], r, cols, self.dt)
+                for i in range(n)]
+
+    def free(self):
+        for lst in list(self.w.values()) + list(self.y.values()):
+            for h in lst:
+                self.hip.free(h)
+        for h in self.x.values():
+            self.hip.free(h)
+
+
+def time_steps(hip, layer, steps, start=0):
+    ops = [op for s in range(start, start + steps) for op in layer.ops_for_step(s)]
+    hip.synchronize()
+    ms = hip.time_qmv_ops(ops, 1, use_graph=True)
+    hip.synchronize()
+    return ms
+
+
+def matrix_rate(hip, layer, name, launches):
+    _, r, c = next(s for s in layer.shapes if s[0] == name)
+    hip.time_qmv_ops(layer.ops_for_matrix(name, min(launches, 64)), 1)       # warm-up
+    ms = hip.time_qmv_ops(layer.ops_for_matrix(name, launches), 1)
+    us = 1e3 * ms / launches
+    gbs = algo_bytes(layer.dt, r, c) / (us * 1e-6) / 1e9
+    return us, gbs
+
+
+def cpu_baseline(layer, budget_s=12.0, max_passes=40):
+    """Yule's CPU decode matvec path (oracle restatement of model_runner.rs:
+    152-244 + simd/avx2.rs) over the same Q4_K layer bytes, host-resident."""
+    import oracle
+    threads = min(16, os.cpu_count() or 1)
+    mats = [(layer.host[n], layer.host[f"x{c}"], r, c) for n, r, c in layer.shapes]
+    for w, x, r, c in mats:                       # warm-up pass
+        oracle.qmv(int(layer.dt), w, x, r, c, threads)
+    passes, t0 = 0, time.perf_counter()
+    while passes < max_passes and (passes < 2 or time.perf_counter() - t0 < budget_s):
+        for w, x, r, c in mats:
+            oracle.qmv(int(layer.dt), w, x, r, c, threads)
+        passes += 1
+    dt = time.perf_counter() - t0
+    gbs = passes * layer.step_bytes / dt / 1e9
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{passes} passes of the Q4_K Llama-3-8B layer (7 projections, "
+                      f"{layer.step_bytes / 1e6:.1f} MB each pass) through the oracle's restatement of Yule's "
+                      f"AVX2 qmv with a per-call std::thread row split, {threads} threads, {dt:.1f} s",
+            "host_cpu": _cpu_model()}
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def traffic_from_profiles():
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3
+    --pmc summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel factor)."""
+    p = ROOT / "profiles" / "qmv_q4k_14336x4096_traffic.json"
+    if p.exists():
+        try:
+            return json.loads(p.read_text()).get("bytes_per_launch")
+        except Exception:
+            return None
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--copies", type=int, default=8)
+    ap.add_argument("--quick", action="store_true", help="primary metric and roofline only")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the matvec shards by "
+              f"rows with no exchange, so N GPUs would each run 1/N of every projection.", file=sys.stderr)
+        sys.exit(2)
+
+    from yule_amd.backend import HipBackend
+    hip = HipBackend(0)
+    info = hip.device_info()
+    log(f"device: {info.name}, {info.compute_units} CUs, {info.memory_bytes / 2**30:.0f} GiB")
+
+    log("generating Llama-3-8B Q4_K layer")
+    q4k = Layer(hip, DType.Q4_K, LLAMA3_LAYER, args.copies, seed=11)
+
+    # warm-up steps, then exactly K timed steps
+    time_steps(hip, q4k, args.warmup)
+    ms = time_steps(hip, q4k, args.steps)
+    ms_per_step = ms / args.steps
+    value = q4k.step_bytes * args.steps / (ms * 1e-3) / 1e9
+    log(f"Q4_K layer: {ms_per_step * 1e3:.2f} us/step, {value:.1f} GB/s ({100 * value / HBM_PEAK_GBS:.1f}% of peak)")
+
+    # dominant kernel: Q4_K 14336x4096 (gate/up), average launch duration
+    n_dom = 1000
+    us, gbs = matrix_rate(hip, q4k, "ffn_gate", n_dom)
+    dom_bytes = algo_bytes(DType.Q4_K, 14336, 4096)
+    roofline = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(),
+                "kernel": "qmv_kernel<Q4K,64,8> 14336x4096", "avg_launch_us": round(us, 3),
+                "algo_bytes_per_launch": dom_bytes}
+    log(f"dominant kernel Q4_K 14336x4096: {us:.2f} us/launch, {gbs:.1f} GB/s")
+
+    extra = {"per_matrix_q4k": {}}
+    for name, r, c in LLAMA3_LAYER:
+        u, g = matrix_rate(hip, q4k, name, 400)
+        extra["per_matrix_q4k"][f"{name} {r}x{c}"] = {"us": round(u, 2), "GB/s": round(g, 1)}
+
+    cpu = None if args.no_cpu else cpu_baseline(q4k)
+    if cpu:
+        log(f"CPU baseline: {cpu['value']} GB/s on {cpu['cores']} threads ({cpu['host_cpu']})")
+    q4k.free()
+
+    if not args.quick:
+        for dt in (DType.Q6_K, DType.Q8_0):
+            log(f"generating Llama-3-8B {dt.name} layer")
+            L = Layer(hip, dt, LLAMA3_LAYER, args.copies, seed=21 + int(dt))
+            n = max(64, args.steps // 4)
+            time_steps(hip, L, 32)
+            m = time_steps(hip, L, n)
+            g = L.step_bytes * n / (m * 1e-3) / 1e9
+            extra[f"llama3_layer_{dt.name.lower()}_GB/s"] = round(g, 1)
+            log(f"{dt.name} layer: {g:.1f} GB/s")
+            L.free()
+        for dt in (DType.Q4_K, DType.Q6_K, DType.Q8_0):
+            L = Layer(hip, dt, [LLAMA3_LM_HEAD], 1, seed=31 + int(dt))
+            u, g = matrix_rate(hip, L, "output", 50)
+            extra[f"llama3_lm_head_{dt.name.lower()}"] = {"us": round(u, 1), "GB/s": round(g, 1)}
+            log(f"lm_head 128256x4096 {dt.name}: {u:.1f} us, {g:.1f} GB/s")
+            L.free()
+        sweep = {}
+        for name, r, c, dt in TINY_SWEEP:
+            L = Layer(hip, dt, [(name, r, c)], 16, seed=41)
+            u, g = matrix_rate(hip, L, name, 800)
+            sweep[f"{name} {r}x{c} {dt.name}"] = {"us": round(u, 2), "GB/s": round(g, 1)}
+            L.free()
+        extra["tinyllama_sweep"] = sweep
+
+    out = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic: W ~ N(0,0.02) seeded, GGUF Q4_K blocks; x ~ N(0,1) f32",
+        "config": {"workload": "Llama-3-8B layer projections, Q4_K decode matvec, batch 1 (BASELINE configs[2])",
+                   "hidden": 4096, "ffn": 14336, "kv_heads": 8, "head_dim": 128, "layer_copies": args.copies,
+                   "step_bytes": q4k.step_bytes},
+        "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "roofline": roofline, "cpu_baseline": cpu, "device": info.name, **extra,
+    }
+    hip.close()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

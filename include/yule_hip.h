@@ -1,0 +1,188 @@
+/*
+ * yule_hip.h — C ABI of libyule_hip.so, the MI355X (gfx950) HIP backend for
+ * Yule.  It mirrors the yule-gpu ComputeBackend trait
+ * (yule-gpu/src/lib.rs:21-132) one entry point per trait method, so a Rust
+ * `impl ComputeBackend for HipBackend` can forward each method to one call
+ * (binding shown in INTEGRATION.md).
+ *
+ * Conventions
+ *  - Every call returns 0 (YULE_OK) or a YULE_ERR_* code; the message of the
+ *    last failure on the calling thread is yule_hip_last_error().  This is
+ *    the trait's Result<()> / YuleError::Gpu(String)
+ *    (yule-core/src/error.rs:44).
+ *  - Buffers are opaque 64-bit handles (BufferHandle(pub u64),
+ *    yule-gpu/src/lib.rs:135), zero-initialised on allocation
+ *    (yule-gpu/src/cpu.rs:157).
+ *  - Kernels are enqueued on one stream owned by the backend, in call order.
+ *    copy_from_device and synchronize block; copy_to_device returns after the
+ *    host bytes have been consumed.  This matches the CUDA backend's
+ *    ordering (yule-gpu/src/cuda/mod.rs, cuda/memory.rs:75-78).
+ *  - Sizes that would read or write outside a buffer are rejected with
+ *    YULE_ERR_INVALID before any kernel is launched.
+ *  - dtype values are GGUF type ids (yule-core/src/dtype.rs:21-33).
+ */
+#ifndef YULE_HIP_H
+#define YULE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define YULE_OK 0
+#define YULE_ERR_INVALID 1     /* bad argument, size or handle */
+#define YULE_ERR_UNSUPPORTED 2 /* dtype / op not supported (trait default Err) */
+#define YULE_ERR_NO_DEVICE 3   /* no usable gfx950 device */
+#define YULE_ERR_OOM 4         /* device allocation failed */
+#define YULE_ERR_HIP 5         /* HIP runtime error */
+
+#define YULE_DTYPE_F32 0
+#define YULE_DTYPE_F16 1
+#define YULE_DTYPE_Q4_0 2
+#define YULE_DTYPE_Q8_0 8
+#define YULE_DTYPE_Q4_K 12
+#define YULE_DTYPE_Q6_K 14
+
+typedef struct yule_hip_backend yule_hip_backend;
+typedef uint64_t yule_buffer;
+
+/* DeviceInfo, yule-gpu/src/lib.rs:137-143; backend is always 4 (HIP) here */
+typedef struct {
+    char name[256];
+    uint32_t backend;
+    uint64_t memory_bytes;
+    uint32_t compute_units;
+} yule_device_info;
+
+const char *yule_hip_last_error(void);
+
+/* Vulkan/CUDA is_available() probes (yule-gpu/src/vulkan/device.rs:150);
+ * 1 when a gfx950 device is present, else 0. */
+int yule_hip_is_available(void);
+
+/* create_backend(BackendKind) (yule-gpu/src/lib.rs:175-189) */
+int yule_hip_create(int device, yule_hip_backend **out);
+int yule_hip_destroy(yule_hip_backend *be);
+
+/* ComputeBackend::name (lib.rs:22) -> "hip" */
+const char *yule_hip_name(const yule_hip_backend *be);
+/* ComputeBackend::device_info (lib.rs:23) */
+int yule_hip_device_info(yule_hip_backend *be, yule_device_info *out);
+
+/* ComputeBackend::allocate / free (lib.rs:24-25) */
+int yule_hip_allocate(yule_hip_backend *be, size_t size_bytes, yule_buffer *out);
+int yule_hip_free(yule_hip_backend *be, yule_buffer h);
+
+/* copy_to_device / copy_from_device / copy_buffer / copy_buffer_offset /
+ * synchronize (lib.rs:68-80) */
+int yule_hip_copy_to_device(yule_hip_backend *be, const void *data, size_t size, yule_buffer h);
+int yule_hip_copy_from_device(yule_hip_backend *be, yule_buffer h, void *data, size_t size);
+int yule_hip_copy_buffer(yule_hip_backend *be, yule_buffer src, yule_buffer dst, size_t size);
+int yule_hip_copy_buffer_offset(yule_hip_backend *be, yule_buffer src, yule_buffer dst,
+                                size_t src_offset, size_t dst_offset, size_t size);
+int yule_hip_synchronize(yule_hip_backend *be);
+
+/* ComputeBackend::matmul (lib.rs:26-34): C[m,n] = A[m,k] * B[k,n], f32 row-major */
+int yule_hip_matmul(yule_hip_backend *be, yule_buffer a, yule_buffer b, yule_buffer out,
+                    uint32_t m, uint32_t n, uint32_t k);
+/* ComputeBackend::softmax (lib.rs:35) */
+int yule_hip_softmax(yule_hip_backend *be, yule_buffer in, yule_buffer out, uint32_t size);
+/* ComputeBackend::rms_norm (lib.rs:36-43): out = in / sqrt(mean(in^2)+eps) * weight */
+int yule_hip_rms_norm(yule_hip_backend *be, yule_buffer in, yule_buffer weight, yule_buffer out,
+                      uint32_t size, float eps);
+/* ComputeBackend::rope (lib.rs:44-53): in place on q and k, interleaved pairs,
+ * freq_i = 1/freq_base^(2i/head_dim), every head of each buffer. */
+int yule_hip_rope(yule_hip_backend *be, yule_buffer q, yule_buffer k, uint32_t pos,
+                  uint32_t head_dim, float freq_base, uint32_t n_heads_q, uint32_t n_heads_k);
+/* ComputeBackend::silu (lib.rs:54): out = in * sigmoid(in) (the trait's and
+ * CpuBackend's meaning, yule-gpu/src/cpu.rs:339-357) */
+int yule_hip_silu(yule_hip_backend *be, yule_buffer in, yule_buffer out, uint32_t size);
+/* ComputeBackend::element_mul (lib.rs:55-61): out = a * b */
+int yule_hip_element_mul(yule_hip_backend *be, yule_buffer a, yule_buffer b, yule_buffer out,
+                         uint32_t size);
+/* ComputeBackend::add (lib.rs:62-68): out = a + b */
+int yule_hip_add(yule_hip_backend *be, yule_buffer a, yule_buffer b, yule_buffer out, uint32_t size);
+
+/* ComputeBackend::attn_score (lib.rs:82-96):
+ * scores[t] = (q[head_offset..+hd] . k[t*kv_stride+kv_offset..+hd]) / sqrt(hd) */
+int yule_hip_attn_score(yule_hip_backend *be, yule_buffer q, yule_buffer k_cache, yule_buffer scores,
+                        uint32_t head_dim, uint32_t seq_len, uint32_t head_offset,
+                        uint32_t kv_offset, uint32_t kv_stride);
+/* ComputeBackend::attn_value (lib.rs:98-114):
+ * out[out_offset+d] = sum_t w[t] * v[t*kv_stride+kv_offset+d] */
+int yule_hip_attn_value(yule_hip_backend *be, yule_buffer weights, yule_buffer v_cache,
+                        yule_buffer out, uint32_t head_dim, uint32_t seq_len,
+                        uint32_t kv_offset, uint32_t kv_stride, uint32_t out_offset);
+
+/* ComputeBackend::quantized_matmul (lib.rs:116-131) — the hot path.
+ * y[r] = sum_b vec_dot(W[r, b], x[b*bs .. (b+1)*bs]) for r < n_rows.
+ * weights: raw GGUF blocks, row-major, n_cols/bs blocks per row;
+ * input: f32[n_cols]; output: f32[n_rows], fully overwritten.
+ * dtype: Q4_0, Q8_0, Q4_K or Q6_K; n_cols must be a multiple of the block
+ * size (GGUF rows always are).  Other dtypes -> YULE_ERR_UNSUPPORTED, as the
+ * Vulkan backend's Err (yule-gpu/src/vulkan/mod.rs:333-343). */
+int yule_hip_quantized_matmul(yule_hip_backend *be, yule_buffer weights, yule_buffer input,
+                              yule_buffer output, uint32_t n_rows, uint32_t n_cols, uint32_t dtype);
+
+/* ---- extensions beyond the trait (used by the HIP runner) ---- */
+
+/* dequant_block over n_blocks consecutive blocks starting src_offset bytes
+ * into src (yule-core/src/dequant.rs:1232-1275), bit-exact, f32 out.
+ * Replaces the CPU embedding dequant + upload of
+ * yule-infer/src/gpu_runner.rs:309-343. */
+int yule_hip_dequantize(yule_hip_backend *be, yule_buffer src, size_t src_offset, yule_buffer dst,
+                        uint32_t n_blocks, uint32_t dtype);
+
+/* The fused SwiGLU the GPU backends run under the names silu/element_mul
+ * (yule-gpu/src/vulkan/mod.rs:397-428, cuda/mod.rs:173-208) and the CPU
+ * runner inlines (yule-infer/src/model_runner.rs:967-972):
+ * out[i] = gate[i] * sigmoid(gate[i]) * up[i]. */
+int yule_hip_silu_mul(yule_hip_backend *be, yule_buffer gate, yule_buffer up, yule_buffer out,
+                      uint32_t size);
+
+/* Fused GQA decode attention for one token over an f32 KV cache, replacing
+ * the per-head attn_score + softmax + attn_value sequence
+ * (yule-infer/src/model_runner.rs:679-758, shaders/multihead_attn.comp):
+ * for each query head h (kv head h / (n_heads/n_kv_heads)):
+ *   s_t = q_h . K_t / sqrt(hd); p = softmax(s); out_h = sum_t p_t V_t
+ * k_cache/v_cache: [seq][n_kv_heads*head_dim] f32 rows, t < seq_len. */
+int yule_hip_gqa_decode_attn(yule_hip_backend *be, yule_buffer q, yule_buffer k_cache,
+                             yule_buffer v_cache, yule_buffer out, uint32_t n_heads,
+                             uint32_t n_kv_heads, uint32_t head_dim, uint32_t seq_len);
+
+/* Greedy argmax over f32[n] written as one u32 into out (argmax_ct,
+ * yule-infer/src/sampler.rs:150-163: the last maximal index wins). */
+int yule_hip_argmax(yule_hip_backend *be, yule_buffer in, uint32_t n, yule_buffer out);
+
+/* Prefill dequant-GEMM (no counterpart in the reference, whose prefill runs
+ * token by token, yule-infer/src/model_runner.rs:1075-1081):
+ * Y[m][r] = sum_c X[m][c] * W[r][c] for m < M, with X bf16 [M][n_cols]
+ * (row-major), W raw GGUF blocks as in quantized_matmul, Y f32 [M][n_rows].
+ * Runs on the MFMA units; Q4_K and Q6_K, M any positive size. */
+int yule_hip_quantized_gemm(yule_hip_backend *be, yule_buffer weights, yule_buffer x_bf16,
+                            yule_buffer y, uint32_t m, uint32_t n_rows, uint32_t n_cols,
+                            uint32_t dtype);
+
+/* ---- timing helpers for harnesses (no trait counterpart) ---- */
+
+/* One quantized_matmul call, for the timing helper below. */
+typedef struct {
+    yule_buffer weights, input, output;
+    uint32_t n_rows, n_cols, dtype;
+} yule_qmv_op;
+
+/* Run the list `ops` `iters` times on the backend stream and report the
+ * elapsed milliseconds between two HIP events recorded on that stream
+ * around all iterations.  With use_graph != 0 the list is captured once
+ * into a HIP graph and replayed, so host launch latency does not enter the
+ * measurement.  Callers cycle distinct weight copies through `ops` so that
+ * no launch re-reads a matrix left in the 256 MB last-level cache. */
+int yule_hip_time_qmv_ops(yule_hip_backend *be, const yule_qmv_op *ops, uint32_t n_ops, uint32_t iters,
+                          int use_graph, float *ms_total);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

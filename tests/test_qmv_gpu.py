@@ -1,0 +1,174 @@
+"""GPU parity of the hot path through the C ABI: block dequant (bit-exact)
+and quantized_matmul (max|y - y_ref| <= 1e-3 * ||y_ref||_2 / sqrt(N), y_ref
+the f64-accumulated dot of the oracle's bit-exact dequantized weights; the
+reference's own f32 CpuBackend result is checked against the same bar)."""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+from refgen import kats, tolerance_bar, xorshift_blocks
+from yule_amd import DType, synth
+from yule_amd.backend import YuleGpuError
+
+pytestmark = pytest.mark.gpu
+
+FMTS = [DType.Q4_0, DType.Q8_0, DType.Q4_K, DType.Q6_K]
+XS_NAME = {DType.Q4_0: "q4_0", DType.Q8_0: "q8_0", DType.Q4_K: "q4_k", DType.Q6_K: "q6_k"}
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def same_bits(a: np.ndarray, b: np.ndarray) -> bool:
+    a = np.asarray(a, np.float32)
+    b = np.asarray(b, np.float32)
+    nan = np.isnan(a) & np.isnan(b)
+    return bool(np.array_equal(a.view(np.uint32)[~nan], b.view(np.uint32)[~nan]) and
+                np.array_equal(np.isnan(a), np.isnan(b)))
+
+
+def gpu_dequant(hip, dt, data: np.ndarray, offset: int = 0) -> np.ndarray:
+    bs, bb = oracle.GEOM[int(dt)]
+    nb = (data.size - offset) // bb
+    src = hip.upload(data)
+    dst = hip.allocate(nb * bs * 4)
+    hip.dequantize(src, offset, dst, nb, dt)
+    out = hip.download(dst, nb * bs)
+    hip.free(src); hip.free(dst)
+    return out
+
+
+def gpu_qmv(hip, dt, w, x, n_rows, n_cols) -> np.ndarray:
+    hw, hx, hy = hip.upload(w), hip.upload(x), hip.allocate(n_rows * 4)
+    hip.quantized_matmul(hw, hx, hy, n_rows, n_cols, dt)
+    y = hip.download(hy, n_rows)
+    for h in (hw, hx, hy):
+        hip.free(h)
+    return y
+
+
+# ------------------------------------------------------------------ dequant
+@pytest.mark.parametrize("dt", FMTS, ids=lambda d: d.name)
+def test_dequant_bit_exact_reference_generators(hip, dt):
+    say(f"[dequant] {dt.name} reference xorshift blocks")
+    blocks = np.concatenate([b for b, _ in xorshift_blocks(XS_NAME[dt], 512)])
+    assert same_bits(gpu_dequant(hip, dt, blocks), oracle.dequant(int(dt), blocks))
+
+
+@pytest.mark.parametrize("dt", FMTS, ids=lambda d: d.name)
+def test_dequant_bit_exact_random_bytes(hip, dt):
+    """Uniformly random block bytes (every scale/min/quant pattern, any f16
+    header incl. denormals, inf and NaN), at an odd block offset."""
+    say(f"[dequant] {dt.name} random bytes")
+    bs, bb = oracle.GEOM[int(dt)]
+    rng = np.random.default_rng(int(dt))
+    data = rng.integers(0, 256, bb * 4096 + bb, dtype=np.uint8)
+    assert same_bits(gpu_dequant(hip, dt, data, offset=bb), oracle.dequant(int(dt), data[bb:]))
+
+
+def test_dequant_reference_kats(hip):
+    say("[dequant] reference KATs")
+    k = kats()
+    out = gpu_dequant(hip, DType.Q4_0, np.frombuffer(bytes.fromhex(k["q4_0_interleave"]["block_hex"]), np.uint8))
+    assert out[0] == -8.0 and out[1] == 7.0
+    out = gpu_dequant(hip, DType.Q8_0, np.frombuffer(bytes.fromhex(k["q8_0_extremes"]["block_hex"]), np.uint8))
+    assert out[0] == 127.0 and out[1] == -128.0
+
+
+# ------------------------------------------------------------------ matvec
+def test_qmv_reference_kat(hip):
+    say("[qmv] cpu.rs 2-row Q4_0 KAT")
+    k = kats()["q4_0_qmm_two_rows"]
+    w = np.frombuffer(bytes.fromhex(k["weights_hex"] + k["weights_hex_row1"]), np.uint8)
+    y = gpu_qmv(hip, DType.Q4_0, w, np.ones(32, np.float32), 2, 32)
+    assert np.all(np.abs(y - 32.0) < k["tol"])
+
+
+@pytest.mark.parametrize("dt", FMTS, ids=lambda d: d.name)
+def test_qmv_reference_generator_rows(hip, dt):
+    """Rows built from the reference's xorshift blocks and activations."""
+    say(f"[qmv] {dt.name} xorshift rows")
+    bs, bb = oracle.GEOM[int(dt)]
+    pairs = list(xorshift_blocks(XS_NAME[dt], 256))
+    per_row = 8
+    n_rows = len(pairs) // per_row
+    w = np.concatenate([b for b, _ in pairs])
+    x = np.concatenate([a for _, a in pairs[:per_row]])
+    n_cols = per_row * bs
+    ref = oracle.qmv_f64(int(dt), w, x, n_rows, n_cols)
+    y = gpu_qmv(hip, dt, w, x, n_rows, n_cols)
+    assert np.max(np.abs(y - ref)) <= tolerance_bar(ref)
+
+
+SHAPES = [(1, 256), (3, 512), (7, 1024), (33, 2048), (255, 2048), (257, 4096), (300, 5632), (64, 14336),
+          (1000, 768), (4099, 256)]
+
+
+@pytest.mark.parametrize("dt", FMTS, ids=lambda d: d.name)
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: f"{s[0]}x{s[1]}")
+def test_qmv_shapes(hip, dt, shape):
+    n_rows, n_cols = shape
+    say(f"[qmv] {dt.name} {n_rows}x{n_cols}")
+    w = synth.gen_quant(dt, 100 + n_rows, n_rows, n_cols)
+    x = synth.gauss(200 + n_cols, n_cols)
+    ref = oracle.qmv_f64(int(dt), w, x, n_rows, n_cols)
+    y = gpu_qmv(hip, dt, w, x, n_rows, n_cols)
+    bar = tolerance_bar(ref)
+    assert np.max(np.abs(y - ref)) <= bar
+    # the reference's own f32 path meets the same bar (sanity of the bar)
+    assert np.max(np.abs(oracle.qmv_scalar(int(dt), w, x, n_rows, n_cols) - ref)) <= bar
+
+
+def test_qmv_config0_full_size(hip):
+    """Q4_0 5632x2048, W ~ N(0,0.02) seed 0, x ~ N(0,1)."""
+    say("[qmv] config0 Q4_0 5632x2048")
+    w = synth.gen_quant(DType.Q4_0, 0, 5632, 2048)
+    x = synth.gauss(1, 2048)
+    ref = oracle.qmv_f64(int(DType.Q4_0), w, x, 5632, 2048)
+    y = gpu_qmv(hip, DType.Q4_0, w, x, 5632, 2048)
+    assert np.max(np.abs(y - ref)) <= tolerance_bar(ref)
+
+
+def test_qmv_rows_independent_and_linear(hip):
+    """Size-independent properties at a large shape: y(a x1 + b x2) = a y(x1) + b y(x2)
+    and each output row depends only on its own weight row."""
+    say("[qmv] linearity Q4_K 14336x4096")
+    dt, n_rows, n_cols = DType.Q4_K, 14336, 4096
+    w = synth.gen_quant(dt, 5, n_rows, n_cols)
+    x1, x2 = synth.gauss(6, n_cols), synth.gauss(7, n_cols)
+    y1, y2 = gpu_qmv(hip, dt, w, x1, n_rows, n_cols), gpu_qmv(hip, dt, w, x2, n_rows, n_cols)
+    y12 = gpu_qmv(hip, dt, w, (0.5 * x1 + 2.0 * x2).astype(np.float32), n_rows, n_cols)
+    assert np.max(np.abs(y12 - (0.5 * y1 + 2.0 * y2))) <= 2 * tolerance_bar(y12)
+    rows = [0, 1, 4095, 7777, 14335]
+    sub = np.concatenate([w[r * 16 * 144:(r + 1) * 16 * 144] for r in rows])
+    assert np.array_equal(gpu_qmv(hip, dt, sub, x1, len(rows), n_cols), y1[rows])
+
+
+def test_qmv_edge_cases_and_errors(hip):
+    say("[qmv] edge cases")
+    dt = DType.Q4_K
+    w = synth.gen_quant(dt, 9, 4, 256)
+    x = synth.gauss(9, 256)
+    hw, hx, hy = hip.upload(w), hip.upload(x), hip.allocate(16)
+    # zero columns -> zero outputs; zero rows -> no-op
+    hip.copy_to_device(np.full(4, 7.0, np.float32), hy)
+    hip.quantized_matmul(hw, hx, hy, 4, 0, dt)
+    assert np.all(hip.download(hy, 4) == 0.0)
+    hip.quantized_matmul(hw, hx, hy, 0, 256, dt)
+    with pytest.raises(YuleGpuError) as e:
+        hip.quantized_matmul(hw, hx, hy, 4, 256, 3)   # Q4_1: not on the GPU path
+    assert e.value.code == 2
+    with pytest.raises(YuleGpuError):
+        hip.quantized_matmul(hw, hx, hy, 4, 100, dt)  # not a block multiple
+    with pytest.raises(YuleGpuError):
+        hip.quantized_matmul(hw, hx, hy, 5, 256, dt)  # weights too small
+    with pytest.raises(YuleGpuError):
+        hip.quantized_matmul(hw, hx, hx, 1, 256, dt)  # input aliases output
+    with pytest.raises(YuleGpuError):
+        hip.quantized_matmul(hw, hx, 999999, 4, 256, dt)  # unknown handle
+    for h in (hw, hx, hy):
+        hip.free(h)

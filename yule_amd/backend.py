@@ -1,0 +1,259 @@
+"""HipBackend — Python mirror of Yule's ComputeBackend trait over libyule_hip.so.
+
+Method names, argument order and meaning follow `yule-gpu/src/lib.rs:21-132`
+(the trait) so that tests read like Yule's own backend tests
+(`yule-gpu/src/cpu.rs:597-1157`).  Failures raise `YuleGpuError`, the
+counterpart of `YuleError::Gpu(String)` (yule-core/src/error.rs:44).
+
+There is no fallback: if libyule_hip.so is missing or no gfx950 device is
+present, construction raises.  Buffers are `BufferHandle` (a u64 wrapper,
+lib.rs:135).
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+from pathlib import Path
+
+import numpy as np
+
+from .formats import DType
+
+LIB_PATH = Path(__file__).resolve().parent / "libyule_hip.so"
+
+# every symbol declared in include/yule_hip.h (checked by tests/test_abi.py)
+_SIGS: dict[str, tuple] = {
+    "yule_hip_last_error": (C.c_char_p, []),
+    "yule_hip_is_available": (C.c_int, []),
+    "yule_hip_create": (C.c_int, [C.c_int, C.POINTER(C.c_void_p)]),
+    "yule_hip_destroy": (C.c_int, [C.c_void_p]),
+    "yule_hip_name": (C.c_char_p, [C.c_void_p]),
+    "yule_hip_device_info": (C.c_int, [C.c_void_p, C.c_void_p]),
+    "yule_hip_allocate": (C.c_int, [C.c_void_p, C.c_size_t, C.POINTER(C.c_uint64)]),
+    "yule_hip_free": (C.c_int, [C.c_void_p, C.c_uint64]),
+    "yule_hip_copy_to_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_uint64]),
+    "yule_hip_copy_from_device": (C.c_int, [C.c_void_p, C.c_uint64, C.c_void_p, C.c_size_t]),
+    "yule_hip_copy_buffer": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_size_t]),
+    "yule_hip_copy_buffer_offset": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_size_t, C.c_size_t, C.c_size_t]),
+    "yule_hip_synchronize": (C.c_int, [C.c_void_p]),
+    "yule_hip_matmul": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint32]),
+    "yule_hip_softmax": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint32]),
+    "yule_hip_rms_norm": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint32, C.c_float]),
+    "yule_hip_rope": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint32, C.c_uint32, C.c_float, C.c_uint32, C.c_uint32]),
+    "yule_hip_silu": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint32]),
+    "yule_hip_element_mul": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint32]),
+    "yule_hip_add": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint32]),
+    "yule_hip_attn_score": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint64] + [C.c_uint32] * 5),
+    "yule_hip_attn_value": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint64] + [C.c_uint32] * 5),
+    "yule_hip_quantized_matmul": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint32]),
+    "yule_hip_dequantize": (C.c_int, [C.c_void_p, C.c_uint64, C.c_size_t, C.c_uint64, C.c_uint32, C.c_uint32]),
+    "yule_hip_silu_mul": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint32]),
+    "yule_hip_gqa_decode_attn": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint64] + [C.c_uint32] * 4),
+    "yule_hip_argmax": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint32, C.c_uint64]),
+    "yule_hip_quantized_gemm": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint64] + [C.c_uint32] * 4),
+    "yule_hip_time_qmv_ops": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_int,
+                                        C.POINTER(C.c_float)]),
+}
+
+
+class YuleGpuError(RuntimeError):
+    """YuleError::Gpu(String): a failed backend call (code + message)."""
+
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[{code}] {msg}")
+        self.code = code
+
+
+class QmvOp(C.Structure):
+    """yule_qmv_op: one quantized_matmul call for time_qmv_ops."""
+    _fields_ = [("weights", C.c_uint64), ("input", C.c_uint64), ("output", C.c_uint64), ("n_rows", C.c_uint32),
+                ("n_cols", C.c_uint32), ("dtype", C.c_uint32)]
+
+
+class _DeviceInfo(C.Structure):
+    _fields_ = [("name", C.c_char * 256), ("backend", C.c_uint32), ("memory_bytes", C.c_uint64),
+                ("compute_units", C.c_uint32)]
+
+
+@dataclass(frozen=True)
+class BufferHandle:
+    """BufferHandle(pub u64), yule-gpu/src/lib.rs:135."""
+    id: int
+
+
+@dataclass
+class DeviceInfo:
+    """DeviceInfo, yule-gpu/src/lib.rs:137-143."""
+    name: str
+    backend: str
+    memory_bytes: int
+    compute_units: int
+
+
+_lib: C.CDLL | None = None
+
+
+def load_library(path: Path | str = LIB_PATH) -> C.CDLL:
+    """Load libyule_hip.so and declare every exported signature; raises if absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    p = Path(path)
+    if not p.exists():
+        raise FileNotFoundError(f"{p} is not built: run `python -m yule_amd.build` (no CPU fallback exists)")
+    lib = C.CDLL(str(p))
+    for name, (res, args) in _SIGS.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def is_available() -> bool:
+    return bool(load_library().yule_hip_is_available())
+
+
+def _h(x: BufferHandle | int) -> int:
+    return x.id if isinstance(x, BufferHandle) else int(x)
+
+
+class HipBackend:
+    """impl ComputeBackend for HipBackend — one object per device."""
+
+    def __init__(self, device: int = 0):
+        self._lib = load_library()
+        be = C.c_void_p()
+        self._check(self._lib.yule_hip_create(device, C.byref(be)))
+        self._be = be
+
+    # -- plumbing ------------------------------------------------------------
+    def _check(self, rc: int) -> None:
+        if rc != 0:
+            raise YuleGpuError(rc, self._lib.yule_hip_last_error().decode(errors="replace"))
+
+    def close(self) -> None:
+        if getattr(self, "_be", None):
+            self._lib.yule_hip_destroy(self._be)
+            self._be = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def raw(self) -> C.c_void_p:
+        return self._be
+
+    # -- trait methods -------------------------------------------------------
+    def name(self) -> str:
+        return self._lib.yule_hip_name(self._be).decode()
+
+    def device_info(self) -> DeviceInfo:
+        info = _DeviceInfo()
+        self._check(self._lib.yule_hip_device_info(self._be, C.byref(info)))
+        return DeviceInfo(info.name.decode(errors="replace"), "hip", info.memory_bytes, info.compute_units)
+
+    def allocate(self, size_bytes: int) -> BufferHandle:
+        h = C.c_uint64()
+        self._check(self._lib.yule_hip_allocate(self._be, size_bytes, C.byref(h)))
+        return BufferHandle(h.value)
+
+    def free(self, handle: BufferHandle) -> None:
+        self._check(self._lib.yule_hip_free(self._be, _h(handle)))
+
+    def copy_to_device(self, data, handle: BufferHandle) -> None:
+        a = np.ascontiguousarray(data)
+        self._check(self._lib.yule_hip_copy_to_device(self._be, a.ctypes.data, a.nbytes, _h(handle)))
+
+    def copy_from_device(self, handle: BufferHandle, out: np.ndarray) -> np.ndarray:
+        if not out.flags["C_CONTIGUOUS"]:
+            raise ValueError("copy_from_device needs a C-contiguous array")
+        self._check(self._lib.yule_hip_copy_from_device(self._be, _h(handle), out.ctypes.data, out.nbytes))
+        return out
+
+    def copy_buffer(self, src: BufferHandle, dst: BufferHandle, size: int) -> None:
+        self._check(self._lib.yule_hip_copy_buffer(self._be, _h(src), _h(dst), size))
+
+    def copy_buffer_offset(self, src, dst, src_offset: int, dst_offset: int, size: int) -> None:
+        self._check(self._lib.yule_hip_copy_buffer_offset(self._be, _h(src), _h(dst), src_offset, dst_offset, size))
+
+    def synchronize(self) -> None:
+        self._check(self._lib.yule_hip_synchronize(self._be))
+
+    def matmul(self, a, b, out, m: int, n: int, k: int) -> None:
+        self._check(self._lib.yule_hip_matmul(self._be, _h(a), _h(b), _h(out), m, n, k))
+
+    def softmax(self, inp, out, size: int) -> None:
+        self._check(self._lib.yule_hip_softmax(self._be, _h(inp), _h(out), size))
+
+    def rms_norm(self, inp, weight, out, size: int, eps: float) -> None:
+        self._check(self._lib.yule_hip_rms_norm(self._be, _h(inp), _h(weight), _h(out), size, eps))
+
+    def rope(self, q, k, pos: int, head_dim: int, freq_base: float, n_heads_q: int, n_heads_k: int) -> None:
+        self._check(self._lib.yule_hip_rope(self._be, _h(q), _h(k), pos, head_dim, freq_base, n_heads_q, n_heads_k))
+
+    def silu(self, inp, out, size: int) -> None:
+        self._check(self._lib.yule_hip_silu(self._be, _h(inp), _h(out), size))
+
+    def element_mul(self, a, b, out, size: int) -> None:
+        self._check(self._lib.yule_hip_element_mul(self._be, _h(a), _h(b), _h(out), size))
+
+    def add(self, a, b, out, size: int) -> None:
+        self._check(self._lib.yule_hip_add(self._be, _h(a), _h(b), _h(out), size))
+
+    def attn_score(self, q, k_cache, scores, head_dim, seq_len, head_offset, kv_offset, kv_stride) -> None:
+        self._check(self._lib.yule_hip_attn_score(self._be, _h(q), _h(k_cache), _h(scores), head_dim, seq_len,
+                                                  head_offset, kv_offset, kv_stride))
+
+    def attn_value(self, weights, v_cache, out, head_dim, seq_len, kv_offset, kv_stride, out_offset) -> None:
+        self._check(self._lib.yule_hip_attn_value(self._be, _h(weights), _h(v_cache), _h(out), head_dim, seq_len,
+                                                  kv_offset, kv_stride, out_offset))
+
+    def quantized_matmul(self, weights, inp, out, n_rows: int, n_cols: int, dtype: DType | int) -> None:
+        self._check(self._lib.yule_hip_quantized_matmul(self._be, _h(weights), _h(inp), _h(out), n_rows, n_cols,
+                                                        int(dtype)))
+
+    # -- extensions ----------------------------------------------------------
+    def dequantize(self, src, src_offset: int, dst, n_blocks: int, dtype: DType | int) -> None:
+        self._check(self._lib.yule_hip_dequantize(self._be, _h(src), src_offset, _h(dst), n_blocks, int(dtype)))
+
+    def silu_mul(self, gate, up, out, size: int) -> None:
+        self._check(self._lib.yule_hip_silu_mul(self._be, _h(gate), _h(up), _h(out), size))
+
+    def gqa_decode_attn(self, q, k_cache, v_cache, out, n_heads, n_kv_heads, head_dim, seq_len) -> None:
+        self._check(self._lib.yule_hip_gqa_decode_attn(self._be, _h(q), _h(k_cache), _h(v_cache), _h(out), n_heads,
+                                                       n_kv_heads, head_dim, seq_len))
+
+    def argmax(self, inp, n: int, out) -> None:
+        self._check(self._lib.yule_hip_argmax(self._be, _h(inp), n, _h(out)))
+
+    def quantized_gemm(self, weights, x_bf16, y, m: int, n_rows: int, n_cols: int, dtype: DType | int) -> None:
+        self._check(self._lib.yule_hip_quantized_gemm(self._be, _h(weights), _h(x_bf16), _h(y), m, n_rows, n_cols,
+                                                      int(dtype)))
+
+    def time_qmv_ops(self, ops, iters: int, use_graph: bool = True) -> float:
+        """Milliseconds (HIP events on the backend stream) for `iters` passes over
+        `ops`, a list of (weights, input, output, n_rows, n_cols, dtype)."""
+        arr = (QmvOp * len(ops))(*[QmvOp(_h(w), _h(x), _h(y), r, c, int(d)) for (w, x, y, r, c, d) in ops])
+        ms = C.c_float()
+        self._check(self._lib.yule_hip_time_qmv_ops(self._be, arr, len(ops), iters, int(use_graph), C.byref(ms)))
+        return ms.value
+
+    # -- conveniences ----------------------------------------------------------
+    def upload(self, data) -> BufferHandle:
+        a = np.ascontiguousarray(data)
+        h = self.allocate(a.nbytes)
+        self.copy_to_device(a, h)
+        return h
+
+    def download(self, handle, shape, dtype=np.float32) -> np.ndarray:
+        return self.copy_from_device(handle, np.empty(shape, dtype=dtype))

@@ -1,0 +1,67 @@
+// internal.h — shared host-side state of libyule_hip.so (not part of the ABI).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+
+#include "../../include/yule_hip.h"
+
+namespace yule {
+
+// Every allocation carries this many bytes of slack past its requested size:
+// the matvec kernels read 2-byte-aligned GGUF blocks (Q4_0 18 B, Q8_0 34 B,
+// Q6_K 210 B) through 4-byte-aligned dword loads, so the last block of a
+// buffer may be fetched up to 4 bytes past its end.
+constexpr size_t kAllocSlack = 64;
+
+struct Buffer {
+    void *ptr = nullptr;
+    size_t size = 0;  // bytes requested by the caller (validation bound)
+};
+
+}  // namespace yule
+
+struct yule_hip_backend {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    hipDeviceProp_t props{};
+    std::mutex mu;  // guards `buffers`; ComputeBackend is Send + Sync
+    std::unordered_map<uint64_t, yule::Buffer> buffers;
+};
+
+namespace yule {
+
+// thread-local last error, returned by yule_hip_last_error()
+int set_error(int code, const std::string &msg);
+int hip_error(hipError_t e, const char *what);
+
+// Look up a handle and check that [offset, offset+need) lies inside it.
+int get_buffer(yule_hip_backend *be, uint64_t h, size_t need, void **ptr, const char *what,
+               size_t offset = 0);
+
+// Launch failures surface through hipGetLastError after a kernel launch.
+int check_launch(const char *what);
+
+// Block geometry of the supported GGUF formats (dtype.rs:62-118); false if
+// unsupported by the quantized kernels.
+bool quant_geometry(uint32_t dtype, uint32_t *block_size, uint32_t *block_bytes);
+
+// Kernel launchers (device code in qmv.hip / ops.hip / attn.hip / gemm.hip).
+// Arguments are already validated; all enqueue on `stream`.
+int launch_qmv(hipStream_t stream, uint32_t dtype, const uint8_t *w, const float *x, float *y,
+               uint32_t n_rows, uint32_t n_cols);
+int launch_dequant(hipStream_t stream, uint32_t dtype, const uint8_t *src, float *dst,
+                   uint32_t n_blocks);
+// dequantize row token[0] (clamped to n_rows-1) of a [n_rows][dim] quantized
+// table; the token is read on the device so the launch can sit in a graph
+int launch_embed_rows(hipStream_t stream, uint32_t dtype, const uint8_t *table, const uint32_t *token,
+                      uint32_t n_rows, float *dst, uint32_t dim);
+// out[i] = value for i < n
+int launch_fill(hipStream_t stream, float *out, float value, uint64_t n);
+
+}  // namespace yule

@@ -1,0 +1,431 @@
+// ops.hip — the remaining ComputeBackend methods (yule-gpu/src/lib.rs:26-114)
+// as gfx950 kernels, plus the fused GQA decode attention and the greedy
+// argmax the HIP runner uses.  Semantics follow CpuBackend
+// (yule-gpu/src/cpu.rs:163-539); f32 results agree to rounding, since
+// reductions run as trees instead of the reference's sequential loops.
+#include <string>
+
+#include "internal.h"
+
+namespace yule {
+
+// ------------------------------------------------------------ reductions
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+// block-wide reductions for blockDim.x a multiple of 64 and <= 1024
+__device__ float block_sum(float v, float *red) {
+    v = wave_sum(v);
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[w] = v;
+    __syncthreads();
+    float t = 0.f;
+    for (int i = 0; i < nw; i++) t += red[i];
+    return t;
+}
+__device__ float block_max(float v, float *red) {
+    v = wave_max(v);
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[w] = v;
+    __syncthreads();
+    float t = -INFINITY;
+    for (int i = 0; i < nw; i++) t = fmaxf(t, red[i]);
+    return t;
+}
+
+// ------------------------------------------------------------ elementwise
+__global__ void fill_kernel(float *out, float v, uint64_t n) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = v;
+}
+
+int launch_fill(hipStream_t s, float *out, float v, uint64_t n) {
+    if (!n) return YULE_OK;
+    hipLaunchKernelGGL(fill_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, out, v, n);
+    return check_launch("fill");
+}
+
+// op 0: silu (cpu.rs:339-357), 1: element_mul, 2: add, 3: silu_mul
+// (model_runner.rs:967-972: g * (1/(1+exp(-g))) * u)
+__global__ void eltwise_kernel(int op, const float *__restrict__ a, const float *__restrict__ b,
+                               float *__restrict__ out, uint32_t n) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float x = a[i];
+    switch (op) {
+    case 0: out[i] = x * (1.0f / (1.0f + expf(-x))); break;
+    case 1: out[i] = x * b[i]; break;
+    case 2: out[i] = x + b[i]; break;
+    default: out[i] = x * (1.0f / (1.0f + expf(-x))) * b[i]; break;
+    }
+}
+
+int launch_eltwise(hipStream_t s, int op, const float *a, const float *b, float *out, uint32_t n) {
+    if (!n) return YULE_OK;
+    hipLaunchKernelGGL(eltwise_kernel, dim3((n + 255) / 256), dim3(256), 0, s, op, a, b, out, n);
+    return check_launch("elementwise");
+}
+
+// ------------------------------------------------------------ rms_norm
+// cpu.rs:263-295 / model_runner.rs:246-275: out = x * (1/sqrt(mean(x^2)+eps)) * w
+__global__ __launch_bounds__(1024) void rms_norm_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                                        float *__restrict__ out, uint32_t n, float eps) {
+    __shared__ float red[16];
+    float ss = 0.f;
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) ss += x[i] * x[i];
+    ss = block_sum(ss, red);
+    const float inv = 1.0f / sqrtf(ss / (float)n + eps);
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) out[i] = x[i] * inv * w[i];
+}
+
+int launch_rms_norm(hipStream_t s, const float *x, const float *w, float *out, uint32_t n, float eps) {
+    hipLaunchKernelGGL(rms_norm_kernel, dim3(1), dim3(1024), 0, s, x, w, out, n, eps);
+    return check_launch("rms_norm");
+}
+
+// ------------------------------------------------------------ softmax
+// cpu.rs:226-258, single workgroup
+__global__ __launch_bounds__(1024) void softmax_kernel(const float *__restrict__ in, float *__restrict__ out,
+                                                       uint32_t n) {
+    __shared__ float red[16];
+    float m = -INFINITY;
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) m = fmaxf(m, in[i]);
+    m = block_max(m, red);
+    float sum = 0.f;
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+        const float e = expf(in[i] - m);
+        out[i] = e;
+        sum += e;
+    }
+    sum = block_sum(sum, red);
+    const float inv = 1.0f / sum;
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) out[i] *= inv;
+}
+
+// ------------------------------------------------------------ rope
+// cpu.rs:300-335: interleaved pairs, freq = 1/base^(2i/hd), theta = pos*freq
+__global__ void rope_kernel(float *__restrict__ q, float *__restrict__ k, uint32_t pos, uint32_t hd, float base,
+                            uint32_t nq, uint32_t nk) {
+    const uint32_t half = hd / 2;
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t total = (nq + nk) * half;
+    if (i >= total) return;
+    const uint32_t head = i / half, p = i % half;
+    float *v = head < nq ? q + head * hd : k + (head - nq) * hd;
+    const float freq = 1.0f / powf(base, 2.0f * (float)p / (float)hd);
+    const float theta = (float)pos * freq;
+    const float c = cosf(theta), sn = sinf(theta);
+    const float x0 = v[2 * p], x1 = v[2 * p + 1];
+    v[2 * p] = x0 * c - x1 * sn;
+    v[2 * p + 1] = x0 * sn + x1 * c;
+}
+
+// ------------------------------------------------------------ matmul (f32)
+// cpu.rs:163-222: C[m,n] = A[m,k] * B[k,n]; one thread per output, f32 FMA
+// over k.  Not on the quantized hot path (kept for trait completeness).
+__global__ void matmul_kernel(const float *__restrict__ a, const float *__restrict__ b, float *__restrict__ c,
+                              uint32_t m, uint32_t n, uint32_t k) {
+    const uint32_t j = blockIdx.x * blockDim.x + threadIdx.x, i = blockIdx.y;
+    if (j >= n || i >= m) return;
+    float acc = 0.f;
+    for (uint32_t p = 0; p < k; p++) acc += a[(size_t)i * k + p] * b[(size_t)p * n + j];
+    c[(size_t)i * n + j] = acc;
+}
+
+// ------------------------------------------------------------ attention (trait)
+// cpu.rs:462-500: one wave per position, lanes over the head dimension
+__global__ void attn_score_kernel(const float *__restrict__ q, const float *__restrict__ kc, float *__restrict__ sc,
+                                  uint32_t hd, uint32_t seq, uint32_t ho, uint32_t kvo, uint32_t kvs) {
+    const uint32_t t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (t >= seq) return;
+    float acc = 0.f;
+    for (uint32_t d = lane; d < hd; d += 64) acc += q[ho + d] * kc[(size_t)t * kvs + kvo + d];
+    acc = wave_sum(acc);
+    if (lane == 0) sc[t] = acc * (1.0f / sqrtf((float)hd));
+}
+
+// cpu.rs:502-539: thread per output dimension, sequential over positions
+__global__ void attn_value_kernel(const float *__restrict__ w, const float *__restrict__ vc, float *__restrict__ out,
+                                  uint32_t hd, uint32_t seq, uint32_t kvo, uint32_t kvs, uint32_t oo) {
+    const uint32_t d = blockIdx.x * blockDim.x + threadIdx.x;
+    if (d >= hd) return;
+    float acc = 0.f;
+    for (uint32_t t = 0; t < seq; t++) acc += w[t] * vc[(size_t)t * kvs + kvo + d];
+    out[oo + d] = acc;
+}
+
+// ------------------------------------------------------------ GQA decode attention
+// One workgroup (4 waves) per query head; model_runner.rs:679-758 semantics.
+// Scores live in LDS (seq_len <= kMaxSeqLds); K rows are read with lanes
+// over the head dimension (coalesced), V likewise, and the four waves split
+// the positions and combine through LDS.  K/V of a KV head are shared by its
+// n_heads/n_kv_heads query heads through L2.
+constexpr uint32_t kMaxSeqLds = 16384;
+constexpr uint32_t kMaxHeadDim = 256;
+
+__global__ __launch_bounds__(256) void gqa_attn_kernel(const float *__restrict__ q, const float *__restrict__ kc,
+                                                       const float *__restrict__ vc, float *__restrict__ out,
+                                                       uint32_t group, uint32_t n_kv, uint32_t hd,
+                                                       const uint32_t *__restrict__ seq_dev, uint32_t seq_host) {
+    extern __shared__ float smem[];
+    float *scores = smem;                        // [seq]
+    __shared__ float red[16];
+    __shared__ float part[4][kMaxHeadDim];
+    const uint32_t h = blockIdx.x, kvh = h / group, kvs = n_kv * hd;
+    const uint32_t seq = seq_dev ? seq_dev[0] + 1 : seq_host;   // device counter holds the position
+    const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const float scale = 1.0f / sqrtf((float)hd);
+    const float *qh = q + (size_t)h * hd;
+    float qr[kMaxHeadDim / 64];
+#pragma unroll
+    for (uint32_t c = 0; c < kMaxHeadDim / 64; c++) qr[c] = (lane + 64 * c < hd) ? qh[lane + 64 * c] : 0.f;
+
+    for (uint32_t t = w; t < seq; t += 4) {
+        const float *kr = kc + (size_t)t * kvs + kvh * hd;
+        float acc = 0.f;
+#pragma unroll
+        for (uint32_t c = 0; c < kMaxHeadDim / 64; c++)
+            if (lane + 64 * c < hd) acc += qr[c] * kr[lane + 64 * c];
+        acc = wave_sum(acc);
+        if (lane == 0) scores[t] = acc * scale;
+    }
+    __syncthreads();
+    float m = -INFINITY;
+    for (uint32_t t = threadIdx.x; t < seq; t += blockDim.x) m = fmaxf(m, scores[t]);
+    m = block_max(m, red);
+    float sum = 0.f;
+    for (uint32_t t = threadIdx.x; t < seq; t += blockDim.x) {
+        const float e = expf(scores[t] - m);
+        scores[t] = e;
+        sum += e;
+    }
+    sum = block_sum(sum, red);   // ends with a barrier-protected read; scores[] complete
+    const float inv = 1.0f / sum;
+    float o[kMaxHeadDim / 64] = {};
+    for (uint32_t t = w; t < seq; t += 4) {
+        const float p = scores[t] * inv;
+        const float *vr = vc + (size_t)t * kvs + kvh * hd;
+#pragma unroll
+        for (uint32_t c = 0; c < kMaxHeadDim / 64; c++)
+            if (lane + 64 * c < hd) o[c] += p * vr[lane + 64 * c];
+    }
+#pragma unroll
+    for (uint32_t c = 0; c < kMaxHeadDim / 64; c++)
+        if (lane + 64 * c < hd) part[w][lane + 64 * c] = o[c];
+    __syncthreads();
+    for (uint32_t d = threadIdx.x; d < hd; d += blockDim.x)
+        out[(size_t)h * hd + d] = part[0][d] + part[1][d] + part[2][d] + part[3][d];
+}
+
+int launch_gqa_attn(hipStream_t s, const float *q, const float *kc, const float *vc, float *out, uint32_t n_heads,
+                    uint32_t n_kv, uint32_t hd, const uint32_t *pos_dev, uint32_t seq_host, uint32_t max_seq) {
+    const size_t lds = (size_t)max_seq * sizeof(float);
+    hipLaunchKernelGGL(gqa_attn_kernel, dim3(n_heads), dim3(256), lds, s, q, kc, vc, out, n_heads / n_kv, n_kv, hd,
+                       pos_dev, seq_host);
+    return check_launch("gqa_decode_attn");
+}
+
+// ------------------------------------------------------------ argmax
+// argmax_ct (sampler.rs:150-163): the last maximal index wins.
+__device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t bi) {
+    return v > bv || (v == bv && i > bi);
+}
+
+__global__ __launch_bounds__(1024) void argmax_kernel(const float *__restrict__ in, uint32_t n,
+                                                      uint32_t *__restrict__ out) {
+    __shared__ float rv[16];
+    __shared__ uint32_t ri[16];
+    float bv = -INFINITY;
+    uint32_t bi = 0;
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x)
+        if (better(in[i], i, bv, bi)) { bv = in[i]; bi = i; }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float ov = __shfl_xor(bv, off, 64);
+        const uint32_t oi = __shfl_xor(bi, off, 64);
+        if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+    }
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    if (lane == 0) { rv[w] = bv; ri[w] = bi; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int k = 1; k < (int)(blockDim.x >> 6); k++)
+            if (better(rv[k], ri[k], bv, bi)) { bv = rv[k]; bi = ri[k]; }
+        out[0] = n ? bi : 0u;
+    }
+}
+
+int launch_argmax(hipStream_t s, const float *in, uint32_t n, uint32_t *out) {
+    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, s, in, n, out);
+    return check_launch("argmax");
+}
+
+}  // namespace yule
+
+using namespace yule;
+
+#define BE_OR_FAIL(be) \
+    if (!(be)) return set_error(YULE_ERR_INVALID, "null backend")
+
+static int f32buf(yule_hip_backend *be, yule_buffer h, size_t n_floats, float **p, const char *what,
+                  size_t off_floats = 0) {
+    void *v;
+    int rc = get_buffer(be, h, n_floats * 4, &v, what, off_floats * 4);
+    *p = (float *)v;
+    return rc;
+}
+
+extern "C" {
+
+int yule_hip_matmul(yule_hip_backend *be, yule_buffer a, yule_buffer b, yule_buffer out, uint32_t m, uint32_t n,
+                    uint32_t k) {
+    BE_OR_FAIL(be);
+    float *pa, *pb, *pc;
+    int rc;
+    if ((rc = f32buf(be, a, (size_t)m * k, &pa, "matmul (a)")) || (rc = f32buf(be, b, (size_t)k * n, &pb, "matmul (b)")) ||
+        (rc = f32buf(be, out, (size_t)m * n, &pc, "matmul (out)")))
+        return rc;
+    if (!m || !n) return YULE_OK;
+    hipLaunchKernelGGL(matmul_kernel, dim3((n + 255) / 256, m), dim3(256), 0, be->stream, pa, pb, pc, m, n, k);
+    return check_launch("matmul");
+}
+
+int yule_hip_softmax(yule_hip_backend *be, yule_buffer in, yule_buffer out, uint32_t size) {
+    BE_OR_FAIL(be);
+    float *pi, *po;
+    int rc;
+    if ((rc = f32buf(be, in, size, &pi, "softmax (in)")) || (rc = f32buf(be, out, size, &po, "softmax (out)")))
+        return rc;
+    if (!size) return YULE_OK;
+    hipLaunchKernelGGL(softmax_kernel, dim3(1), dim3(1024), 0, be->stream, pi, po, size);
+    return check_launch("softmax");
+}
+
+int yule_hip_rms_norm(yule_hip_backend *be, yule_buffer in, yule_buffer weight, yule_buffer out, uint32_t size,
+                      float eps) {
+    BE_OR_FAIL(be);
+    float *pi, *pw, *po;
+    int rc;
+    if ((rc = f32buf(be, in, size, &pi, "rms_norm (in)")) || (rc = f32buf(be, weight, size, &pw, "rms_norm (weight)")) ||
+        (rc = f32buf(be, out, size, &po, "rms_norm (out)")))
+        return rc;
+    if (!size) return YULE_OK;
+    return launch_rms_norm(be->stream, pi, pw, po, size, eps);
+}
+
+int yule_hip_rope(yule_hip_backend *be, yule_buffer q, yule_buffer k, uint32_t pos, uint32_t head_dim, float freq_base,
+                  uint32_t n_heads_q, uint32_t n_heads_k) {
+    BE_OR_FAIL(be);
+    if (head_dim == 0 || head_dim % 2) return set_error(YULE_ERR_INVALID, "rope: head_dim must be even and > 0");
+    if (q == k) return set_error(YULE_ERR_INVALID, "rope: q and k alias");
+    float *pq, *pk;
+    int rc;
+    if ((rc = f32buf(be, q, (size_t)n_heads_q * head_dim, &pq, "rope (q)")) ||
+        (rc = f32buf(be, k, (size_t)n_heads_k * head_dim, &pk, "rope (k)")))
+        return rc;
+    const uint32_t total = (n_heads_q + n_heads_k) * (head_dim / 2);
+    if (!total) return YULE_OK;
+    hipLaunchKernelGGL(rope_kernel, dim3((total + 255) / 256), dim3(256), 0, be->stream, pq, pk, pos, head_dim,
+                       freq_base, n_heads_q, n_heads_k);
+    return check_launch("rope");
+}
+
+static int eltwise_entry(yule_hip_backend *be, int op, yule_buffer a, yule_buffer b, yule_buffer out, uint32_t size,
+                         const char *what) {
+    BE_OR_FAIL(be);
+    float *pa, *pb = nullptr, *po;
+    int rc;
+    if ((rc = f32buf(be, a, size, &pa, what)) || (rc = f32buf(be, out, size, &po, what))) return rc;
+    if (op != 0 && (rc = f32buf(be, b, size, &pb, what))) return rc;
+    return launch_eltwise(be->stream, op, pa, pb, po, size);
+}
+
+int yule_hip_silu(yule_hip_backend *be, yule_buffer in, yule_buffer out, uint32_t size) {
+    return eltwise_entry(be, 0, in, 0, out, size, "silu");
+}
+int yule_hip_element_mul(yule_hip_backend *be, yule_buffer a, yule_buffer b, yule_buffer out, uint32_t size) {
+    return eltwise_entry(be, 1, a, b, out, size, "element_mul");
+}
+int yule_hip_add(yule_hip_backend *be, yule_buffer a, yule_buffer b, yule_buffer out, uint32_t size) {
+    return eltwise_entry(be, 2, a, b, out, size, "add");
+}
+int yule_hip_silu_mul(yule_hip_backend *be, yule_buffer gate, yule_buffer up, yule_buffer out, uint32_t size) {
+    return eltwise_entry(be, 3, gate, up, out, size, "silu_mul");
+}
+
+int yule_hip_attn_score(yule_hip_backend *be, yule_buffer q, yule_buffer k_cache, yule_buffer scores,
+                        uint32_t head_dim, uint32_t seq_len, uint32_t head_offset, uint32_t kv_offset,
+                        uint32_t kv_stride) {
+    BE_OR_FAIL(be);
+    float *pq, *pk, *ps;
+    int rc;
+    if (seq_len && kv_offset + head_dim > kv_stride)
+        return set_error(YULE_ERR_INVALID, "attn_score: kv_offset + head_dim exceeds kv_stride");
+    if ((rc = f32buf(be, q, (size_t)head_offset + head_dim, &pq, "attn_score (q)")) ||
+        (rc = f32buf(be, k_cache, (size_t)seq_len * kv_stride, &pk, "attn_score (k_cache)")) ||
+        (rc = f32buf(be, scores, seq_len, &ps, "attn_score (scores)")))
+        return rc;
+    if (!seq_len) return YULE_OK;
+    hipLaunchKernelGGL(attn_score_kernel, dim3((seq_len + 3) / 4), dim3(256), 0, be->stream, pq, pk, ps, head_dim,
+                       seq_len, head_offset, kv_offset, kv_stride);
+    return check_launch("attn_score");
+}
+
+int yule_hip_attn_value(yule_hip_backend *be, yule_buffer weights, yule_buffer v_cache, yule_buffer out,
+                        uint32_t head_dim, uint32_t seq_len, uint32_t kv_offset, uint32_t kv_stride,
+                        uint32_t out_offset) {
+    BE_OR_FAIL(be);
+    float *pw, *pv, *po;
+    int rc;
+    if (seq_len && kv_offset + head_dim > kv_stride)
+        return set_error(YULE_ERR_INVALID, "attn_value: kv_offset + head_dim exceeds kv_stride");
+    if ((rc = f32buf(be, weights, seq_len, &pw, "attn_value (weights)")) ||
+        (rc = f32buf(be, v_cache, (size_t)seq_len * kv_stride, &pv, "attn_value (v_cache)")) ||
+        (rc = f32buf(be, out, (size_t)out_offset + head_dim, &po, "attn_value (out)")))
+        return rc;
+    if (!head_dim) return YULE_OK;
+    hipLaunchKernelGGL(attn_value_kernel, dim3((head_dim + 255) / 256), dim3(256), 0, be->stream, pw, pv, po,
+                       head_dim, seq_len, kv_offset, kv_stride, out_offset);
+    return check_launch("attn_value");
+}
+
+int yule_hip_gqa_decode_attn(yule_hip_backend *be, yule_buffer q, yule_buffer k_cache, yule_buffer v_cache,
+                             yule_buffer out, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
+                             uint32_t seq_len) {
+    BE_OR_FAIL(be);
+    if (!n_kv_heads || n_heads % n_kv_heads)
+        return set_error(YULE_ERR_INVALID, "gqa_decode_attn: n_heads must be a multiple of n_kv_heads");
+    if (!head_dim || head_dim > kMaxHeadDim)
+        return set_error(YULE_ERR_INVALID, "gqa_decode_attn: head_dim must be in 1..256");
+    if (!seq_len || seq_len > kMaxSeqLds)
+        return set_error(YULE_ERR_INVALID, "gqa_decode_attn: seq_len must be in 1..16384");
+    float *pq, *pk, *pv, *po;
+    int rc;
+    const size_t kv = (size_t)seq_len * n_kv_heads * head_dim;
+    if ((rc = f32buf(be, q, (size_t)n_heads * head_dim, &pq, "gqa_decode_attn (q)")) ||
+        (rc = f32buf(be, k_cache, kv, &pk, "gqa_decode_attn (k_cache)")) ||
+        (rc = f32buf(be, v_cache, kv, &pv, "gqa_decode_attn (v_cache)")) ||
+        (rc = f32buf(be, out, (size_t)n_heads * head_dim, &po, "gqa_decode_attn (out)")))
+        return rc;
+    return launch_gqa_attn(be->stream, pq, pk, pv, po, n_heads, n_kv_heads, head_dim, nullptr, seq_len, seq_len);
+}
+
+int yule_hip_argmax(yule_hip_backend *be, yule_buffer in, uint32_t n, yule_buffer out) {
+    BE_OR_FAIL(be);
+    float *pi;
+    void *po;
+    int rc;
+    if ((rc = f32buf(be, in, n, &pi, "argmax (in)")) || (rc = get_buffer(be, out, 4, &po, "argmax (out)"))) return rc;
+    return launch_argmax(be->stream, pi, n, (uint32_t *)po);
+}
+
+}  // extern "C"

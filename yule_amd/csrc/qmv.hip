@@ -1,0 +1,459 @@
+// qmv.hip — fused dequant+dot quantized matvec (decode, batch 1) for raw GGUF
+// blocks on gfx950, and the bit-exact block dequant kernel.
+//
+// Semantics: yule-gpu ComputeBackend::quantized_matmul (yule-gpu/src/lib.rs:
+// 116-131), i.e. y[r] = sum_b vec_dot(W[r,b], x[b*bs..]) with the block dots
+// of yule-core/src/dequant.rs:902-1009.  Results agree with the reference to
+// f32 rounding (the summation order differs); dequant is bit-exact.
+//
+// Work decomposition (all formats):
+//  * A "unit" is the slice of one block that one lane owns: Q4_K 64 weights
+//    (one 32-byte qs group = sub-blocks 2j and 2j+1), Q6_K 32 weights, Q8_0
+//    and Q4_0 one whole 32-weight block.
+//  * A team of TEAM lanes (16/32/64) owns a row; a wave64 carries 64/TEAM
+//    teams ("slots") on consecutive rows, so one load instruction streams a
+//    contiguous stretch of consecutive rows.
+//  * Each wave owns R row-groups.  At each column step a lane loads its
+//    activation slice once into registers and applies it to all R rows, so
+//    activation traffic is 1/R of a per-row re-read; weight bytes are read
+//    from HBM exactly once, with no dequantized copy anywhere.
+//  * After the column loop the TEAM partial sums are combined with xor
+//    shuffles and one lane per slot stores y.
+//
+// Nibble arithmetic: a 4-bit (or 6/8-bit, biased to unsigned) quant masked
+// into one 16-bit half of a dword is an f16 *denormal* of value q * 2^-24.
+// v_fma_mix_f32 multiplies that half by an f32 activation and accumulates in
+// f32 exactly as an f32 FMA on q would, scaled by 2^-24 (f16 denormals are
+// preserved: the kernels run with FP16 denorm mode on).  Two AND masks per
+// 4 bytes thus replace per-weight unpack + convert; the 2^24 (and the x16 of
+// high nibbles masked in place) fold into the block scale.  Biased formats
+// (Q6_K q+32, Q8_0 q+128, Q4_0 nib-8) subtract bias * sum(x) per unit,
+// where sum(x) is computed once per column step.
+#include "internal.h"
+
+namespace yule {
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float mix_lo(uint32_t v, float x, float acc) {
+    h2_t h = __builtin_bit_cast(h2_t, v);
+    return __builtin_fmaf((float)h.x, x, acc);
+}
+__device__ __forceinline__ float mix_hi(uint32_t v, float x, float acc) {
+    h2_t h = __builtin_bit_cast(h2_t, v);
+    return __builtin_fmaf((float)h.y, x, acc);
+}
+__device__ __forceinline__ float f16_bits(uint32_t b) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(b & 0xFFFFu));
+}
+// dword of bytes [s, s+4) of the little-endian pair {hi:lo}, s in 0..3
+__device__ __forceinline__ uint32_t align_bytes(uint32_t hi, uint32_t lo, uint32_t s) {
+    return __builtin_amdgcn_alignbyte(hi, lo, s);
+}
+// bytes [s/8, s/8+4) of {hi:lo}, s in {16, 32}
+__device__ __forceinline__ uint32_t shr64(uint32_t hi, uint32_t lo, uint32_t s) {
+    return (uint32_t)((((uint64_t)hi << 32) | lo) >> s);
+}
+
+constexpr float kTwo24 = 16777216.0f;
+
+// ---------------------------------------------------------------- Q4_K
+// 144 B: d f16 @0, dmin f16 @2, scales[12] @4, qs[128] @16 (dequant.rs:255-290)
+struct Q4K {
+    static constexpr uint32_t BS = 256, BB = 144, UPB = 4, NX = 64, NAUX = 2;
+    struct Raw { uint4 h, qa, qb; };
+    __device__ static void load_x(const float *__restrict__ x, uint32_t k, uint32_t j, float *xs, float *aux) {
+        const float4 *p = reinterpret_cast<const float4 *>(x + k * 256 + j * 64);
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            float4 v = p[i];
+            xs[4 * i] = v.x; xs[4 * i + 1] = v.y; xs[4 * i + 2] = v.z; xs[4 * i + 3] = v.w;
+        }
+        float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+        for (int i = 0; i < 32; i++) { s0 += xs[i]; s1 += xs[32 + i]; }
+        aux[0] = s0; aux[1] = s1;
+    }
+    __device__ static Raw load(const uint8_t *__restrict__ blk, uint32_t j) {
+        Raw r;
+        r.h = *reinterpret_cast<const uint4 *>(blk);
+        r.qa = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * j);
+        r.qb = *reinterpret_cast<const uint4 *>(blk + 32 + 32 * j);
+        return r;
+    }
+    __device__ static float dot(const Raw &r, uint32_t j, const float *xs, const float *aux) {
+        const float d = f16_bits(r.h.x), dmin = f16_bits(r.h.x >> 16);
+        // 6-bit scales/mins of sub-blocks 2j, 2j+1 (get_scale_min_k4,
+        // dequant.rs:176-190), two bytes at a time
+        const uint32_t sh = (j & 1u) << 4;
+        const bool low = j < 2;
+        const uint32_t A = low ? r.h.y : r.h.w, Am = low ? r.h.z : (r.h.w >> 4);
+        const uint32_t mA = low ? 0x3F3Fu : 0x0F0Fu, mB = low ? 0u : 0x3030u;
+        const uint32_t scs = ((A >> sh) & mA) | ((r.h.y >> (sh + 2)) & mB);
+        const uint32_t mns = ((Am >> sh) & mA) | ((r.h.z >> (sh + 2)) & mB);
+        const uint32_t q[8] = {r.qa.x, r.qa.y, r.qa.z, r.qa.w, r.qb.x, r.qb.y, r.qb.z, r.qb.w};
+        float alo = 0.f, ahi = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t w = q[i], s = w >> 8;
+            const uint32_t a = w & 0x000F000Fu, b = s & 0x000F000Fu;   // low nibbles (x1)
+            const uint32_t c = w & 0x00F000F0u, e = s & 0x00F000F0u;   // high nibbles (x16)
+            alo = mix_lo(a, xs[4 * i + 0], alo);
+            alo = mix_lo(b, xs[4 * i + 1], alo);
+            alo = mix_hi(a, xs[4 * i + 2], alo);
+            alo = mix_hi(b, xs[4 * i + 3], alo);
+            ahi = mix_lo(c, xs[32 + 4 * i + 0], ahi);
+            ahi = mix_lo(e, xs[32 + 4 * i + 1], ahi);
+            ahi = mix_hi(c, xs[32 + 4 * i + 2], ahi);
+            ahi = mix_hi(e, xs[32 + 4 * i + 3], ahi);
+        }
+        const float sc0 = (float)(scs & 0xFFu), sc1 = (float)(scs >> 8);
+        const float mn0 = (float)(mns & 0xFFu), mn1 = (float)(mns >> 8);
+        const float t = sc0 * alo + (sc1 * 0.0625f) * ahi;
+        return (d * kTwo24) * t - dmin * (mn0 * aux[0] + mn1 * aux[1]);
+    }
+};
+
+// ---------------------------------------------------------------- Q6_K
+// 210 B: ql[128] @0, qh[64] @128, scales i8[16] @192, d f16 @208
+// (dequant.rs:340-372).  Unit u (0..7) = half h = u/4, positions
+// l in [8p, 8p+8) with p = u%4, all four quarters g: 32 weights
+// 128h + 32g + l, scales sc[8h + p/2 + 2g].  Blocks are only 2-byte aligned,
+// so each field is read through an aligned dword window and realigned.
+struct Q6K {
+    static constexpr uint32_t BS = 256, BB = 210, UPB = 8, NX = 32, NAUX = 4;
+    struct Raw { uint32_t a[3], b[3], h[3], s[3], d; uint32_t ma; };
+    __device__ static void load_x(const float *__restrict__ x, uint32_t k, uint32_t u, float *xs, float *aux) {
+        const uint32_t h = u >> 2, p = u & 3u;
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const float4 *q = reinterpret_cast<const float4 *>(x + k * 256 + h * 128 + g * 32 + p * 8);
+            float4 v0 = q[0], v1 = q[1];
+            xs[8 * g + 0] = v0.x; xs[8 * g + 1] = v0.y; xs[8 * g + 2] = v0.z; xs[8 * g + 3] = v0.w;
+            xs[8 * g + 4] = v1.x; xs[8 * g + 5] = v1.y; xs[8 * g + 6] = v1.z; xs[8 * g + 7] = v1.w;
+            float s = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; i++) s += xs[8 * g + i];
+            aux[g] = s;
+        }
+    }
+    __device__ static Raw load(const uint8_t *__restrict__ blk, uint32_t u) {
+        const uint32_t h = u >> 2, p = u & 3u;
+        Raw r;
+        r.ma = (uint32_t)(reinterpret_cast<uintptr_t>(blk) & 3u);
+        const uint8_t *b0 = blk - r.ma;
+        const uint32_t *pa = reinterpret_cast<const uint32_t *>(b0 + 64 * h + 8 * p);
+        const uint32_t *pb = reinterpret_cast<const uint32_t *>(b0 + 64 * h + 32 + 8 * p);
+        const uint32_t *ph = reinterpret_cast<const uint32_t *>(b0 + 128 + 32 * h + 8 * p);
+        const uint32_t so = 192 + 8 * h + (p >> 1) + r.ma;   // scale bytes, from b0
+        const uint32_t *ps = reinterpret_cast<const uint32_t *>(b0 + (so & ~3u));
+#pragma unroll
+        for (int i = 0; i < 3; i++) { r.a[i] = pa[i]; r.b[i] = pb[i]; r.h[i] = ph[i]; r.s[i] = ps[i]; }
+        r.d = *reinterpret_cast<const uint32_t *>(b0 + 208);
+        return r;
+    }
+    __device__ static float dot(const Raw &r, uint32_t u, const float *xs, const float *aux) {
+        const uint32_t ma = r.ma, ms = (ma + ((u & 3u) >> 1)) & 3u;
+        const float d = f16_bits(r.d >> (8 * ma));
+        const uint32_t s_lo = align_bytes(r.s[1], r.s[0], ms), s_hi = align_bytes(r.s[2], r.s[1], ms);
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const uint32_t qa = align_bytes(r.a[i + 1], r.a[i], ma);
+            const uint32_t qb = align_bytes(r.b[i + 1], r.b[i], ma);
+            const uint32_t hh = align_bytes(r.h[i + 1], r.h[i], ma);
+            uint32_t q[4];
+            q[0] = (qa & 0x0F0F0F0Fu) | ((hh & 0x03030303u) << 4);
+            q[1] = (qb & 0x0F0F0F0Fu) | ((hh & 0x0C0C0C0Cu) << 2);
+            q[2] = ((qa >> 4) & 0x0F0F0F0Fu) | (hh & 0x30303030u);
+            q[3] = ((qb >> 4) & 0x0F0F0F0Fu) | ((hh >> 2) & 0x30303030u);
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const uint32_t ev = q[g] & 0x00FF00FFu, od = (q[g] >> 8) & 0x00FF00FFu;
+                acc[g] = mix_lo(ev, xs[8 * g + 4 * i + 0], acc[g]);
+                acc[g] = mix_lo(od, xs[8 * g + 4 * i + 1], acc[g]);
+                acc[g] = mix_hi(ev, xs[8 * g + 4 * i + 2], acc[g]);
+                acc[g] = mix_hi(od, xs[8 * g + 4 * i + 3], acc[g]);
+            }
+        }
+        const float sc0 = (float)(int8_t)(s_lo & 0xFFu), sc1 = (float)(int8_t)((s_lo >> 16) & 0xFFu);
+        const float sc2 = (float)(int8_t)(s_hi & 0xFFu), sc3 = (float)(int8_t)((s_hi >> 16) & 0xFFu);
+        float t = sc0 * (acc[0] * kTwo24 - 32.f * aux[0]);
+        t += sc1 * (acc[1] * kTwo24 - 32.f * aux[1]);
+        t += sc2 * (acc[2] * kTwo24 - 32.f * aux[2]);
+        t += sc3 * (acc[3] * kTwo24 - 32.f * aux[3]);
+        return d * t;
+    }
+};
+
+// ---------------------------------------------------------------- Q8_0
+// 34 B: d f16 @0, qs i8[32] @2 (dequant.rs:139-150). One block per unit.
+struct Q80 {
+    static constexpr uint32_t BS = 32, BB = 34, UPB = 1, NX = 32, NAUX = 1;
+    struct Raw { uint32_t w[9]; uint32_t ma; };
+    __device__ static void load_x(const float *__restrict__ x, uint32_t k, uint32_t, float *xs, float *aux) {
+        const float4 *p = reinterpret_cast<const float4 *>(x + k * 32);
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            float4 v = p[i];
+            xs[4 * i] = v.x; xs[4 * i + 1] = v.y; xs[4 * i + 2] = v.z; xs[4 * i + 3] = v.w;
+        }
+#pragma unroll
+        for (int i = 0; i < 32; i++) s += xs[i];
+        aux[0] = s;
+    }
+    __device__ static Raw load(const uint8_t *__restrict__ blk, uint32_t) {
+        Raw r;
+        r.ma = (uint32_t)(reinterpret_cast<uintptr_t>(blk) & 3u);
+        const uint32_t *p = reinterpret_cast<const uint32_t *>(blk - r.ma);
+#pragma unroll
+        for (int i = 0; i < 9; i++) r.w[i] = p[i];
+        return r;
+    }
+    __device__ static float dot(const Raw &r, uint32_t, const float *xs, const float *aux) {
+        const float d = f16_bits(r.w[0] >> (8 * r.ma));
+        const uint32_t sh = 8 * (r.ma + 2);
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t q = shr64(r.w[i + 1], r.w[i], sh) ^ 0x80808080u;   // q + 128
+            const uint32_t ev = q & 0x00FF00FFu, od = (q >> 8) & 0x00FF00FFu;
+            acc = mix_lo(ev, xs[4 * i + 0], acc);
+            acc = mix_lo(od, xs[4 * i + 1], acc);
+            acc = mix_hi(ev, xs[4 * i + 2], acc);
+            acc = mix_hi(od, xs[4 * i + 3], acc);
+        }
+        return d * (acc * kTwo24 - 128.f * aux[0]);
+    }
+};
+
+// ---------------------------------------------------------------- Q4_0
+// 18 B: d f16 @0, qs[16] @2, Yule's interleaved order: byte i holds weight
+// 2i (low nibble) and 2i+1 (high nibble) (dequant.rs:77-86).
+struct Q40 {
+    static constexpr uint32_t BS = 32, BB = 18, UPB = 1, NX = 32, NAUX = 1;
+    struct Raw { uint32_t w[5]; uint32_t ma; };
+    __device__ static void load_x(const float *__restrict__ x, uint32_t k, uint32_t u, float *xs, float *aux) {
+        Q80::load_x(x, k, u, xs, aux);
+    }
+    __device__ static Raw load(const uint8_t *__restrict__ blk, uint32_t) {
+        Raw r;
+        r.ma = (uint32_t)(reinterpret_cast<uintptr_t>(blk) & 3u);
+        const uint32_t *p = reinterpret_cast<const uint32_t *>(blk - r.ma);
+#pragma unroll
+        for (int i = 0; i < 5; i++) r.w[i] = p[i];
+        return r;
+    }
+    __device__ static float dot(const Raw &r, uint32_t, const float *xs, const float *aux) {
+        const float d = f16_bits(r.w[0] >> (8 * r.ma));
+        const uint32_t sh = 8 * (r.ma + 2);
+        float a1 = 0.f, a16 = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t w = shr64(r.w[i + 1], r.w[i], sh), s = w >> 8;
+            const uint32_t a = w & 0x000F000Fu, b = s & 0x000F000Fu;   // weights 8i+{0,4}, 8i+{2,6}
+            const uint32_t c = w & 0x00F000F0u, e = s & 0x00F000F0u;   // 8i+{1,5}, 8i+{3,7} (x16)
+            a1 = mix_lo(a, xs[8 * i + 0], a1);
+            a1 = mix_lo(b, xs[8 * i + 2], a1);
+            a1 = mix_hi(a, xs[8 * i + 4], a1);
+            a1 = mix_hi(b, xs[8 * i + 6], a1);
+            a16 = mix_lo(c, xs[8 * i + 1], a16);
+            a16 = mix_lo(e, xs[8 * i + 3], a16);
+            a16 = mix_hi(c, xs[8 * i + 5], a16);
+            a16 = mix_hi(e, xs[8 * i + 7], a16);
+        }
+        return d * ((a1 + a16 * 0.0625f) * kTwo24 - 8.f * aux[0]);
+    }
+};
+
+// ---------------------------------------------------------------- kernel
+template <class F, int TEAM, int R>
+__global__ __launch_bounds__(256) void qmv_kernel(const uint8_t *__restrict__ w, const float *__restrict__ x,
+                                                  float *__restrict__ y, uint32_t n_rows, uint32_t bpr) {
+    constexpr uint32_t SLOTS = 64 / TEAM;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = blockIdx.x * 4u + (threadIdx.x >> 6);
+    const uint32_t slot = lane / TEAM, t = lane % TEAM;
+    const uint32_t row0 = wave * (SLOTS * R) + slot;
+    const uint32_t units = bpr * F::UPB;
+    const size_t row_bytes = (size_t)bpr * F::BB;
+
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.f;
+
+    for (uint32_t u0 = 0; u0 < units; u0 += TEAM) {
+        const uint32_t u = u0 + t;
+        if (u < units) {
+            const uint32_t k = u / F::UPB, sub = u % F::UPB;
+            float xs[F::NX], aux[F::NAUX];
+            F::load_x(x, k, sub, xs, aux);
+            typename F::Raw raw[R];
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                uint32_t row = row0 + r * SLOTS;
+                row = row < n_rows ? row : n_rows - 1;   // rows past the end re-read the last row
+                raw[r] = F::load(w + row * row_bytes + (size_t)k * F::BB, sub);
+            }
+#pragma unroll
+            for (int r = 0; r < R; r++) acc[r] += F::dot(raw[r], sub, xs, aux);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+#pragma unroll
+        for (int off = TEAM / 2; off >= 1; off >>= 1) acc[r] += __shfl_xor(acc[r], off, 64);
+    }
+    if (t == 0) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t row = row0 + r * SLOTS;
+            if (row < n_rows) y[row] = acc[r];
+        }
+    }
+}
+
+template <class F, int TEAM, int R>
+static void launch_one(hipStream_t s, const uint8_t *w, const float *x, float *y, uint32_t n_rows, uint32_t bpr) {
+    constexpr uint32_t rows_per_wave = (64 / TEAM) * R;
+    const uint32_t waves = (n_rows + rows_per_wave - 1) / rows_per_wave;
+    const uint32_t blocks = (waves + 3) / 4;
+    hipLaunchKernelGGL((qmv_kernel<F, TEAM, R>), dim3(blocks), dim3(256), 0, s, w, x, y, n_rows, bpr);
+}
+
+template <class F, int TEAM>
+static void launch_team(hipStream_t s, const uint8_t *w, const float *x, float *y, uint32_t n_rows, uint32_t bpr) {
+    // Rows per wave: as many as keep >= 2048 waves in flight (8 per SIMD on
+    // 256 CUs), so small matrices still spread over the whole chip.
+    constexpr uint32_t slots = 64 / TEAM;
+    if ((uint64_t)n_rows >= 2048ull * slots * 8) launch_one<F, TEAM, 8>(s, w, x, y, n_rows, bpr);
+    else if ((uint64_t)n_rows >= 2048ull * slots * 4) launch_one<F, TEAM, 4>(s, w, x, y, n_rows, bpr);
+    else if ((uint64_t)n_rows >= 2048ull * slots * 2) launch_one<F, TEAM, 2>(s, w, x, y, n_rows, bpr);
+    else launch_one<F, TEAM, 1>(s, w, x, y, n_rows, bpr);
+}
+
+// Team width: the one of 64/32/16 lanes that wastes the fewest lanes on the
+// row's last column step (ties go to the wider team: fewer steps).
+static uint32_t pick_team(uint32_t units) {
+    uint32_t best = 64;
+    double best_eff = -1.0;
+    for (uint32_t team : {64u, 32u, 16u}) {
+        const uint32_t steps = (units + team - 1) / team;
+        const double eff = (double)units / (double)(steps * team);
+        if (eff > best_eff + 1e-9) { best_eff = eff; best = team; }
+    }
+    return best;
+}
+
+template <class F>
+static void launch_fmt(hipStream_t s, const uint8_t *w, const float *x, float *y, uint32_t n_rows, uint32_t n_cols) {
+    const uint32_t bpr = n_cols / F::BS;
+    switch (pick_team(bpr * F::UPB)) {
+    case 64: launch_team<F, 64>(s, w, x, y, n_rows, bpr); break;
+    case 32: launch_team<F, 32>(s, w, x, y, n_rows, bpr); break;
+    default: launch_team<F, 16>(s, w, x, y, n_rows, bpr); break;
+    }
+}
+
+int launch_qmv(hipStream_t s, uint32_t dtype, const uint8_t *w, const float *x, float *y, uint32_t n_rows,
+               uint32_t n_cols) {
+    switch (dtype) {
+    case YULE_DTYPE_Q4_K: launch_fmt<Q4K>(s, w, x, y, n_rows, n_cols); break;
+    case YULE_DTYPE_Q6_K: launch_fmt<Q6K>(s, w, x, y, n_rows, n_cols); break;
+    case YULE_DTYPE_Q8_0: launch_fmt<Q80>(s, w, x, y, n_rows, n_cols); break;
+    case YULE_DTYPE_Q4_0: launch_fmt<Q40>(s, w, x, y, n_rows, n_cols); break;
+    default: return set_error(YULE_ERR_UNSUPPORTED, "quantized_matmul: unsupported dtype");
+    }
+    return check_launch("quantized_matmul");
+}
+
+// ---------------------------------------------------------------- dequant
+// One thread per output weight, exactly the reference's f32 operation order
+// (no contraction): dequant.rs:77-86, 142-150, 260-290, 346-372.
+__device__ __forceinline__ float f16_exact(const uint8_t *p) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(p[0] | (p[1] << 8)));
+}
+
+__device__ float dequant_one(uint32_t dtype, const uint8_t *__restrict__ blk, uint32_t e) {
+#pragma clang fp contract(off)
+    switch (dtype) {
+    case YULE_DTYPE_Q4_0: {
+        const uint8_t byte = blk[2 + e / 2];
+        const uint32_t nib = (e & 1u) ? (byte >> 4) : (byte & 0x0Fu);
+        return ((float)nib - 8.0f) * f16_exact(blk);
+    }
+    case YULE_DTYPE_Q8_0:
+        return (float)(int8_t)blk[2 + e] * f16_exact(blk);
+    case YULE_DTYPE_Q4_K: {
+        const float d = f16_exact(blk), dmin = f16_exact(blk + 2);
+        const uint32_t j = e / 64, hi = (e / 32) & 1u, l = e & 31u, sb = 2 * j + hi;
+        const uint8_t *q = blk + 4;
+        uint32_t sc, mn;
+        if (sb < 4) { sc = q[sb] & 63u; mn = q[sb + 4] & 63u; }
+        else {
+            sc = (q[sb + 4] & 0xFu) | ((uint32_t)(q[sb - 4] >> 6) << 4);
+            mn = (uint32_t)(q[sb + 4] >> 4) | ((uint32_t)(q[sb] >> 6) << 4);
+        }
+        const uint8_t qs = blk[16 + 32 * j + l];
+        const uint32_t v = hi ? (qs >> 4) : (qs & 0x0Fu);
+        const float scale = d * (float)sc, mnv = dmin * (float)mn;
+        return (float)v * scale - mnv;
+    }
+    case YULE_DTYPE_Q6_K: {
+        const float d = f16_exact(blk + 208);
+        const uint32_t half = e / 128, rr = e % 128, g = rr / 32, l = rr % 32;
+        const uint8_t *ql = blk + 64 * half, *qh = blk + 128 + 32 * half;
+        uint32_t v;
+        switch (g) {
+        case 0: v = (ql[l] & 0xFu) | ((qh[l] & 3u) << 4); break;
+        case 1: v = (ql[l + 32] & 0xFu) | (((qh[l] >> 2) & 3u) << 4); break;
+        case 2: v = (uint32_t)(ql[l] >> 4) | (((qh[l] >> 4) & 3u) << 4); break;
+        default: v = (uint32_t)(ql[l + 32] >> 4) | (((qh[l] >> 6) & 3u) << 4); break;
+        }
+        const int q = (int)v - 32;
+        const int8_t sc = (int8_t)blk[192 + 8 * half + l / 16 + 2 * g];
+        return d * (float)sc * (float)q;
+    }
+    default:
+        return 0.f;
+    }
+}
+
+__global__ void dequant_kernel(uint32_t dtype, uint32_t bs, uint32_t bb, const uint8_t *__restrict__ src,
+                               float *__restrict__ dst, uint64_t n) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    dst[i] = dequant_one(dtype, src + (i / bs) * bb, (uint32_t)(i % bs));
+}
+
+__global__ void embed_kernel(uint32_t dtype, uint32_t bs, uint32_t bb, const uint8_t *__restrict__ table,
+                             const uint32_t *__restrict__ token, uint32_t n_rows, float *__restrict__ dst,
+                             uint32_t dim) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= dim) return;
+    uint32_t t = token[0];
+    t = t < n_rows ? t : n_rows - 1;   // a host-checked token is always in range
+    const uint8_t *row = table + (size_t)t * (dim / bs) * bb;
+    dst[i] = dequant_one(dtype, row + (i / bs) * bb, i % bs);
+}
+
+int launch_dequant(hipStream_t s, uint32_t dtype, const uint8_t *src, float *dst, uint32_t n_blocks) {
+    uint32_t bs, bb;
+    if (!quant_geometry(dtype, &bs, &bb)) return set_error(YULE_ERR_UNSUPPORTED, "dequantize: unsupported dtype");
+    const uint64_t n = (uint64_t)n_blocks * bs;
+    if (n == 0) return YULE_OK;
+    hipLaunchKernelGGL(dequant_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, dtype, bs, bb, src, dst, n);
+    return check_launch("dequantize");
+}
+
+int launch_embed_rows(hipStream_t s, uint32_t dtype, const uint8_t *table, const uint32_t *token, uint32_t n_rows,
+                      float *dst, uint32_t dim) {
+    uint32_t bs, bb;
+    if (!quant_geometry(dtype, &bs, &bb)) return set_error(YULE_ERR_UNSUPPORTED, "embedding: unsupported dtype");
+    hipLaunchKernelGGL(embed_kernel, dim3((dim + 255) / 256), dim3(256), 0, s, dtype, bs, bb, table, token, n_rows,
+                       dst, dim);
+    return check_launch("embedding");
+}
+
+}  // namespace yule

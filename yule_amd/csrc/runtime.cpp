@@ -1,0 +1,336 @@
+// runtime.cpp — backend object, buffer handles, copies and the validated
+// quantized_matmul entry point of libyule_hip.so.
+//
+// Mirrors the ComputeBackend trait's host-side contract
+// (yule-gpu/src/lib.rs:21-132): opaque u64 handles from a global counter
+// (yule-gpu/src/buffer.rs:5-9), zero-initialised buffers
+// (yule-gpu/src/cpu.rs:157), Result<()> as status code + message.
+#include <atomic>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "internal.h"
+
+namespace {
+thread_local std::string g_last_error;
+std::atomic<uint64_t> g_next_handle{1};
+}  // namespace
+
+namespace yule {
+
+int set_error(int code, const std::string &msg) {
+    g_last_error = msg;
+    return code;
+}
+
+int hip_error(hipError_t e, const char *what) {
+    if (e == hipSuccess) return YULE_OK;
+    return set_error(e == hipErrorOutOfMemory ? YULE_ERR_OOM : YULE_ERR_HIP,
+                     std::string(what) + ": " + hipGetErrorString(e));
+}
+
+int check_launch(const char *what) {
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? YULE_OK : hip_error(e, what);
+}
+
+int get_buffer(yule_hip_backend *be, uint64_t h, size_t need, void **ptr, const char *what, size_t offset) {
+    std::lock_guard<std::mutex> lk(be->mu);
+    auto it = be->buffers.find(h);
+    if (it == be->buffers.end())
+        return set_error(YULE_ERR_INVALID, std::string(what) + ": buffer " + std::to_string(h) + " not found");
+    if (offset > it->second.size || need > it->second.size - offset)
+        return set_error(YULE_ERR_INVALID, std::string(what) + ": access of " + std::to_string(need) +
+                                               " bytes at offset " + std::to_string(offset) +
+                                               " exceeds buffer " + std::to_string(h) + " of " +
+                                               std::to_string(it->second.size) + " bytes");
+    *ptr = static_cast<uint8_t *>(it->second.ptr) + offset;
+    return YULE_OK;
+}
+
+bool quant_geometry(uint32_t dtype, uint32_t *bs, uint32_t *bb) {
+    switch (dtype) {  // yule-core/src/dtype.rs:62-118
+    case YULE_DTYPE_Q4_0: *bs = 32; *bb = 18; return true;
+    case YULE_DTYPE_Q8_0: *bs = 32; *bb = 34; return true;
+    case YULE_DTYPE_Q4_K: *bs = 256; *bb = 144; return true;
+    case YULE_DTYPE_Q6_K: *bs = 256; *bb = 210; return true;
+    default: return false;
+    }
+}
+
+}  // namespace yule
+
+using namespace yule;
+
+#define YULE_CHECK_BE(be)                                                         \
+    do {                                                                          \
+        if (!(be)) return set_error(YULE_ERR_INVALID, "null backend");            \
+    } while (0)
+
+extern "C" {
+
+const char *yule_hip_last_error(void) { return g_last_error.c_str(); }
+
+static bool is_gfx950(const hipDeviceProp_t &p) { return std::strncmp(p.gcnArchName, "gfx950", 6) == 0; }
+
+int yule_hip_is_available(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return 0;
+    for (int i = 0; i < n; i++) {
+        hipDeviceProp_t p;
+        if (hipGetDeviceProperties(&p, i) == hipSuccess && is_gfx950(p)) return 1;
+    }
+    return 0;
+}
+
+int yule_hip_create(int device, yule_hip_backend **out) {
+    if (!out) return set_error(YULE_ERR_INVALID, "create: null out pointer");
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0)
+        return set_error(YULE_ERR_NO_DEVICE, "create: no HIP device present");
+    if (device < 0 || device >= n)
+        return set_error(YULE_ERR_NO_DEVICE, "create: device " + std::to_string(device) + " out of range");
+    auto *be = new yule_hip_backend();
+    be->device = device;
+    int rc;
+    if ((rc = hip_error(hipSetDevice(device), "hipSetDevice")) ||
+        (rc = hip_error(hipGetDeviceProperties(&be->props, device), "hipGetDeviceProperties"))) {
+        delete be;
+        return rc;
+    }
+    if (!is_gfx950(be->props)) {
+        std::string arch = be->props.gcnArchName;
+        delete be;
+        return set_error(YULE_ERR_NO_DEVICE, "create: device is " + arch + ", this build targets gfx950");
+    }
+    // default-priority stream (no priority games); non-blocking w.r.t. the null stream
+    if ((rc = hip_error(hipStreamCreateWithFlags(&be->stream, hipStreamNonBlocking), "hipStreamCreate"))) {
+        delete be;
+        return rc;
+    }
+    *out = be;
+    return YULE_OK;
+}
+
+int yule_hip_destroy(yule_hip_backend *be) {
+    if (!be) return YULE_OK;
+    hipSetDevice(be->device);
+    hipStreamSynchronize(be->stream);
+    for (auto &kv : be->buffers) hipFree(kv.second.ptr);
+    be->buffers.clear();
+    hipStreamDestroy(be->stream);
+    delete be;
+    return YULE_OK;
+}
+
+const char *yule_hip_name(const yule_hip_backend *) { return "hip"; }
+
+int yule_hip_device_info(yule_hip_backend *be, yule_device_info *out) {
+    YULE_CHECK_BE(be);
+    if (!out) return set_error(YULE_ERR_INVALID, "device_info: null out");
+    std::memset(out, 0, sizeof(*out));
+    std::snprintf(out->name, sizeof(out->name), "%s (%s)", be->props.name, be->props.gcnArchName);
+    out->backend = 4;
+    out->memory_bytes = be->props.totalGlobalMem;
+    out->compute_units = (uint32_t)be->props.multiProcessorCount;
+    return YULE_OK;
+}
+
+int yule_hip_allocate(yule_hip_backend *be, size_t size, yule_buffer *out) {
+    YULE_CHECK_BE(be);
+    if (!out) return set_error(YULE_ERR_INVALID, "allocate: null out");
+    void *p = nullptr;
+    int rc = hip_error(hipMalloc(&p, size + kAllocSlack), "allocate");
+    if (rc) return rc;
+    // zero-initialised like the reference backends; ordered before any later
+    // work on the same stream
+    if ((rc = hip_error(hipMemsetAsync(p, 0, size + kAllocSlack, be->stream), "allocate: zero-fill"))) {
+        hipFree(p);
+        return rc;
+    }
+    const uint64_t h = g_next_handle.fetch_add(1);
+    {
+        std::lock_guard<std::mutex> lk(be->mu);
+        be->buffers[h] = Buffer{p, size};
+    }
+    *out = h;
+    return YULE_OK;
+}
+
+int yule_hip_free(yule_hip_backend *be, yule_buffer h) {
+    YULE_CHECK_BE(be);
+    void *p = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(be->mu);
+        auto it = be->buffers.find(h);
+        if (it == be->buffers.end()) return YULE_OK;  // CpuBackend::free ignores unknown handles
+        p = it->second.ptr;
+        be->buffers.erase(it);
+    }
+    // queued kernels may still read the buffer
+    int rc = hip_error(hipStreamSynchronize(be->stream), "free: synchronize");
+    hipFree(p);
+    return rc;
+}
+
+int yule_hip_copy_to_device(yule_hip_backend *be, const void *data, size_t size, yule_buffer h) {
+    YULE_CHECK_BE(be);
+    if (!data && size) return set_error(YULE_ERR_INVALID, "copy_to_device: null data");
+    void *p;
+    int rc = get_buffer(be, h, size, &p, "copy_to_device");
+    if (rc || !size) return rc;
+    if ((rc = hip_error(hipMemcpyAsync(p, data, size, hipMemcpyHostToDevice, be->stream), "copy_to_device")))
+        return rc;
+    return hip_error(hipStreamSynchronize(be->stream), "copy_to_device: synchronize");
+}
+
+int yule_hip_copy_from_device(yule_hip_backend *be, yule_buffer h, void *data, size_t size) {
+    YULE_CHECK_BE(be);
+    if (!data && size) return set_error(YULE_ERR_INVALID, "copy_from_device: null data");
+    void *p;
+    int rc = get_buffer(be, h, size, &p, "copy_from_device");
+    if (rc || !size) return rc;
+    if ((rc = hip_error(hipMemcpyAsync(data, p, size, hipMemcpyDeviceToHost, be->stream), "copy_from_device")))
+        return rc;
+    return hip_error(hipStreamSynchronize(be->stream), "copy_from_device: synchronize");
+}
+
+// yule-gpu/src/cpu.rs:425-434: copies min(size, src_len, dst_len) bytes
+int yule_hip_copy_buffer(yule_hip_backend *be, yule_buffer src, yule_buffer dst, size_t size) {
+    YULE_CHECK_BE(be);
+    size_t ssz = 0, dsz = 0;
+    void *ps = nullptr, *pd = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(be->mu);
+        auto a = be->buffers.find(src), b = be->buffers.find(dst);
+        if (a == be->buffers.end() || b == be->buffers.end())
+            return set_error(YULE_ERR_INVALID, "copy_buffer: buffer not found");
+        ps = a->second.ptr; ssz = a->second.size;
+        pd = b->second.ptr; dsz = b->second.size;
+    }
+    size_t n = size < ssz ? size : ssz;
+    n = n < dsz ? n : dsz;
+    if (!n) return YULE_OK;
+    return hip_error(hipMemcpyAsync(pd, ps, n, hipMemcpyDeviceToDevice, be->stream), "copy_buffer");
+}
+
+// yule-gpu/src/cpu.rs:436-452: dst[dst_off..dst_off+size] = src[src_off..src_off+size]
+int yule_hip_copy_buffer_offset(yule_hip_backend *be, yule_buffer src, yule_buffer dst, size_t src_offset,
+                                size_t dst_offset, size_t size) {
+    YULE_CHECK_BE(be);
+    void *ps, *pd;
+    int rc;
+    if ((rc = get_buffer(be, src, size, &ps, "copy_buffer_offset (src)", src_offset))) return rc;
+    if ((rc = get_buffer(be, dst, size, &pd, "copy_buffer_offset (dst)", dst_offset))) return rc;
+    if (!size) return YULE_OK;
+    return hip_error(hipMemcpyAsync(pd, ps, size, hipMemcpyDeviceToDevice, be->stream), "copy_buffer_offset");
+}
+
+int yule_hip_synchronize(yule_hip_backend *be) {
+    YULE_CHECK_BE(be);
+    return hip_error(hipStreamSynchronize(be->stream), "synchronize");
+}
+
+// Shared validation of the quantized entry points.
+static int check_qmv_args(yule_hip_backend *be, yule_buffer weights, yule_buffer input, yule_buffer output,
+                          uint32_t n_rows, uint32_t n_cols, uint32_t dtype, const char *what, const uint8_t **w,
+                          const float **x, float **y, bool *empty_rows) {
+    uint32_t bs, bb;
+    if (!quant_geometry(dtype, &bs, &bb))
+        return set_error(YULE_ERR_UNSUPPORTED,
+                         std::string(what) + ": dtype " + std::to_string(dtype) + " not supported on this backend");
+    if (n_cols % bs)
+        return set_error(YULE_ERR_INVALID, std::string(what) + ": n_cols " + std::to_string(n_cols) +
+                                               " is not a multiple of the block size " + std::to_string(bs));
+    if (input == output) return set_error(YULE_ERR_INVALID, std::string(what) + ": input and output alias");
+    void *pw, *px, *py;
+    int rc;
+    const size_t wbytes = (size_t)n_rows * (n_cols / bs) * bb;
+    if ((rc = get_buffer(be, weights, wbytes, &pw, what))) return rc;
+    if ((rc = get_buffer(be, input, (size_t)n_cols * 4, &px, what))) return rc;
+    if ((rc = get_buffer(be, output, (size_t)n_rows * 4, &py, what))) return rc;
+    *w = (const uint8_t *)pw; *x = (const float *)px; *y = (float *)py;
+    *empty_rows = n_cols == 0;
+    return YULE_OK;
+}
+
+int yule_hip_quantized_matmul(yule_hip_backend *be, yule_buffer weights, yule_buffer input, yule_buffer output,
+                              uint32_t n_rows, uint32_t n_cols, uint32_t dtype) {
+    YULE_CHECK_BE(be);
+    const uint8_t *w; const float *x; float *y; bool empty;
+    int rc = check_qmv_args(be, weights, input, output, n_rows, n_cols, dtype, "quantized_matmul", &w, &x, &y, &empty);
+    if (rc) return rc;
+    if (n_rows == 0) return YULE_OK;
+    if (empty) return launch_fill(be->stream, y, 0.0f, n_rows);  // zero blocks per row -> y = 0
+    return launch_qmv(be->stream, dtype, w, x, y, n_rows, n_cols);
+}
+
+int yule_hip_dequantize(yule_hip_backend *be, yule_buffer src, size_t src_offset, yule_buffer dst,
+                        uint32_t n_blocks, uint32_t dtype) {
+    YULE_CHECK_BE(be);
+    uint32_t bs, bb;
+    if (!quant_geometry(dtype, &bs, &bb))
+        return set_error(YULE_ERR_UNSUPPORTED, "dequantize: dtype " + std::to_string(dtype) + " not supported");
+    void *ps, *pd;
+    int rc;
+    if ((rc = get_buffer(be, src, (size_t)n_blocks * bb, &ps, "dequantize (src)", src_offset))) return rc;
+    if ((rc = get_buffer(be, dst, (size_t)n_blocks * bs * 4, &pd, "dequantize (dst)"))) return rc;
+    return launch_dequant(be->stream, dtype, (const uint8_t *)ps, (float *)pd, n_blocks);
+}
+
+int yule_hip_time_qmv_ops(yule_hip_backend *be, const yule_qmv_op *ops, uint32_t n_ops, uint32_t iters,
+                          int use_graph, float *ms_total) {
+    YULE_CHECK_BE(be);
+    if (!ops || !ms_total || n_ops == 0 || iters == 0)
+        return set_error(YULE_ERR_INVALID, "time_qmv_ops: bad arguments");
+    struct Launch { uint32_t dtype, n_rows, n_cols; const uint8_t *w; const float *x; float *y; };
+    std::vector<Launch> L(n_ops);
+    for (uint32_t i = 0; i < n_ops; i++) {
+        bool empty;
+        int rc = check_qmv_args(be, ops[i].weights, ops[i].input, ops[i].output, ops[i].n_rows, ops[i].n_cols,
+                                ops[i].dtype, "time_qmv_ops", &L[i].w, &L[i].x, &L[i].y, &empty);
+        if (rc) return rc;
+        if (empty || ops[i].n_rows == 0) return set_error(YULE_ERR_INVALID, "time_qmv_ops: empty matrix");
+        L[i].dtype = ops[i].dtype; L[i].n_rows = ops[i].n_rows; L[i].n_cols = ops[i].n_cols;
+    }
+    auto enqueue = [&]() -> int {
+        for (const Launch &l : L) {
+            int rc = launch_qmv(be->stream, l.dtype, l.w, l.x, l.y, l.n_rows, l.n_cols);
+            if (rc) return rc;
+        }
+        return YULE_OK;
+    };
+    int rc = YULE_OK;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    if (use_graph) {
+        if ((rc = hip_error(hipStreamBeginCapture(be->stream, hipStreamCaptureModeThreadLocal), "begin capture")))
+            return rc;
+        int erc = enqueue();
+        rc = hip_error(hipStreamEndCapture(be->stream, &graph), "end capture");
+        if (erc) rc = erc;
+        if (!rc) rc = hip_error(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0), "graph instantiate");
+        if (!rc) rc = hip_error(hipGraphLaunch(exec, be->stream), "graph warm-up launch");
+    }
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (!rc) rc = hip_error(hipEventCreate(&e0), "hipEventCreate");
+    if (!rc) rc = hip_error(hipEventCreate(&e1), "hipEventCreate");
+    if (!rc) rc = hip_error(hipEventRecord(e0, be->stream), "hipEventRecord");
+    for (uint32_t it = 0; it < iters && !rc; it++)
+        rc = use_graph ? hip_error(hipGraphLaunch(exec, be->stream), "graph launch") : enqueue();
+    if (!rc) rc = hip_error(hipEventRecord(e1, be->stream), "hipEventRecord");
+    if (!rc) rc = hip_error(hipEventSynchronize(e1), "hipEventSynchronize");
+    float ms = 0.f;
+    if (!rc) rc = hip_error(hipEventElapsedTime(&ms, e0, e1), "hipEventElapsedTime");
+    if (e0) hipEventDestroy(e0);
+    if (e1) hipEventDestroy(e1);
+    if (exec) hipGraphExecDestroy(exec);
+    if (graph) hipGraphDestroy(graph);
+    if (!rc) *ms_total = ms;
+    return rc;
+}
+
+}  // extern "C"
