@@ -2,8 +2,11 @@
 
 A "step" is one pass of the hot path over one batch of synthetic input: the
 seven batch-1 projections of one Llama-3-8B layer (Q 4096x4096, K and V
-1024x4096, O 4096x4096, gate and up 14336x4096, down 4096x14336) in Q4_K,
-each a `quantized_matmul` over raw GGUF blocks.
+1024x4096, O 4096x4096, gate and up 14336x4096, down 4096x14336) in Q4_K
+over raw GGUF blocks, launched as the HIP runner
+launches them: Q/K/V in one `quantized_matmul_multi` (they share the normed
+input), O, gate/up in one, down.  The same layer as seven separate
+`quantized_matmul` calls is reported beside it.
 Steps cycle through `--copies` distinct copies of the layer (8 x 122.7 MB by
 default) so no step re-reads weights left in the 256 MB last-level cache;
 all inputs are resident in HBM before the timed region.  Timing: HIP events
@@ -78,9 +81,20 @@ class Layer:
         self.copies = copies
         self.step_bytes = sum(algo_bytes(dt, r, c) for _, r, c in shapes)
 
-    def ops_for_step(self, s):
+    def ops_for_step(self, s, fused=True):
+        """One layer pass.  fused: the HIP runner's launches -- Q/K/V as one
+        multi-matrix launch, O, gate/up as one, down; else seven calls."""
         c = s % self.copies
-        return [(self.w[n][c], self.x[cols], self.y[n][c], r, cols, self.dt) for n, r, cols in self.shapes]
+        if not fused or [n for n, _, _ in self.shapes] != [n for n, _, _ in LLAMA3_LAYER]:
+            return [(self.w[n][c], self.x[cols], self.y[n][c], r, cols, self.dt) for n, r, cols in self.shapes]
+        sh = {n: (r, cols) for n, r, cols in self.shapes}
+
+        def group(names):
+            cols = sh[names[0]][1]
+            return ([self.w[n][c] for n in names], self.x[cols], [self.y[n][c] for n in names],
+                    [sh[n][0] for n in names], cols, self.dt)
+        return [group(["attn_q", "attn_k", "attn_v"]), group(["attn_output"]), group(["ffn_gate", "ffn_up"]),
+                group(["ffn_down"])]
 
     def ops_for_matrix(self, name, n):
         _, r, cols = next(s for s in self.shapes if s[0] == name)
@@ -95,24 +109,27 @@ class Layer:
             self.hip.free(h)
 
 
-def time_steps(hip, layer, steps, start=0):
-    ops = [op for s in range(start, start + steps) for op in layer.ops_for_step(s)]
+USE_GRAPH = True
+
+
+def time_steps(hip, layer, steps, start=0, fused=True):
+    ops = [op for s in range(start, start + steps) for op in layer.ops_for_step(s, fused)]
     hip.synchronize()
-    ms = hip.time_qmv_ops(ops, 1, use_graph=True)
+    ms = hip.time_qmv_ops(ops, 1, use_graph=USE_GRAPH)
     hip.synchronize()
     return ms
 
 
 def matrix_rate(hip, layer, name, launches):
     _, r, c = next(s for s in layer.shapes if s[0] == name)
-    hip.time_qmv_ops(layer.ops_for_matrix(name, min(launches, 64)), 1)       # warm-up
-    ms = hip.time_qmv_ops(layer.ops_for_matrix(name, launches), 1)
+    hip.time_qmv_ops(layer.ops_for_matrix(name, min(launches, 64)), 1, USE_GRAPH)       # warm-up
+    ms = hip.time_qmv_ops(layer.ops_for_matrix(name, launches), 1, USE_GRAPH)
     us = 1e3 * ms / launches
     gbs = algo_bytes(layer.dt, r, c) / (us * 1e-6) / 1e9
     return us, gbs
 
 
-def cpu_baseline(layer, budget_s=12.0, max_passes=40):
+def cpu_baseline(layer, budget_s=12.0, max_passes=2000):
     """Yule's CPU decode matvec path (oracle restatement of model_runner.rs:
     152-244 + simd/avx2.rs) over the same Q4_K layer bytes, host-resident."""
     import oracle
@@ -164,7 +181,11 @@ def main():
     ap.add_argument("--copies", type=int, default=8)
     ap.add_argument("--quick", action="store_true", help="primary metric and roofline only")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="launch kernels one by one instead of replaying a HIP graph (for profilers)")
     args = ap.parse_args()
+    global USE_GRAPH
+    USE_GRAPH = not args.no_graph
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the matvec shards by "
               f"rows with no exchange, so N GPUs would each run 1/N of every projection.", file=sys.stderr)
@@ -184,6 +205,9 @@ def main():
     ms_per_step = ms / args.steps
     value = q4k.step_bytes * args.steps / (ms * 1e-3) / 1e9
     log(f"Q4_K layer: {ms_per_step * 1e3:.2f} us/step, {value:.1f} GB/s ({100 * value / HBM_PEAK_GBS:.1f}% of peak)")
+    ms7 = time_steps(hip, q4k, args.steps, fused=False)
+    value7 = q4k.step_bytes * args.steps / (ms7 * 1e-3) / 1e9
+    log(f"Q4_K layer as 7 separate calls: {value7:.1f} GB/s")
 
     # dominant kernel: Q4_K 14336x4096 (gate/up), average launch duration
     n_dom = 1000
@@ -195,7 +219,7 @@ def main():
                 "algo_bytes_per_launch": dom_bytes}
     log(f"dominant kernel Q4_K 14336x4096: {us:.2f} us/launch, {gbs:.1f} GB/s")
 
-    extra = {"per_matrix_q4k": {}}
+    extra = {"layer_as_7_calls_GB/s": round(value7, 1), "per_matrix_q4k": {}}
     for name, r, c in LLAMA3_LAYER:
         u, g = matrix_rate(hip, q4k, name, 400)
         extra["per_matrix_q4k"][f"{name} {r}x{c}"] = {"us": round(u, 2), "GB/s": round(g, 1)}

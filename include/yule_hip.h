@@ -128,6 +128,16 @@ int yule_hip_quantized_matmul(yule_hip_backend *be, yule_buffer weights, yule_bu
 
 /* ---- extensions beyond the trait (used by the HIP runner) ---- */
 
+/* quantized_matmul of n_mats (1..4) matrices that share one input vector,
+ * n_cols and dtype, in a single launch over their concatenated rows:
+ * outputs[i][r] = sum_b vec_dot(weights[i][r, b], input[b*bs..]).  The
+ * Q/K/V and gate/up projections of a decode step (yule-infer/src/
+ * model_runner.rs:636-638, :963-964; gpu_runner.rs:392-419) each become
+ * one launch.  Same validation and results as n_mats separate calls. */
+int yule_hip_quantized_matmul_multi(yule_hip_backend *be, uint32_t n_mats, const yule_buffer *weights,
+                                    const yule_buffer *outputs, const uint32_t *n_rows, yule_buffer input,
+                                    uint32_t n_cols, uint32_t dtype);
+
 /* dequant_block over n_blocks consecutive blocks starting src_offset bytes
  * into src (yule-core/src/dequant.rs:1232-1275), bit-exact, f32 out.
  * Replaces the CPU embedding dequant + upload of
@@ -167,10 +177,14 @@ int yule_hip_quantized_gemm(yule_hip_backend *be, yule_buffer weights, yule_buff
 
 /* ---- timing helpers for harnesses (no trait counterpart) ---- */
 
-/* One quantized_matmul call, for the timing helper below. */
+/* One quantized_matmul (n_mats == 1) or quantized_matmul_multi call, for
+ * the timing helper below. */
 typedef struct {
-    yule_buffer weights, input, output;
-    uint32_t n_rows, n_cols, dtype;
+    uint32_t n_mats;
+    yule_buffer weights[4], outputs[4];
+    uint32_t n_rows[4];
+    yule_buffer input;
+    uint32_t n_cols, dtype;
 } yule_qmv_op;
 
 /* Run the list `ops` `iters` times on the backend stream and report the

@@ -172,3 +172,34 @@ def test_qmv_edge_cases_and_errors(hip):
         hip.quantized_matmul(hw, hx, 999999, 4, 256, dt)  # unknown handle
     for h in (hw, hx, hy):
         hip.free(h)
+
+
+@pytest.mark.parametrize("dt", FMTS, ids=lambda d: d.name)
+def test_qmv_multi_equals_separate_calls(hip, dt):
+    """quantized_matmul_multi (Q/K/V- and gate/up-style fusion) returns exactly
+    what separate quantized_matmul calls return, for 1..4 matrices."""
+    n_cols = 2048
+    rows = [2048, 256, 256, 777]
+    say(f"[qmv_multi] {dt.name} rows={rows}")
+    ws = [synth.gen_quant(dt, 300 + i, r, n_cols) for i, r in enumerate(rows)]
+    x = synth.gauss(301, n_cols)
+    hx = hip.upload(x)
+    hws = [hip.upload(w) for w in ws]
+    for n in (1, 2, 3, 4):
+        outs = [hip.allocate(4 * r) for r in rows[:n]]
+        hip.quantized_matmul_multi(hws[:n], hx, outs, rows[:n], n_cols, dt)
+        got = [hip.download(o, r) for o, r in zip(outs, rows)]
+        for i in range(n):
+            sep = gpu_qmv(hip, dt, ws[i], x, rows[i], n_cols)
+            assert np.array_equal(got[i], sep)
+            ref = oracle.qmv_f64(int(dt), ws[i], x, rows[i], n_cols)
+            assert np.max(np.abs(got[i] - ref)) <= tolerance_bar(ref)
+        for o in outs:
+            hip.free(o)
+    o1, o2 = hip.allocate(4 * 2048), hip.allocate(4 * 256)
+    with pytest.raises(YuleGpuError):
+        hip.quantized_matmul_multi(hws[:2], hx, [o1, o1], rows[:2], n_cols, dt)   # outputs alias
+    with pytest.raises(YuleGpuError):
+        hip.quantized_matmul_multi(hws[:2], hx, [o1, hx], rows[:2], n_cols, dt)   # output aliases input
+    for h in hws + [hx, o1, o2]:
+        hip.free(h)

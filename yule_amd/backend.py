@@ -46,6 +46,9 @@ _SIGS: dict[str, tuple] = {
     "yule_hip_attn_score": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint64] + [C.c_uint32] * 5),
     "yule_hip_attn_value": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint64] + [C.c_uint32] * 5),
     "yule_hip_quantized_matmul": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint32]),
+    "yule_hip_quantized_matmul_multi": (C.c_int, [C.c_void_p, C.c_uint32, C.POINTER(C.c_uint64),
+                                                  C.POINTER(C.c_uint64), C.POINTER(C.c_uint32), C.c_uint64,
+                                                  C.c_uint32, C.c_uint32]),
     "yule_hip_dequantize": (C.c_int, [C.c_void_p, C.c_uint64, C.c_size_t, C.c_uint64, C.c_uint32, C.c_uint32]),
     "yule_hip_silu_mul": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint32]),
     "yule_hip_gqa_decode_attn": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint64] + [C.c_uint32] * 4),
@@ -65,9 +68,17 @@ class YuleGpuError(RuntimeError):
 
 
 class QmvOp(C.Structure):
-    """yule_qmv_op: one quantized_matmul call for time_qmv_ops."""
-    _fields_ = [("weights", C.c_uint64), ("input", C.c_uint64), ("output", C.c_uint64), ("n_rows", C.c_uint32),
-                ("n_cols", C.c_uint32), ("dtype", C.c_uint32)]
+    """yule_qmv_op: one quantized_matmul(_multi) call for time_qmv_ops."""
+    _fields_ = [("n_mats", C.c_uint32), ("weights", C.c_uint64 * 4), ("outputs", C.c_uint64 * 4),
+                ("n_rows", C.c_uint32 * 4), ("input", C.c_uint64), ("n_cols", C.c_uint32), ("dtype", C.c_uint32)]
+
+    @classmethod
+    def make(cls, weights, outputs, n_rows, inp, n_cols, dtype):
+        n = len(weights)
+        pad = lambda v, f: list(v) + [f] * (4 - n)  # noqa: E731
+        return cls(n, (C.c_uint64 * 4)(*pad([_h(w) for w in weights], 0)),
+                   (C.c_uint64 * 4)(*pad([_h(y) for y in outputs], 0)), (C.c_uint32 * 4)(*pad(n_rows, 0)),
+                   _h(inp), n_cols, int(dtype))
 
 
 class _DeviceInfo(C.Structure):
@@ -223,6 +234,12 @@ class HipBackend:
                                                         int(dtype)))
 
     # -- extensions ----------------------------------------------------------
+    def quantized_matmul_multi(self, weights, inp, outputs, n_rows, n_cols: int, dtype: DType | int) -> None:
+        n = len(weights)
+        self._check(self._lib.yule_hip_quantized_matmul_multi(
+            self._be, n, (C.c_uint64 * n)(*map(_h, weights)), (C.c_uint64 * n)(*map(_h, outputs)),
+            (C.c_uint32 * n)(*n_rows), _h(inp), n_cols, int(dtype)))
+
     def dequantize(self, src, src_offset: int, dst, n_blocks: int, dtype: DType | int) -> None:
         self._check(self._lib.yule_hip_dequantize(self._be, _h(src), src_offset, _h(dst), n_blocks, int(dtype)))
 
@@ -242,8 +259,15 @@ class HipBackend:
 
     def time_qmv_ops(self, ops, iters: int, use_graph: bool = True) -> float:
         """Milliseconds (HIP events on the backend stream) for `iters` passes over
-        `ops`, a list of (weights, input, output, n_rows, n_cols, dtype)."""
-        arr = (QmvOp * len(ops))(*[QmvOp(_h(w), _h(x), _h(y), r, c, int(d)) for (w, x, y, r, c, d) in ops])
+        `ops`: tuples (weights, input, output, n_rows, n_cols, dtype) for one
+        matrix, or ([weights...], input, [outputs...], [n_rows...], n_cols, dtype)
+        for a multi-matrix launch."""
+        def mk(op):
+            w, x, y, r, c, d = op
+            if isinstance(w, (list, tuple)):
+                return QmvOp.make(w, y, r, x, c, d)
+            return QmvOp.make([w], [y], [r], x, c, d)
+        arr = (QmvOp * len(ops))(*[mk(op) for op in ops])
         ms = C.c_float()
         self._check(self._lib.yule_hip_time_qmv_ops(self._be, arr, len(ops), iters, int(use_graph), C.byref(ms)))
         return ms.value

@@ -51,10 +51,20 @@ int check_launch(const char *what);
 // unsupported by the quantized kernels.
 bool quant_geometry(uint32_t dtype, uint32_t *block_size, uint32_t *block_bytes);
 
+// One matrix of a multi-matrix matvec launch (all share input and n_cols).
+constexpr int kMaxSegs = 4;
+struct QmvSeg {
+    const uint8_t *w;
+    float *y;
+    uint32_t n_rows;
+};
+
 // Kernel launchers (device code in qmv.hip / ops.hip / attn.hip / gemm.hip).
 // Arguments are already validated; all enqueue on `stream`.
 int launch_qmv(hipStream_t stream, uint32_t dtype, const uint8_t *w, const float *x, float *y,
                uint32_t n_rows, uint32_t n_cols);
+int launch_qmv_multi(hipStream_t stream, uint32_t dtype, const QmvSeg *segs, uint32_t n_seg, const float *x,
+                     uint32_t n_cols);
 int launch_dequant(hipStream_t stream, uint32_t dtype, const uint8_t *src, float *dst,
                    uint32_t n_blocks);
 // dequantize row token[0] (clamped to n_rows-1) of a [n_rows][dim] quantized

@@ -57,16 +57,29 @@ __device__ __forceinline__ uint32_t shr64(uint32_t hi, uint32_t lo, uint32_t s) 
 
 constexpr float kTwo24 = 16777216.0f;
 
+// Activation accessors: float4 at element i (i % 4 == 0) of x, either from
+// global memory or from the LDS copy, which pads 4 floats after every 32 so
+// that lanes reading consecutive unit slices spread over the LDS banks.
+struct XGlobal {
+    const float *__restrict__ p;
+    __device__ float4 operator()(uint32_t i) const { return *reinterpret_cast<const float4 *>(p + i); }
+};
+__host__ __device__ __forceinline__ uint32_t lds_pad(uint32_t i) { return i + ((i >> 5) << 2); }
+struct XLds {
+    const float *p;
+    __device__ float4 operator()(uint32_t i) const { return *reinterpret_cast<const float4 *>(p + lds_pad(i)); }
+};
+
 // ---------------------------------------------------------------- Q4_K
 // 144 B: d f16 @0, dmin f16 @2, scales[12] @4, qs[128] @16 (dequant.rs:255-290)
 struct Q4K {
     static constexpr uint32_t BS = 256, BB = 144, UPB = 4, NX = 64, NAUX = 2;
     struct Raw { uint4 h, qa, qb; };
-    __device__ static void load_x(const float *__restrict__ x, uint32_t k, uint32_t j, float *xs, float *aux) {
-        const float4 *p = reinterpret_cast<const float4 *>(x + k * 256 + j * 64);
+    template <class X>
+    __device__ static void load_x(const X &x, uint32_t k, uint32_t j, float *xs, float *aux) {
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            float4 v = p[i];
+            float4 v = x(k * 256 + j * 64 + 4 * i);
             xs[4 * i] = v.x; xs[4 * i + 1] = v.y; xs[4 * i + 2] = v.z; xs[4 * i + 3] = v.w;
         }
         float s0 = 0.f, s1 = 0.f;
@@ -123,12 +136,13 @@ struct Q4K {
 struct Q6K {
     static constexpr uint32_t BS = 256, BB = 210, UPB = 8, NX = 32, NAUX = 4;
     struct Raw { uint32_t a[3], b[3], h[3], s[3], d; uint32_t ma; };
-    __device__ static void load_x(const float *__restrict__ x, uint32_t k, uint32_t u, float *xs, float *aux) {
+    template <class X>
+    __device__ static void load_x(const X &x, uint32_t k, uint32_t u, float *xs, float *aux) {
         const uint32_t h = u >> 2, p = u & 3u;
 #pragma unroll
         for (int g = 0; g < 4; g++) {
-            const float4 *q = reinterpret_cast<const float4 *>(x + k * 256 + h * 128 + g * 32 + p * 8);
-            float4 v0 = q[0], v1 = q[1];
+            const uint32_t o = k * 256 + h * 128 + g * 32 + p * 8;
+            float4 v0 = x(o), v1 = x(o + 4);
             xs[8 * g + 0] = v0.x; xs[8 * g + 1] = v0.y; xs[8 * g + 2] = v0.z; xs[8 * g + 3] = v0.w;
             xs[8 * g + 4] = v1.x; xs[8 * g + 5] = v1.y; xs[8 * g + 6] = v1.z; xs[8 * g + 7] = v1.w;
             float s = 0.f;
@@ -191,12 +205,12 @@ struct Q6K {
 struct Q80 {
     static constexpr uint32_t BS = 32, BB = 34, UPB = 1, NX = 32, NAUX = 1;
     struct Raw { uint32_t w[9]; uint32_t ma; };
-    __device__ static void load_x(const float *__restrict__ x, uint32_t k, uint32_t, float *xs, float *aux) {
-        const float4 *p = reinterpret_cast<const float4 *>(x + k * 32);
+    template <class X>
+    __device__ static void load_x(const X &x, uint32_t k, uint32_t, float *xs, float *aux) {
         float s = 0.f;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            float4 v = p[i];
+            float4 v = x(k * 32 + 4 * i);
             xs[4 * i] = v.x; xs[4 * i + 1] = v.y; xs[4 * i + 2] = v.z; xs[4 * i + 3] = v.w;
         }
 #pragma unroll
@@ -234,7 +248,8 @@ struct Q80 {
 struct Q40 {
     static constexpr uint32_t BS = 32, BB = 18, UPB = 1, NX = 32, NAUX = 1;
     struct Raw { uint32_t w[5]; uint32_t ma; };
-    __device__ static void load_x(const float *__restrict__ x, uint32_t k, uint32_t u, float *xs, float *aux) {
+    template <class X>
+    __device__ static void load_x(const X &x, uint32_t k, uint32_t u, float *xs, float *aux) {
         Q80::load_x(x, k, u, xs, aux);
     }
     __device__ static Raw load(const uint8_t *__restrict__ blk, uint32_t) {
@@ -288,7 +303,7 @@ __global__ __launch_bounds__(256) void qmv_kernel(const uint8_t *__restrict__ w,
         if (u < units) {
             const uint32_t k = u / F::UPB, sub = u % F::UPB;
             float xs[F::NX], aux[F::NAUX];
-            F::load_x(x, k, sub, xs, aux);
+            F::load_x(XGlobal{x}, k, sub, xs, aux);
             typename F::Raw raw[R];
 #pragma unroll
             for (int r = 0; r < R; r++) {
@@ -324,8 +339,6 @@ static void launch_one(hipStream_t s, const uint8_t *w, const float *x, float *y
 
 template <class F, int TEAM>
 static void launch_team(hipStream_t s, const uint8_t *w, const float *x, float *y, uint32_t n_rows, uint32_t bpr) {
-    // Rows per wave: as many as keep >= 2048 waves in flight (8 per SIMD on
-    // 256 CUs), so small matrices still spread over the whole chip.
     constexpr uint32_t slots = 64 / TEAM;
     if ((uint64_t)n_rows >= 2048ull * slots * 8) launch_one<F, TEAM, 8>(s, w, x, y, n_rows, bpr);
     else if ((uint64_t)n_rows >= 2048ull * slots * 4) launch_one<F, TEAM, 4>(s, w, x, y, n_rows, bpr);
@@ -333,8 +346,8 @@ static void launch_team(hipStream_t s, const uint8_t *w, const float *x, float *
     else launch_one<F, TEAM, 1>(s, w, x, y, n_rows, bpr);
 }
 
-// Team width: the one of 64/32/16 lanes that wastes the fewest lanes on the
-// row's last column step (ties go to the wider team: fewer steps).
+// Team width of the column-looping kernel: the one of 64/32/16 lanes that
+// wastes the fewest lanes on the row's last column step.
 static uint32_t pick_team(uint32_t units) {
     uint32_t best = 64;
     double best_eff = -1.0;
@@ -346,26 +359,229 @@ static uint32_t pick_team(uint32_t units) {
     return best;
 }
 
-template <class F>
-static void launch_fmt(hipStream_t s, const uint8_t *w, const float *x, float *y, uint32_t n_rows, uint32_t n_cols) {
-    const uint32_t bpr = n_cols / F::BS;
-    switch (pick_team(bpr * F::UPB)) {
-    case 64: launch_team<F, 64>(s, w, x, y, n_rows, bpr); break;
-    case 32: launch_team<F, 32>(s, w, x, y, n_rows, bpr); break;
-    default: launch_team<F, 16>(s, w, x, y, n_rows, bpr); break;
+// ---------------------------------------------------------------- streaming kernel
+// Rows stream through persistent workgroups.  A team of W lanes (16..256)
+// covers a whole row, one unit per lane, so each lane's activation slice is
+// loaded into registers once for the life of the workgroup; the team then
+// walks rows row0, row0 + stride, ... with the next row's blocks already in
+// flight while the current one is computed.  With several teams per
+// workgroup, x is staged once through LDS.  Teams wider than a wave combine
+// their per-wave sums through LDS.
+template <int W>
+__device__ __forceinline__ float team_sum(float v) {
+    // within rows of 16 lanes: xor 1, xor 2 (quad_perm), half-mirror, mirror
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+    if (W >= 32) v += __shfl_xor(v, 16, 64);
+    if (W >= 64) v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
+// Up to kMaxSegs matrices sharing one activation vector (same n_cols and
+// format) run as one launch over their concatenated rows: Q/K/V, gate/up.
+struct Segs {
+    const uint8_t *w[kMaxSegs];
+    float *y[kMaxSegs];
+    uint32_t start[kMaxSegs];   // first concatenated row of each segment (unused: = total)
+    uint32_t total;
+};
+
+template <class F, int W, bool STAGE, int D>
+__global__ __launch_bounds__(256) void qmv_stream_kernel(const Segs sg, const float *__restrict__ x, uint32_t bpr,
+                                                         uint32_t early) {
+    constexpr uint32_t RI = 256 / W;                  // rows per workgroup iteration
+    constexpr uint32_t WPT = W >= 64 ? W / 64 : 1;    // waves per team
+    extern __shared__ float xl[];
+    __shared__ float part[2][4];
+    const uint32_t tid = threadIdx.x, team = tid / W, t = tid % W;
+    const uint32_t units = bpr * F::UPB, n_rows = sg.total;
+    const size_t row_bytes = (size_t)bpr * F::BB;
+    const bool active = t < units;
+    const uint32_t k = active ? t / F::UPB : 0, sub = t % F::UPB;
+    const uint32_t stride = gridDim.x * RI;
+    const uint32_t r0 = blockIdx.x * RI;
+    if (r0 >= n_rows) return;   // uniform per workgroup
+
+    // concatenated row -> weight row pointer / output slot.  vbase[i] is
+    // segment i's weight base moved back by start[i] rows, so a row's
+    // address is vbase[seg] + row * row_bytes.  With whole-wave teams the
+    // row is wave-uniform and all of this runs on the scalar unit.
+    auto uni = [&](uint32_t v) { return W >= 64 ? __builtin_amdgcn_readfirstlane(v) : v; };
+    auto seg_of = [&](uint32_t row) {
+        uint32_t s = 0;
+#pragma unroll
+        for (int i = 1; i < kMaxSegs; i++) s += row >= sg.start[i];
+        return s;
+    };
+    auto fetch = [&](uint32_t rbase) {
+        uint32_t row = rbase + team;
+        row = uni(row < n_rows ? row : n_rows - 1);
+        const uint32_t s = seg_of(row);
+        const uint8_t *wb = sg.w[0] - (size_t)sg.start[0] * row_bytes;
+#pragma unroll
+        for (int i = 1; i < kMaxSegs; i++) wb = s == (uint32_t)i ? sg.w[i] - (size_t)sg.start[i] * row_bytes : wb;
+        return F::load(wb + (size_t)row * row_bytes + (size_t)k * F::BB, sub);
+    };
+    auto store = [&](uint32_t row, float v) {
+        row = uni(row);
+        const uint32_t s = seg_of(row);
+        float *yb = sg.y[0] - sg.start[0];
+#pragma unroll
+        for (int i = 1; i < kMaxSegs; i++) yb = s == (uint32_t)i ? sg.y[i] - sg.start[i] : yb;
+        yb[row] = v;
+    };
+
+    // With `early`, the first rows' weight loads go out before the
+    // activation vector is staged, so HBM latency overlaps the x load.
+    typename F::Raw buf[D];
+    if (early) {
+#pragma unroll
+        for (int j = 0; j < D - 1; j++)
+            if (r0 + j * stride < n_rows) buf[j] = fetch(r0 + j * stride);
     }
+    if (STAGE) {
+        const uint32_t n4 = bpr * F::BS / 4;
+        for (uint32_t i = tid; i < n4; i += 256)
+            *reinterpret_cast<float4 *>(xl + lds_pad(4 * i)) = reinterpret_cast<const float4 *>(x)[i];
+        __syncthreads();
+    }
+    float xs[F::NX], aux[F::NAUX];
+    if (STAGE) F::load_x(XLds{xl}, k, sub, xs, aux);
+    else F::load_x(XGlobal{x}, k, sub, xs, aux);
+    if (!early) {
+#pragma unroll
+        for (int j = 0; j < D - 1; j++)
+            if (r0 + j * stride < n_rows) buf[j] = fetch(r0 + j * stride);
+    }
+
+    auto finish = [&](float acc, uint32_t rbase, uint32_t it) {
+        const uint32_t row = rbase + team;
+        acc = team_sum<(W < 64 ? W : 64)>(active ? acc : 0.f);
+        if (WPT == 1) {
+            if (t == 0 && row < n_rows) store(row, acc);
+        } else {
+            const uint32_t wave = tid >> 6;
+            if ((tid & 63) == 0) part[it & 1][wave] = acc;
+            __syncthreads();
+            if (t == 0 && row < n_rows) {
+                float s = 0.f;
+#pragma unroll
+                for (uint32_t i = 0; i < WPT; i++) s += part[it & 1][wave + i];
+                store(row, s);
+            }
+        }
+    };
+    // D-deep ring of row buffers: before computing row r, the load of row
+    // r + (D-1)*stride is issued into the slot the previous row freed.
+    uint32_t it = 0;
+    for (uint32_t base = r0; base < n_rows; base += D * stride) {
+#pragma unroll
+        for (int j = 0; j < D; j++) {
+            const uint32_t r = base + j * stride;
+            if (r >= n_rows) break;
+            const uint32_t rn = r + (D - 1) * stride;
+            if (rn < n_rows) buf[(j + D - 1) % D] = fetch(rn);
+            finish(F::dot(buf[j], sub, xs, aux), r, it++);
+        }
+    }
+}
+
+static int g_cus = 0;
+static int device_cus() {
+    if (!g_cus) {
+        int dev = 0, n = 0;
+        (void)hipGetDevice(&dev);
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        g_cus = n;
+    }
+    return g_cus;
+}
+
+static int env_int(const char *name, int dflt) {
+    const char *e = getenv(name);
+    const int v = e ? atoi(e) : dflt;
+    return v > 0 ? v : dflt;
+}
+
+template <class F, int W, int D>
+static void launch_stream_d(hipStream_t s, const Segs &sg, const float *x, uint32_t bpr, uint32_t blocks) {
+    static const uint32_t early = (uint32_t)env_int("YULE_QMV_EARLY", 1) - 1;
+    constexpr uint32_t RI = 256 / W;
+    if constexpr (RI >= 2) {
+        const size_t lds = (size_t)lds_pad(bpr * F::BS) * sizeof(float);
+        hipLaunchKernelGGL((qmv_stream_kernel<F, W, true, D>), dim3(blocks), dim3(256), lds, s, sg, x, bpr, early);
+    } else {
+        hipLaunchKernelGGL((qmv_stream_kernel<F, W, false, D>), dim3(blocks), dim3(256), 0, s, sg, x, bpr, early);
+    }
+}
+
+template <class F, int W>
+static void launch_stream(hipStream_t s, const Segs &sg, const float *x, uint32_t bpr) {
+    constexpr uint32_t RI = 256 / W;
+    static const int wg = env_int("YULE_QMV_WG_PER_CU", 4), depth = env_int("YULE_QMV_DEPTH", 2);
+    const uint32_t iters = (sg.total + RI - 1) / RI;
+    const uint32_t cap = (uint32_t)(device_cus() * wg);
+    const uint32_t blocks = iters < cap ? iters : cap;
+    switch (depth) {
+    case 1: return launch_stream_d<F, W, 1>(s, sg, x, bpr, blocks);
+    case 3: return launch_stream_d<F, W, 3>(s, sg, x, bpr, blocks);
+    case 4: return launch_stream_d<F, W, 4>(s, sg, x, bpr, blocks);
+    default: return launch_stream_d<F, W, 2>(s, sg, x, bpr, blocks);
+    }
+}
+
+// Largest activation vector staged in LDS by the streaming kernel (floats).
+constexpr uint32_t kMaxStageCols = 32768;
+
+template <class F>
+static void launch_fmt(hipStream_t s, const QmvSeg *segs, uint32_t n_seg, const float *x, uint32_t n_cols) {
+    const uint32_t bpr = n_cols / F::BS, units = bpr * F::UPB;
+    static const bool v1 = getenv("YULE_QMV_V1") != nullptr;
+    if (!v1 && units <= 256 && n_cols <= kMaxStageCols) {
+        Segs sg{};
+        uint32_t total = 0;
+        for (uint32_t i = 0; i < kMaxSegs; i++) {
+            sg.w[i] = segs[i < n_seg ? i : 0].w;
+            sg.y[i] = segs[i < n_seg ? i : 0].y;
+            sg.start[i] = total;
+            if (i < n_seg) total += segs[i].n_rows;
+        }
+        for (uint32_t i = n_seg; i < kMaxSegs; i++) sg.start[i] = total;
+        sg.total = total;
+        if (units <= 16) return launch_stream<F, 16>(s, sg, x, bpr);
+        if (units <= 32) return launch_stream<F, 32>(s, sg, x, bpr);
+        if (units <= 64) return launch_stream<F, 64>(s, sg, x, bpr);
+        if (units <= 128) return launch_stream<F, 128>(s, sg, x, bpr);
+        return launch_stream<F, 256>(s, sg, x, bpr);
+    }
+    for (uint32_t i = 0; i < n_seg; i++) {   // one column-looping launch per matrix
+        switch (pick_team(units)) {
+        case 64: launch_team<F, 64>(s, segs[i].w, x, segs[i].y, segs[i].n_rows, bpr); break;
+        case 32: launch_team<F, 32>(s, segs[i].w, x, segs[i].y, segs[i].n_rows, bpr); break;
+        default: launch_team<F, 16>(s, segs[i].w, x, segs[i].y, segs[i].n_rows, bpr); break;
+        }
+    }
+}
+
+int launch_qmv_multi(hipStream_t s, uint32_t dtype, const QmvSeg *segs, uint32_t n_seg, const float *x,
+                     uint32_t n_cols) {
+    if (n_seg == 0 || n_seg > kMaxSegs) return set_error(YULE_ERR_INVALID, "quantized_matmul: bad segment count");
+    switch (dtype) {
+    case YULE_DTYPE_Q4_K: launch_fmt<Q4K>(s, segs, n_seg, x, n_cols); break;
+    case YULE_DTYPE_Q6_K: launch_fmt<Q6K>(s, segs, n_seg, x, n_cols); break;
+    case YULE_DTYPE_Q8_0: launch_fmt<Q80>(s, segs, n_seg, x, n_cols); break;
+    case YULE_DTYPE_Q4_0: launch_fmt<Q40>(s, segs, n_seg, x, n_cols); break;
+    default: return set_error(YULE_ERR_UNSUPPORTED, "quantized_matmul: unsupported dtype");
+    }
+    return check_launch("quantized_matmul");
 }
 
 int launch_qmv(hipStream_t s, uint32_t dtype, const uint8_t *w, const float *x, float *y, uint32_t n_rows,
                uint32_t n_cols) {
-    switch (dtype) {
-    case YULE_DTYPE_Q4_K: launch_fmt<Q4K>(s, w, x, y, n_rows, n_cols); break;
-    case YULE_DTYPE_Q6_K: launch_fmt<Q6K>(s, w, x, y, n_rows, n_cols); break;
-    case YULE_DTYPE_Q8_0: launch_fmt<Q80>(s, w, x, y, n_rows, n_cols); break;
-    case YULE_DTYPE_Q4_0: launch_fmt<Q40>(s, w, x, y, n_rows, n_cols); break;
-    default: return set_error(YULE_ERR_UNSUPPORTED, "quantized_matmul: unsupported dtype");
-    }
-    return check_launch("quantized_matmul");
+    const QmvSeg seg{w, y, n_rows};
+    return launch_qmv_multi(s, dtype, &seg, 1, x, n_cols);
 }
 
 // ---------------------------------------------------------------- dequant

@@ -257,6 +257,27 @@ static int check_qmv_args(yule_hip_backend *be, yule_buffer weights, yule_buffer
     return YULE_OK;
 }
 
+// Validate a multi-matrix call: every matrix checked like quantized_matmul,
+// and no output may alias the input or another output.
+static int prepare_multi(yule_hip_backend *be, uint32_t n_mats, const yule_buffer *weights, const yule_buffer *outputs,
+                         const uint32_t *n_rows, yule_buffer input, uint32_t n_cols, uint32_t dtype, const char *what,
+                         QmvSeg *segs, const float **x) {
+    if (n_mats == 0 || n_mats > (uint32_t)kMaxSegs || !weights || !outputs || !n_rows)
+        return set_error(YULE_ERR_INVALID, std::string(what) + ": n_mats must be 1..4 with non-null arrays");
+    for (uint32_t i = 0; i < n_mats; i++) {
+        for (uint32_t j = 0; j < i; j++)
+            if (outputs[i] == outputs[j]) return set_error(YULE_ERR_INVALID, std::string(what) + ": outputs alias");
+        bool empty;
+        float *y;
+        int rc = check_qmv_args(be, weights[i], input, outputs[i], n_rows[i], n_cols, dtype, what, &segs[i].w, x, &y,
+                                &empty);
+        if (rc) return rc;
+        segs[i].y = y;
+        segs[i].n_rows = n_rows[i];
+    }
+    return YULE_OK;
+}
+
 int yule_hip_quantized_matmul(yule_hip_backend *be, yule_buffer weights, yule_buffer input, yule_buffer output,
                               uint32_t n_rows, uint32_t n_cols, uint32_t dtype) {
     YULE_CHECK_BE(be);
@@ -266,6 +287,27 @@ int yule_hip_quantized_matmul(yule_hip_backend *be, yule_buffer weights, yule_bu
     if (n_rows == 0) return YULE_OK;
     if (empty) return launch_fill(be->stream, y, 0.0f, n_rows);  // zero blocks per row -> y = 0
     return launch_qmv(be->stream, dtype, w, x, y, n_rows, n_cols);
+}
+
+int yule_hip_quantized_matmul_multi(yule_hip_backend *be, uint32_t n_mats, const yule_buffer *weights,
+                                    const yule_buffer *outputs, const uint32_t *n_rows, yule_buffer input,
+                                    uint32_t n_cols, uint32_t dtype) {
+    YULE_CHECK_BE(be);
+    QmvSeg segs[kMaxSegs];
+    const float *x = nullptr;
+    int rc = prepare_multi(be, n_mats, weights, outputs, n_rows, input, n_cols, dtype, "quantized_matmul_multi", segs,
+                           &x);
+    if (rc) return rc;
+    uint32_t n = 0;
+    for (uint32_t i = 0; i < n_mats; i++)
+        if (segs[i].n_rows) segs[n++] = segs[i];
+    if (n == 0) return YULE_OK;
+    if (n_cols == 0) {
+        for (uint32_t i = 0; i < n; i++)
+            if ((rc = launch_fill(be->stream, segs[i].y, 0.0f, segs[i].n_rows))) return rc;
+        return YULE_OK;
+    }
+    return launch_qmv_multi(be->stream, dtype, segs, n, x, n_cols);
 }
 
 int yule_hip_dequantize(yule_hip_backend *be, yule_buffer src, size_t src_offset, yule_buffer dst,
@@ -286,19 +328,20 @@ int yule_hip_time_qmv_ops(yule_hip_backend *be, const yule_qmv_op *ops, uint32_t
     YULE_CHECK_BE(be);
     if (!ops || !ms_total || n_ops == 0 || iters == 0)
         return set_error(YULE_ERR_INVALID, "time_qmv_ops: bad arguments");
-    struct Launch { uint32_t dtype, n_rows, n_cols; const uint8_t *w; const float *x; float *y; };
+    struct Launch { uint32_t dtype, n_cols, n; QmvSeg segs[kMaxSegs]; const float *x; };
     std::vector<Launch> L(n_ops);
     for (uint32_t i = 0; i < n_ops; i++) {
-        bool empty;
-        int rc = check_qmv_args(be, ops[i].weights, ops[i].input, ops[i].output, ops[i].n_rows, ops[i].n_cols,
-                                ops[i].dtype, "time_qmv_ops", &L[i].w, &L[i].x, &L[i].y, &empty);
+        int rc = prepare_multi(be, ops[i].n_mats, ops[i].weights, ops[i].outputs, ops[i].n_rows, ops[i].input,
+                               ops[i].n_cols, ops[i].dtype, "time_qmv_ops", L[i].segs, &L[i].x);
         if (rc) return rc;
-        if (empty || ops[i].n_rows == 0) return set_error(YULE_ERR_INVALID, "time_qmv_ops: empty matrix");
-        L[i].dtype = ops[i].dtype; L[i].n_rows = ops[i].n_rows; L[i].n_cols = ops[i].n_cols;
+        if (ops[i].n_cols == 0) return set_error(YULE_ERR_INVALID, "time_qmv_ops: empty matrix");
+        for (uint32_t j = 0; j < ops[i].n_mats; j++)
+            if (!ops[i].n_rows[j]) return set_error(YULE_ERR_INVALID, "time_qmv_ops: empty matrix");
+        L[i].dtype = ops[i].dtype; L[i].n_cols = ops[i].n_cols; L[i].n = ops[i].n_mats;
     }
     auto enqueue = [&]() -> int {
         for (const Launch &l : L) {
-            int rc = launch_qmv(be->stream, l.dtype, l.w, l.x, l.y, l.n_rows, l.n_cols);
+            int rc = launch_qmv_multi(be->stream, l.dtype, l.segs, l.n, l.x, l.n_cols);
             if (rc) return rc;
         }
         return YULE_OK;
