@@ -151,6 +151,43 @@ def cpu_baseline(layer, budget_s=12.0, max_passes=2000):
             "host_cpu": _cpu_model()}
 
 
+def decode_e2e(hip, cpu: bool):
+    """TinyLlama-shaped Q4_K_M greedy decode, 128-token
+    prompt then 256 decode steps, tok/s = 1000 / mean decode-step ms
+    (yule-validate/src/performance.rs:303-337)."""
+    from yule_amd.backend import HipRunner
+    from yule_amd.model import TINYLLAMA, SyntheticModel
+    t0 = time.time()
+    model = SyntheticModel.generate(TINYLLAMA, seed=0)
+    log(f"TinyLlama-shaped model: {model.weight_bytes / 1e6:.0f} MB ({time.time() - t0:.1f}s)")
+    prompt = synth.uniform_tokens(1, 128, TINYLLAMA.vocab)
+    run = HipRunner(hip, model)
+    run.generate_greedy(prompt, 16)                       # warm-up (graph capture)
+    toks, ms = run.generate_greedy(prompt, 256)
+    run.close()
+    res = {"decode_tok_s": round(1000.0 / ms, 1), "decode_ms_per_step": round(ms, 4),
+           "decode_weight_bytes_per_step": model.bytes_per_token(),
+           "decode_effective_GB/s": round(model.bytes_per_token() / (ms * 1e-3) / 1e9, 1)}
+    golden = ROOT / "tests" / "golden" / "e2e_tinyllama_greedy.json"
+    if golden.exists():
+        res["decode_tokens_match_oracle"] = [int(t) for t in toks] == json.loads(golden.read_text())["tokens"]
+    if cpu:
+        import oracle
+        threads = min(16, os.cpu_count() or 1)
+        r = oracle.Runner(model, n_threads=threads)
+        r.forward(int(prompt[0]))
+        n, t0 = 0, time.perf_counter()
+        while n < 4 or (n < 48 and time.perf_counter() - t0 < 12.0):
+            r.forward(int(prompt[(n + 1) % 128]))
+            n += 1
+        cms = 1e3 * (time.perf_counter() - t0) / n
+        res["cpu_decode"] = {"tok_s": round(1000.0 / cms, 2), "threads": threads, "kind": "port",
+                             "sample": f"{n} forward steps at positions 1..{n} of the same model through the "
+                                       f"oracle's restatement of Yule's CPU TransformerRunner"}
+        res["decode_speedup_vs_cpu"] = round(cms / ms, 1)
+    return res
+
+
 def _cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
@@ -228,6 +265,11 @@ def main():
     if cpu:
         log(f"CPU baseline: {cpu['value']} GB/s on {cpu['cores']} threads ({cpu['host_cpu']})")
     q4k.free()
+
+    e2e = decode_e2e(hip, cpu=not args.no_cpu)
+    log(f"TinyLlama Q4_K_M decode: {e2e['decode_tok_s']} tok/s ({e2e['decode_ms_per_step']} ms/step)"
+        + (f", CPU {e2e['cpu_decode']['tok_s']} tok/s" if "cpu_decode" in e2e else ""))
+    extra.update(e2e)
 
     if not args.quick:
         for dt in (DType.Q6_K, DType.Q8_0):

@@ -175,6 +175,65 @@ int yule_hip_quantized_gemm(yule_hip_backend *be, yule_buffer weights, yule_buff
                             yule_buffer y, uint32_t m, uint32_t n_rows, uint32_t n_cols,
                             uint32_t dtype);
 
+/* ---- decode runner (yule-infer GpuTransformerRunner counterpart) ---- */
+
+/* One transformer layer's tensors as host pointers to raw GGUF data
+ * (weight_loader.rs:158-199 names: blk.N.attn_norm, attn_q, attn_k, attn_v,
+ * attn_output, ffn_norm, ffn_gate, ffn_up, ffn_down).  Matrices are
+ * [rows][cols] blocks of a quantized dtype; norms are F32 or F16. */
+typedef struct {
+    const void *attn_norm;
+    uint32_t attn_norm_dtype;
+    const void *wq, *wk, *wv, *wo;
+    uint32_t wq_dtype, wk_dtype, wv_dtype, wo_dtype;
+    const void *ffn_norm;
+    uint32_t ffn_norm_dtype;
+    const void *w_gate, *w_up, *w_down;
+    uint32_t w_gate_dtype, w_up_dtype, w_down_dtype;
+} yule_layer_desc;
+
+/* Dense Llama-family model (RunnerConfig, model_runner.rs:384-465):
+ * head_dim = dim / n_heads, RoPE over the full head dimension, SwiGLU FFN. */
+typedef struct {
+    uint32_t n_layers, dim, n_heads, n_kv_heads, ff_dim, vocab, max_seq;
+    float norm_eps, rope_base;
+    const void *token_embd;
+    uint32_t token_embd_dtype;
+    const void *output_norm;
+    uint32_t output_norm_dtype;
+    const void *output;
+    uint32_t output_dtype;
+    const yule_layer_desc *layers; /* n_layers entries */
+} yule_model_desc;
+
+typedef struct yule_hip_runner yule_hip_runner;
+
+/* TransformerRunner::new (model_runner.rs:384-531): uploads every tensor
+ * once (gpu_runner.rs:171-254), allocates the f32 KV cache
+ * [n_layers][max_seq][n_kv_heads*head_dim] and the RoPE table.  The host
+ * tensors may be released after the call. */
+int yule_hip_runner_create(yule_hip_backend *be, const yule_model_desc *model, yule_hip_runner **out);
+int yule_hip_runner_destroy(yule_hip_runner *r);
+/* ModelRunner::reset (model_runner.rs:1087-1092): position back to 0. */
+int yule_hip_runner_reset(yule_hip_runner *r);
+uint32_t yule_hip_runner_pos(const yule_hip_runner *r);
+/* ModelRunner::decode_step (model_runner.rs:1083-1085): forward one token
+ * at the current position; logits (f32[vocab]) copied out when non-null.
+ * Fails with "context length exceeded" at pos == max_seq (:538-540). */
+int yule_hip_runner_decode_step(yule_hip_runner *r, uint32_t token, float *logits);
+/* ModelRunner::prefill (model_runner.rs:1075-1081): token by token; logits
+ * of the last token when non-null. */
+int yule_hip_runner_prefill(yule_hip_runner *r, const uint32_t *tokens, uint32_t n, float *logits);
+/* Greedy generation from position 0 entirely on the device: n_prompt
+ * prompt tokens, then n_decode decode steps fed by argmax_ct
+ * (sampler.rs:150-163).  out_tokens receives n_decode + 1 ids: the argmax
+ * after the last prompt token and after each decode step.  When non-null,
+ * ms_per_decode_step is the mean of the decode steps, from HIP events on
+ * the backend stream (the yule-validate/src/performance.rs:303-337
+ * tokens/s method: 1000 / ms). */
+int yule_hip_runner_generate_greedy(yule_hip_runner *r, const uint32_t *prompt, uint32_t n_prompt,
+                                    uint32_t n_decode, uint32_t *out_tokens, float *ms_per_decode_step);
+
 /* ---- timing helpers for harnesses (no trait counterpart) ---- */
 
 /* One quantized_matmul (n_mats == 1) or quantized_matmul_multi call, for

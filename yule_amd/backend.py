@@ -54,6 +54,14 @@ _SIGS: dict[str, tuple] = {
     "yule_hip_gqa_decode_attn": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint64] + [C.c_uint32] * 4),
     "yule_hip_argmax": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint32, C.c_uint64]),
     "yule_hip_quantized_gemm": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint64] + [C.c_uint32] * 4),
+    "yule_hip_runner_create": (C.c_int, [C.c_void_p, C.c_void_p, C.POINTER(C.c_void_p)]),
+    "yule_hip_runner_destroy": (C.c_int, [C.c_void_p]),
+    "yule_hip_runner_reset": (C.c_int, [C.c_void_p]),
+    "yule_hip_runner_pos": (C.c_uint32, [C.c_void_p]),
+    "yule_hip_runner_decode_step": (C.c_int, [C.c_void_p, C.c_uint32, C.c_void_p]),
+    "yule_hip_runner_prefill": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p]),
+    "yule_hip_runner_generate_greedy": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p,
+                                                  C.POINTER(C.c_float)]),
     "yule_hip_time_qmv_ops": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_int,
                                         C.POINTER(C.c_float)]),
 }
@@ -281,3 +289,94 @@ class HipBackend:
 
     def download(self, handle, shape, dtype=np.float32) -> np.ndarray:
         return self.copy_from_device(handle, np.empty(shape, dtype=dtype))
+
+
+class _LayerDesc(C.Structure):
+    _fields_ = [("attn_norm", C.c_void_p), ("attn_norm_dtype", C.c_uint32),
+                ("wq", C.c_void_p), ("wk", C.c_void_p), ("wv", C.c_void_p), ("wo", C.c_void_p),
+                ("wq_dtype", C.c_uint32), ("wk_dtype", C.c_uint32), ("wv_dtype", C.c_uint32), ("wo_dtype", C.c_uint32),
+                ("ffn_norm", C.c_void_p), ("ffn_norm_dtype", C.c_uint32),
+                ("w_gate", C.c_void_p), ("w_up", C.c_void_p), ("w_down", C.c_void_p),
+                ("w_gate_dtype", C.c_uint32), ("w_up_dtype", C.c_uint32), ("w_down_dtype", C.c_uint32)]
+
+
+class _ModelDesc(C.Structure):
+    _fields_ = [("n_layers", C.c_uint32), ("dim", C.c_uint32), ("n_heads", C.c_uint32), ("n_kv_heads", C.c_uint32),
+                ("ff_dim", C.c_uint32), ("vocab", C.c_uint32), ("max_seq", C.c_uint32), ("norm_eps", C.c_float),
+                ("rope_base", C.c_float), ("token_embd", C.c_void_p), ("token_embd_dtype", C.c_uint32),
+                ("output_norm", C.c_void_p), ("output_norm_dtype", C.c_uint32), ("output", C.c_void_p),
+                ("output_dtype", C.c_uint32), ("layers", C.POINTER(_LayerDesc))]
+
+
+class HipRunner:
+    """GpuTransformerRunner counterpart over yule_hip_runner_*: ModelRunner's
+    prefill / decode_step / reset (yule-infer/src/model_runner.rs:12-17)
+    plus a device-resident greedy loop."""
+
+    def __init__(self, backend: HipBackend, model):
+        self._be = backend
+        self._lib = backend._lib
+        cfg = model.cfg
+        keep = []
+
+        def ptr(t):
+            a = np.ascontiguousarray(t.data)
+            keep.append(a)
+            return a.ctypes.data
+
+        layers = (_LayerDesc * cfg.n_layers)()
+        for i in range(cfg.n_layers):
+            t = model.layer(i)
+            L = layers[i]
+            L.attn_norm, L.attn_norm_dtype = ptr(t["attn_norm"]), int(t["attn_norm"].dtype)
+            L.ffn_norm, L.ffn_norm_dtype = ptr(t["ffn_norm"]), int(t["ffn_norm"].dtype)
+            for fld, key in (("wq", "attn_q"), ("wk", "attn_k"), ("wv", "attn_v"), ("wo", "attn_output"),
+                             ("w_gate", "ffn_gate"), ("w_up", "ffn_up"), ("w_down", "ffn_down")):
+                setattr(L, fld, ptr(t[key]))
+                setattr(L, fld + "_dtype", int(t[key].dtype))
+        e, on, o = model["token_embd.weight"], model["output_norm.weight"], model["output.weight"]
+        desc = _ModelDesc(cfg.n_layers, cfg.dim, cfg.n_heads, cfg.n_kv_heads, cfg.ff_dim, cfg.vocab, cfg.max_seq,
+                          cfg.norm_eps, cfg.rope_base, ptr(e), int(e.dtype), ptr(on), int(on.dtype), ptr(o),
+                          int(o.dtype), layers)
+        r = C.c_void_p()
+        backend._check(self._lib.yule_hip_runner_create(backend.raw, C.byref(desc), C.byref(r)))
+        self._r = r
+        self.vocab = cfg.vocab
+
+    def close(self):
+        if getattr(self, "_r", None):
+            self._lib.yule_hip_runner_destroy(self._r)
+            self._r = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def reset(self) -> None:
+        self._be._check(self._lib.yule_hip_runner_reset(self._r))
+
+    @property
+    def pos(self) -> int:
+        return int(self._lib.yule_hip_runner_pos(self._r))
+
+    def decode_step(self, token: int) -> np.ndarray:
+        out = np.empty(self.vocab, np.float32)
+        self._be._check(self._lib.yule_hip_runner_decode_step(self._r, token, out.ctypes.data))
+        return out
+
+    def prefill(self, tokens) -> np.ndarray:
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        out = np.empty(self.vocab, np.float32)
+        self._be._check(self._lib.yule_hip_runner_prefill(self._r, t.ctypes.data, t.size, out.ctypes.data))
+        return out
+
+    def generate_greedy(self, prompt, n_decode: int):
+        """-> (tokens[n_decode + 1], ms per decode step)"""
+        p = np.ascontiguousarray(prompt, dtype=np.uint32)
+        out = np.empty(n_decode + 1, np.uint32)
+        ms = C.c_float()
+        self._be._check(self._lib.yule_hip_runner_generate_greedy(self._r, p.ctypes.data, p.size, n_decode,
+                                                                  out.ctypes.data, C.byref(ms)))
+        return out, ms.value

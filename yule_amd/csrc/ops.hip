@@ -5,6 +5,7 @@
 // reductions run as trees instead of the reference's sequential loops.
 #include <string>
 
+#include "blocks.h"
 #include "internal.h"
 
 namespace yule {
@@ -429,3 +430,112 @@ int yule_hip_argmax(yule_hip_backend *be, yule_buffer in, uint32_t n, yule_buffe
 }
 
 }  // extern "C"
+
+// ------------------------------------------------------------ runner kernels
+namespace yule {
+
+// Device control block of the decode runner: ctl[0] = position, ctl[1] =
+// next input token (written by argmax_advance), ctl[2] = prompt length.
+// Token of this step: prompt[pos] while pos < prompt length, else ctl[1].
+__device__ __forceinline__ uint32_t step_token(const uint32_t *ctl, const uint32_t *prompt) {
+    const uint32_t p = ctl[0];
+    return p < ctl[2] ? prompt[p] : ctl[1];
+}
+
+__global__ void embed_step_kernel(uint32_t dtype, uint32_t bs, uint32_t bb, const uint8_t *__restrict__ table,
+                                  const uint32_t *__restrict__ ctl, const uint32_t *__restrict__ prompt,
+                                  uint32_t vocab, float *__restrict__ dst, uint32_t dim) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= dim) return;
+    uint32_t t = step_token(ctl, prompt);
+    t = t < vocab ? t : vocab - 1;   // host-checked tokens are in range; clamp keeps reads inside the table
+    const uint8_t *row = table + (size_t)t * (dim / bs) * bb;
+    dst[i] = dequant_one(dtype, row + (i / bs) * bb, i % bs);
+}
+
+int launch_embed_step(hipStream_t s, uint32_t dtype, const uint8_t *table, const uint32_t *ctl, const uint32_t *prompt,
+                      uint32_t vocab, float *dst, uint32_t dim) {
+    uint32_t bs, bb;
+    if (!quant_geometry(dtype, &bs, &bb)) return set_error(YULE_ERR_UNSUPPORTED, "embedding: unsupported dtype");
+    hipLaunchKernelGGL(embed_step_kernel, dim3((dim + 255) / 256), dim3(256), 0, s, dtype, bs, bb, table, ctl, prompt,
+                       vocab, dst, dim);
+    return check_launch("embedding");
+}
+
+// RoPE of q (in place) and k with the precomputed table row of the current
+// position (model_runner.rs:277-293), then k and v written into the layer's
+// cache row (model_runner.rs:665-669).
+__global__ void rope_kv_kernel(float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
+                               float *__restrict__ kc, float *__restrict__ vc, const float *__restrict__ cos_t,
+                               const float *__restrict__ sin_t, const uint32_t *__restrict__ ctl, uint32_t nq,
+                               uint32_t nk, uint32_t hd) {
+    const uint32_t half = hd / 2, kvd = nk * hd;
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t pos = ctl[0];
+    const uint32_t nqp = nq * half, nkp = nk * half;
+    if (i < nqp + nkp) {
+        const uint32_t head = i / half, p = i % half;
+        const float c = cos_t[(size_t)pos * half + p], sn = sin_t[(size_t)pos * half + p];
+        if (head < nq) {
+            float *h = q + head * hd;
+            const float x0 = h[2 * p], x1 = h[2 * p + 1];
+            h[2 * p] = x0 * c - x1 * sn;
+            h[2 * p + 1] = x0 * sn + x1 * c;
+        } else {
+            const uint32_t kh = head - nq;
+            const float x0 = k[kh * hd + 2 * p], x1 = k[kh * hd + 2 * p + 1];
+            float *dst = kc + (size_t)pos * kvd + kh * hd;
+            dst[2 * p] = x0 * c - x1 * sn;
+            dst[2 * p + 1] = x0 * sn + x1 * c;
+        }
+    } else if (i < nqp + nkp + kvd) {
+        const uint32_t j = i - nqp - nkp;
+        vc[(size_t)pos * kvd + j] = v[j];
+    }
+}
+
+int launch_rope_kv(hipStream_t s, float *q, const float *k, const float *v, float *kc, float *vc, const float *cos_t,
+                   const float *sin_t, const uint32_t *ctl, uint32_t nq, uint32_t nk, uint32_t hd) {
+    const uint32_t total = (nq + nk) * (hd / 2) + nk * hd;
+    hipLaunchKernelGGL(rope_kv_kernel, dim3((total + 255) / 256), dim3(256), 0, s, q, k, v, kc, vc, cos_t, sin_t, ctl,
+                       nq, nk, hd);
+    return check_launch("rope_kv");
+}
+
+// argmax_ct over the logits (last maximal index wins), then advance the
+// control block: the winner becomes the next input token, is recorded at
+// out_tokens[pos], and the position moves on.
+__global__ __launch_bounds__(1024) void argmax_advance_kernel(const float *__restrict__ in, uint32_t n,
+                                                              uint32_t *__restrict__ ctl,
+                                                              uint32_t *__restrict__ out_tokens) {
+    __shared__ float rv[16];
+    __shared__ uint32_t ri[16];
+    float bv = -INFINITY;
+    uint32_t bi = 0;
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x)
+        if (better(in[i], i, bv, bi)) { bv = in[i]; bi = i; }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float ov = __shfl_xor(bv, off, 64);
+        const uint32_t oi = __shfl_xor(bi, off, 64);
+        if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+    }
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    if (lane == 0) { rv[w] = bv; ri[w] = bi; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int k = 1; k < (int)(blockDim.x >> 6); k++)
+            if (better(rv[k], ri[k], bv, bi)) { bv = rv[k]; bi = ri[k]; }
+        const uint32_t pos = ctl[0];
+        ctl[1] = bi;
+        out_tokens[pos] = bi;
+        ctl[0] = pos + 1;
+    }
+}
+
+int launch_argmax_advance(hipStream_t s, const float *logits, uint32_t n, uint32_t *ctl, uint32_t *out_tokens) {
+    hipLaunchKernelGGL(argmax_advance_kernel, dim3(1), dim3(1024), 0, s, logits, n, ctl, out_tokens);
+    return check_launch("argmax_advance");
+}
+
+}  // namespace yule

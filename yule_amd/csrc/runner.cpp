@@ -1,0 +1,332 @@
+// runner.cpp — decode runner over the HIP backend: the counterpart of
+// yule-infer's GpuTransformerRunner (yule-infer/src/gpu_runner.rs:171-695)
+// with the CPU TransformerRunner's forward-pass semantics
+// (yule-infer/src/model_runner.rs:533-1036; dense Llama branch).
+//
+// Device-resident decode: weights are uploaded once as raw GGUF blocks;
+// embedding lookup, every projection, RoPE, the KV-cache write, attention,
+// SwiGLU, the residual adds, the final norm, the lm_head and the greedy
+// argmax all run on the GPU.  The step reads its position and input token
+// from a device control block (ctl = {pos, token, prompt_len}), so one HIP
+// graph captured once replays every step, prefill and decode alike; the
+// argmax kernel writes the next token and advances the position.
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "internal.h"
+
+using namespace yule;
+
+struct yule_hip_runner {
+    yule_hip_backend *be = nullptr;
+    uint32_t n_layers = 0, dim = 0, n_heads = 0, n_kv = 0, hd = 0, ff = 0, vocab = 0, max_seq = 0;
+    float eps = 1e-5f, rope_base = 10000.f;
+    std::vector<void *> allocs;
+    struct Layer {
+        float *attn_norm, *ffn_norm;
+        const uint8_t *wq, *wk, *wv, *wo, *wg, *wu, *wd;
+        uint32_t tq, tk, tv, to, tg, tu, td;
+        float *kc, *vc;
+    };
+    std::vector<Layer> layers;
+    const uint8_t *embd = nullptr, *out_w = nullptr;
+    uint32_t embd_t = 0, out_t = 0;
+    float *out_norm = nullptr, *cos_t = nullptr, *sin_t = nullptr;
+    float *hidden, *normed, *q, *k, *v, *attn, *proj, *gate, *up, *ffn, *logits;
+    uint32_t *ctl = nullptr, *prompt = nullptr, *tokens = nullptr;
+    uint32_t *ctl_host = nullptr;  // pinned staging for ctl updates
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    uint32_t pos = 0;  // host mirror of ctl[0]
+};
+
+namespace {
+
+int dev_alloc(yule_hip_runner *r, size_t bytes, void **p) {
+    int rc = hip_error(hipMalloc(p, bytes + kAllocSlack), "runner: allocate");
+    if (rc) return rc;
+    r->allocs.push_back(*p);
+    return hip_error(hipMemset(*p, 0, bytes + kAllocSlack), "runner: zero-fill");
+}
+
+int upload(yule_hip_runner *r, const void *src, size_t bytes, void **dst) {
+    int rc = dev_alloc(r, bytes, dst);
+    if (rc) return rc;
+    return hip_error(hipMemcpy(*dst, src, bytes, hipMemcpyHostToDevice), "runner: upload");
+}
+
+// f32 copy of a norm weight given as F32 or F16 (f16_to_f32 is exact;
+// model_runner.rs:257-271 reads either)
+int upload_norm(yule_hip_runner *r, const void *src, uint32_t dtype, uint32_t n, float **dst) {
+    if (!src) return set_error(YULE_ERR_INVALID, "runner: missing norm weight");
+    std::vector<float> tmp(n);
+    if (dtype == YULE_DTYPE_F32) {
+        std::memcpy(tmp.data(), src, (size_t)n * 4);
+    } else if (dtype == YULE_DTYPE_F16) {
+        const uint16_t *h = static_cast<const uint16_t *>(src);
+        for (uint32_t i = 0; i < n; i++) {
+            const uint32_t s = (h[i] >> 15) & 1u, e = (h[i] >> 10) & 0x1Fu, m = h[i] & 0x3FFu;
+            uint32_t bits;
+            if (e == 0) {
+                if (m == 0) bits = s << 31;
+                else {
+                    uint32_t mm = m;
+                    int ee = -14;
+                    while (!(mm & 0x400u)) { mm <<= 1; ee--; }
+                    bits = (s << 31) | ((uint32_t)(ee + 127) << 23) | ((mm & 0x3FFu) << 13);
+                }
+            } else if (e == 31) bits = (s << 31) | (0xFFu << 23) | (m << 13);
+            else bits = (s << 31) | ((e - 15 + 127) << 23) | (m << 13);
+            std::memcpy(&tmp[i], &bits, 4);
+        }
+    } else {
+        return set_error(YULE_ERR_UNSUPPORTED, "runner: norm weights must be F32 or F16");
+    }
+    return upload(r, tmp.data(), (size_t)n * 4, reinterpret_cast<void **>(dst));
+}
+
+int upload_matrix(yule_hip_runner *r, const void *src, uint32_t dtype, uint32_t rows, uint32_t cols, const char *name,
+                  const uint8_t **dst) {
+    uint32_t bs, bb;
+    if (!src) return set_error(YULE_ERR_INVALID, std::string("runner: missing tensor ") + name);
+    if (!quant_geometry(dtype, &bs, &bb))
+        return set_error(YULE_ERR_UNSUPPORTED, std::string("runner: ") + name + " has unsupported dtype " +
+                                                   std::to_string(dtype));
+    if (cols % bs)
+        return set_error(YULE_ERR_INVALID, std::string("runner: ") + name + " columns not a block multiple");
+    return upload(r, src, (size_t)rows * (cols / bs) * bb, reinterpret_cast<void **>(const_cast<uint8_t **>(dst)));
+}
+
+// One decode step for the token selected by ctl, entirely on r->be->stream.
+int enqueue_step(yule_hip_runner *r) {
+    hipStream_t s = r->be->stream;
+    const uint32_t qd = r->n_heads * r->hd, kvd = r->n_kv * r->hd;
+    int rc;
+    if ((rc = launch_embed_step(s, r->embd_t, r->embd, r->ctl, r->prompt, r->vocab, r->hidden, r->dim))) return rc;
+    for (const auto &L : r->layers) {
+        // attention block (model_runner.rs:619-784)
+        if ((rc = launch_rms_norm(s, r->hidden, L.attn_norm, r->normed, r->dim, r->eps))) return rc;
+        if (L.tq == L.tk && L.tk == L.tv) {
+            const QmvSeg segs[3] = {{L.wq, r->q, qd}, {L.wk, r->k, kvd}, {L.wv, r->v, kvd}};
+            if ((rc = launch_qmv_multi(s, L.tq, segs, 3, r->normed, r->dim))) return rc;
+        } else {
+            if ((rc = launch_qmv(s, L.tq, L.wq, r->normed, r->q, qd, r->dim))) return rc;
+            if ((rc = launch_qmv(s, L.tk, L.wk, r->normed, r->k, kvd, r->dim))) return rc;
+            if ((rc = launch_qmv(s, L.tv, L.wv, r->normed, r->v, kvd, r->dim))) return rc;
+        }
+        if ((rc = launch_rope_kv(s, r->q, r->k, r->v, L.kc, L.vc, r->cos_t, r->sin_t, r->ctl, r->n_heads, r->n_kv,
+                                 r->hd)))
+            return rc;
+        if ((rc = launch_gqa_attn(s, r->q, L.kc, L.vc, r->attn, r->n_heads, r->n_kv, r->hd, r->ctl, 0, r->max_seq)))
+            return rc;
+        if ((rc = launch_qmv(s, L.to, L.wo, r->attn, r->proj, r->dim, qd))) return rc;
+        if ((rc = launch_eltwise(s, 2, r->hidden, r->proj, r->hidden, r->dim))) return rc;
+        // feed-forward block (model_runner.rs:792-1004)
+        if ((rc = launch_rms_norm(s, r->hidden, L.ffn_norm, r->normed, r->dim, r->eps))) return rc;
+        if (L.tg == L.tu) {
+            const QmvSeg segs[2] = {{L.wg, r->gate, r->ff}, {L.wu, r->up, r->ff}};
+            if ((rc = launch_qmv_multi(s, L.tg, segs, 2, r->normed, r->dim))) return rc;
+        } else {
+            if ((rc = launch_qmv(s, L.tg, L.wg, r->normed, r->gate, r->ff, r->dim))) return rc;
+            if ((rc = launch_qmv(s, L.tu, L.wu, r->normed, r->up, r->ff, r->dim))) return rc;
+        }
+        if ((rc = launch_eltwise(s, 3, r->gate, r->up, r->gate, r->ff))) return rc;
+        if ((rc = launch_qmv(s, L.td, L.wd, r->gate, r->ffn, r->dim, r->ff))) return rc;
+        if ((rc = launch_eltwise(s, 2, r->hidden, r->ffn, r->hidden, r->dim))) return rc;
+    }
+    if ((rc = launch_rms_norm(s, r->hidden, r->out_norm, r->normed, r->dim, r->eps))) return rc;  // :1008-1016
+    if ((rc = launch_qmv(s, r->out_t, r->out_w, r->normed, r->logits, r->vocab, r->dim))) return rc;  // :1019-1025
+    return launch_argmax_advance(s, r->logits, r->vocab, r->ctl, r->tokens);
+}
+
+int ensure_graph(yule_hip_runner *r) {
+    if (r->exec) return YULE_OK;
+    hipStream_t s = r->be->stream;
+    int rc = hip_error(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "runner: begin capture");
+    if (rc) return rc;
+    const int erc = enqueue_step(r);
+    rc = hip_error(hipStreamEndCapture(s, &r->graph), "runner: end capture");
+    if (erc) return erc;
+    if (rc) return rc;
+    return hip_error(hipGraphInstantiate(&r->exec, r->graph, nullptr, nullptr, 0), "runner: graph instantiate");
+}
+
+int set_ctl(yule_hip_runner *r, uint32_t pos, uint32_t token, uint32_t prompt_len) {
+    // the pinned staging buffer may still feed a queued copy
+    int rc = hip_error(hipStreamSynchronize(r->be->stream), "runner: synchronize");
+    if (rc) return rc;
+    r->ctl_host[0] = pos;
+    r->ctl_host[1] = token;
+    r->ctl_host[2] = prompt_len;
+    return hip_error(hipMemcpyAsync(r->ctl, r->ctl_host, 3 * sizeof(uint32_t), hipMemcpyHostToDevice, r->be->stream),
+                     "runner: control update");
+}
+
+}  // namespace
+
+extern "C" {
+
+int yule_hip_runner_create(yule_hip_backend *be, const yule_model_desc *d, yule_hip_runner **out) {
+    if (!be || !d || !out) return set_error(YULE_ERR_INVALID, "runner_create: null argument");
+    *out = nullptr;
+    if (!d->n_layers || !d->dim || !d->n_heads || !d->n_kv_heads || !d->ff_dim || !d->vocab || !d->max_seq || !d->layers)
+        return set_error(YULE_ERR_INVALID, "runner_create: zero-sized configuration");
+    if (d->dim % d->n_heads || d->n_heads % d->n_kv_heads)
+        return set_error(YULE_ERR_INVALID, "runner_create: dim/n_heads/n_kv_heads inconsistent");
+    const uint32_t hd = d->dim / d->n_heads;
+    if (hd % 2 || hd > 256) return set_error(YULE_ERR_INVALID, "runner_create: head_dim must be even and <= 256");
+    if (d->max_seq > 16384) return set_error(YULE_ERR_INVALID, "runner_create: max_seq above 16384");
+    auto *r = new yule_hip_runner();
+    r->be = be;
+    r->n_layers = d->n_layers; r->dim = d->dim; r->n_heads = d->n_heads; r->n_kv = d->n_kv_heads; r->hd = hd;
+    r->ff = d->ff_dim; r->vocab = d->vocab; r->max_seq = d->max_seq; r->eps = d->norm_eps; r->rope_base = d->rope_base;
+    const uint32_t qd = r->n_heads * hd, kvd = r->n_kv * hd;
+    int rc = YULE_OK;
+    auto fail = [&](int code) { yule_hip_runner_destroy(r); return code; };
+    if ((rc = hip_error(hipSetDevice(be->device), "runner: set device"))) return fail(rc);
+    if ((rc = upload_matrix(r, d->token_embd, d->token_embd_dtype, r->vocab, r->dim, "token_embd", &r->embd)))
+        return fail(rc);
+    r->embd_t = d->token_embd_dtype;
+    if ((rc = upload_norm(r, d->output_norm, d->output_norm_dtype, r->dim, &r->out_norm))) return fail(rc);
+    if ((rc = upload_matrix(r, d->output, d->output_dtype, r->vocab, r->dim, "output", &r->out_w))) return fail(rc);
+    r->out_t = d->output_dtype;
+    r->layers.resize(r->n_layers);
+    for (uint32_t i = 0; i < r->n_layers; i++) {
+        const yule_layer_desc &ld = d->layers[i];
+        auto &L = r->layers[i];
+        L.tq = ld.wq_dtype; L.tk = ld.wk_dtype; L.tv = ld.wv_dtype; L.to = ld.wo_dtype;
+        L.tg = ld.w_gate_dtype; L.tu = ld.w_up_dtype; L.td = ld.w_down_dtype;
+        if ((rc = upload_norm(r, ld.attn_norm, ld.attn_norm_dtype, r->dim, &L.attn_norm)) ||
+            (rc = upload_norm(r, ld.ffn_norm, ld.ffn_norm_dtype, r->dim, &L.ffn_norm)) ||
+            (rc = upload_matrix(r, ld.wq, L.tq, qd, r->dim, "attn_q", &L.wq)) ||
+            (rc = upload_matrix(r, ld.wk, L.tk, kvd, r->dim, "attn_k", &L.wk)) ||
+            (rc = upload_matrix(r, ld.wv, L.tv, kvd, r->dim, "attn_v", &L.wv)) ||
+            (rc = upload_matrix(r, ld.wo, L.to, r->dim, qd, "attn_output", &L.wo)) ||
+            (rc = upload_matrix(r, ld.w_gate, L.tg, r->ff, r->dim, "ffn_gate", &L.wg)) ||
+            (rc = upload_matrix(r, ld.w_up, L.tu, r->ff, r->dim, "ffn_up", &L.wu)) ||
+            (rc = upload_matrix(r, ld.w_down, L.td, r->dim, r->ff, "ffn_down", &L.wd)) ||
+            (rc = dev_alloc(r, (size_t)r->max_seq * kvd * 4, reinterpret_cast<void **>(&L.kc))) ||
+            (rc = dev_alloc(r, (size_t)r->max_seq * kvd * 4, reinterpret_cast<void **>(&L.vc))))
+            return fail(rc);
+    }
+    // RoPE table with RopeTable::new's f32 formula (model_runner.rs:77-100)
+    const uint32_t half = hd / 2;
+    std::vector<float> ct((size_t)r->max_seq * half), st((size_t)r->max_seq * half);
+    for (uint32_t p = 0; p < r->max_seq; p++)
+        for (uint32_t i = 0; i < half; i++) {
+            const float freq = 1.0f / powf(r->rope_base, 2.0f * (float)i / (float)hd);
+            const float theta = (float)p * freq;
+            ct[(size_t)p * half + i] = cosf(theta);
+            st[(size_t)p * half + i] = sinf(theta);
+        }
+    if ((rc = upload(r, ct.data(), ct.size() * 4, reinterpret_cast<void **>(&r->cos_t))) ||
+        (rc = upload(r, st.data(), st.size() * 4, reinterpret_cast<void **>(&r->sin_t))))
+        return fail(rc);
+    struct { float **p; size_t n; } bufs[] = {
+        {&r->hidden, r->dim}, {&r->normed, r->dim}, {&r->q, qd}, {&r->k, kvd}, {&r->v, kvd}, {&r->attn, qd},
+        {&r->proj, r->dim}, {&r->gate, r->ff}, {&r->up, r->ff}, {&r->ffn, r->dim}, {&r->logits, r->vocab}};
+    for (auto &b : bufs)
+        if ((rc = dev_alloc(r, b.n * 4, reinterpret_cast<void **>(b.p)))) return fail(rc);
+    if ((rc = dev_alloc(r, 4 * sizeof(uint32_t), reinterpret_cast<void **>(&r->ctl))) ||
+        (rc = dev_alloc(r, (size_t)r->max_seq * 4, reinterpret_cast<void **>(&r->prompt))) ||
+        (rc = dev_alloc(r, (size_t)r->max_seq * 4, reinterpret_cast<void **>(&r->tokens))))
+        return fail(rc);
+    if ((rc = hip_error(hipHostMalloc(reinterpret_cast<void **>(&r->ctl_host), 4 * sizeof(uint32_t), 0),
+                        "runner: pinned control block")))
+        return fail(rc);
+    *out = r;
+    return YULE_OK;
+}
+
+int yule_hip_runner_destroy(yule_hip_runner *r) {
+    if (!r) return YULE_OK;
+    if (r->be) hipStreamSynchronize(r->be->stream);
+    if (r->exec) hipGraphExecDestroy(r->exec);
+    if (r->graph) hipGraphDestroy(r->graph);
+    for (void *p : r->allocs) hipFree(p);
+    if (r->ctl_host) hipHostFree(r->ctl_host);
+    delete r;
+    return YULE_OK;
+}
+
+// ModelRunner::reset (model_runner.rs:1087-1092)
+int yule_hip_runner_reset(yule_hip_runner *r) {
+    if (!r) return set_error(YULE_ERR_INVALID, "runner_reset: null runner");
+    r->pos = 0;
+    return YULE_OK;
+}
+
+uint32_t yule_hip_runner_pos(const yule_hip_runner *r) { return r ? r->pos : 0; }
+
+// ModelRunner::decode_step (model_runner.rs:1083-1085): one forward pass at
+// the current position; logits copied out when `logits` is non-null.
+int yule_hip_runner_decode_step(yule_hip_runner *r, uint32_t token, float *logits) {
+    if (!r) return set_error(YULE_ERR_INVALID, "runner: null runner");
+    if (r->pos >= r->max_seq) return set_error(YULE_ERR_INVALID, "context length exceeded");
+    if (token >= r->vocab) return set_error(YULE_ERR_INVALID, "token id out of range");
+    int rc;
+    if ((rc = ensure_graph(r))) return rc;
+    if ((rc = set_ctl(r, r->pos, token, 0))) return rc;
+    if ((rc = hip_error(hipGraphLaunch(r->exec, r->be->stream), "runner: graph launch"))) return rc;
+    r->pos++;
+    if (logits &&
+        (rc = hip_error(hipMemcpyAsync(logits, r->logits, (size_t)r->vocab * 4, hipMemcpyDeviceToHost, r->be->stream),
+                        "runner: logits copy")))
+        return rc;
+    return hip_error(hipStreamSynchronize(r->be->stream), "runner: synchronize");
+}
+
+// ModelRunner::prefill (model_runner.rs:1075-1081): token by token; logits
+// of the last token.
+int yule_hip_runner_prefill(yule_hip_runner *r, const uint32_t *tokens, uint32_t n, float *logits) {
+    if (!r || (!tokens && n)) return set_error(YULE_ERR_INVALID, "runner_prefill: null argument");
+    for (uint32_t i = 0; i < n; i++) {
+        int rc = yule_hip_runner_decode_step(r, tokens[i], i + 1 == n ? logits : nullptr);
+        if (rc) return rc;
+    }
+    return YULE_OK;
+}
+
+int yule_hip_runner_generate_greedy(yule_hip_runner *r, const uint32_t *prompt, uint32_t n_prompt, uint32_t n_decode,
+                                    uint32_t *out_tokens, float *ms_per_decode_step) {
+    if (!r || !prompt || !out_tokens || n_prompt == 0)
+        return set_error(YULE_ERR_INVALID, "runner_generate: null argument or empty prompt");
+    if ((uint64_t)n_prompt + n_decode > r->max_seq)
+        return set_error(YULE_ERR_INVALID, "runner_generate: prompt + decode steps exceed the context length");
+    for (uint32_t i = 0; i < n_prompt; i++)
+        if (prompt[i] >= r->vocab) return set_error(YULE_ERR_INVALID, "runner_generate: token id out of range");
+    hipStream_t s = r->be->stream;
+    int rc;
+    if ((rc = ensure_graph(r))) return rc;
+    if ((rc = hip_error(hipMemcpyAsync(r->prompt, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice, s),
+                        "runner: prompt upload")))
+        return rc;
+    if ((rc = set_ctl(r, 0, 0, n_prompt))) return rc;
+    for (uint32_t i = 0; i < n_prompt; i++)
+        if ((rc = hip_error(hipGraphLaunch(r->exec, s), "runner: graph launch"))) return rc;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if ((rc = hip_error(hipEventCreate(&e0), "hipEventCreate")) || (rc = hip_error(hipEventCreate(&e1), "hipEventCreate")))
+        goto done;
+    if ((rc = hip_error(hipEventRecord(e0, s), "hipEventRecord"))) goto done;
+    for (uint32_t i = 0; i < n_decode && !rc; i++) rc = hip_error(hipGraphLaunch(r->exec, s), "runner: graph launch");
+    if (rc || (rc = hip_error(hipEventRecord(e1, s), "hipEventRecord"))) goto done;
+    if ((rc = hip_error(hipEventSynchronize(e1), "hipEventSynchronize"))) goto done;
+    if (ms_per_decode_step) {
+        float ms = 0.f;
+        if ((rc = hip_error(hipEventElapsedTime(&ms, e0, e1), "hipEventElapsedTime"))) goto done;
+        *ms_per_decode_step = n_decode ? ms / (float)n_decode : 0.f;
+    }
+    // the argmax after the last prompt token and after every decode step
+    rc = hip_error(hipMemcpy(out_tokens, r->tokens + (n_prompt - 1), (size_t)(n_decode + 1) * 4,
+                             hipMemcpyDeviceToHost),
+                   "runner: token copy");
+    r->pos = n_prompt + n_decode;
+done:
+    if (e0) hipEventDestroy(e0);
+    if (e1) hipEventDestroy(e1);
+    return rc;
+}
+
+}  // extern "C"
