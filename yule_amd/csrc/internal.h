@@ -76,9 +76,9 @@ int launch_fill(hipStream_t stream, float *out, float value, uint64_t n);
 // op 0 silu, 1 mul, 2 add, 3 silu(a)*b
 int launch_eltwise(hipStream_t stream, int op, const float *a, const float *b, float *out, uint32_t n);
 int launch_rms_norm(hipStream_t stream, const float *x, const float *w, float *out, uint32_t n, float eps);
-// GQA decode attention; seq = pos_dev[0] + 1 when pos_dev, else seq_host
+// GQA decode attention of rotated q over cache rows 0..seq-1
 int launch_gqa_attn(hipStream_t stream, const float *q, const float *kc, const float *vc, float *out, uint32_t n_heads,
-                    uint32_t n_kv, uint32_t hd, const uint32_t *pos_dev, uint32_t seq_host, uint32_t max_seq);
+                    uint32_t n_kv, uint32_t hd, uint32_t seq);
 int launch_argmax(hipStream_t stream, const float *in, uint32_t n, uint32_t *out);
 // decode-runner steps driven by the device control block ctl = {pos, token, prompt_len}
 int launch_embed_step(hipStream_t stream, uint32_t dtype, const uint8_t *table, const uint32_t *ctl,
@@ -86,6 +86,10 @@ int launch_embed_step(hipStream_t stream, uint32_t dtype, const uint8_t *table, 
 int launch_rope_kv(hipStream_t stream, float *q, const float *k, const float *v, float *kc, float *vc,
                    const float *cos_t, const float *sin_t, const uint32_t *ctl, uint32_t nq, uint32_t nk,
                    uint32_t hd);
+// RoPE + KV-cache write + GQA attention of one decode step (one launch)
+int launch_attn_step(hipStream_t stream, const float *q, const float *k, const float *v, float *kc, float *vc,
+                     const float *cos_t, const float *sin_t, const uint32_t *ctl, float *out, uint32_t n_heads,
+                     uint32_t n_kv, uint32_t hd, uint32_t max_seq);
 int launch_argmax_advance(hipStream_t stream, const float *logits, uint32_t n, uint32_t *ctl, uint32_t *out_tokens);
 
 }  // namespace yule

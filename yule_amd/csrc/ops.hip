@@ -122,9 +122,11 @@ __global__ void rope_kernel(float *__restrict__ q, float *__restrict__ k, uint32
     if (i >= total) return;
     const uint32_t head = i / half, p = i % half;
     float *v = head < nq ? q + head * hd : k + (head - nq) * hd;
-    const float freq = 1.0f / powf(base, 2.0f * (float)p / (float)hd);
+    // f32 values of the reference's f32 formula, each evaluated in double and
+    // rounded once, so they match the host libm's rounded f32 results
+    const float freq = (float)(1.0 / pow((double)base, (double)(2.0f * (float)p / (float)hd)));
     const float theta = (float)pos * freq;
-    const float c = cosf(theta), sn = sinf(theta);
+    const float c = (float)cos((double)theta), sn = (float)sin((double)theta);
     const float x0 = v[2 * p], x1 = v[2 * p + 1];
     v[2 * p] = x0 * c - x1 * sn;
     v[2 * p + 1] = x0 * sn + x1 * c;
@@ -165,75 +167,8 @@ __global__ void attn_value_kernel(const float *__restrict__ w, const float *__re
 }
 
 // ------------------------------------------------------------ GQA decode attention
-// One workgroup (4 waves) per query head; model_runner.rs:679-758 semantics.
-// Scores live in LDS (seq_len <= kMaxSeqLds); K rows are read with lanes
-// over the head dimension (coalesced), V likewise, and the four waves split
-// the positions and combine through LDS.  K/V of a KV head are shared by its
-// n_heads/n_kv_heads query heads through L2.
 constexpr uint32_t kMaxSeqLds = 16384;
 constexpr uint32_t kMaxHeadDim = 256;
-
-__global__ __launch_bounds__(256) void gqa_attn_kernel(const float *__restrict__ q, const float *__restrict__ kc,
-                                                       const float *__restrict__ vc, float *__restrict__ out,
-                                                       uint32_t group, uint32_t n_kv, uint32_t hd,
-                                                       const uint32_t *__restrict__ seq_dev, uint32_t seq_host) {
-    extern __shared__ float smem[];
-    float *scores = smem;                        // [seq]
-    __shared__ float red[16];
-    __shared__ float part[4][kMaxHeadDim];
-    const uint32_t h = blockIdx.x, kvh = h / group, kvs = n_kv * hd;
-    const uint32_t seq = seq_dev ? seq_dev[0] + 1 : seq_host;   // device counter holds the position
-    const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const float scale = 1.0f / sqrtf((float)hd);
-    const float *qh = q + (size_t)h * hd;
-    float qr[kMaxHeadDim / 64];
-#pragma unroll
-    for (uint32_t c = 0; c < kMaxHeadDim / 64; c++) qr[c] = (lane + 64 * c < hd) ? qh[lane + 64 * c] : 0.f;
-
-    for (uint32_t t = w; t < seq; t += 4) {
-        const float *kr = kc + (size_t)t * kvs + kvh * hd;
-        float acc = 0.f;
-#pragma unroll
-        for (uint32_t c = 0; c < kMaxHeadDim / 64; c++)
-            if (lane + 64 * c < hd) acc += qr[c] * kr[lane + 64 * c];
-        acc = wave_sum(acc);
-        if (lane == 0) scores[t] = acc * scale;
-    }
-    __syncthreads();
-    float m = -INFINITY;
-    for (uint32_t t = threadIdx.x; t < seq; t += blockDim.x) m = fmaxf(m, scores[t]);
-    m = block_max(m, red);
-    float sum = 0.f;
-    for (uint32_t t = threadIdx.x; t < seq; t += blockDim.x) {
-        const float e = expf(scores[t] - m);
-        scores[t] = e;
-        sum += e;
-    }
-    sum = block_sum(sum, red);   // ends with a barrier-protected read; scores[] complete
-    const float inv = 1.0f / sum;
-    float o[kMaxHeadDim / 64] = {};
-    for (uint32_t t = w; t < seq; t += 4) {
-        const float p = scores[t] * inv;
-        const float *vr = vc + (size_t)t * kvs + kvh * hd;
-#pragma unroll
-        for (uint32_t c = 0; c < kMaxHeadDim / 64; c++)
-            if (lane + 64 * c < hd) o[c] += p * vr[lane + 64 * c];
-    }
-#pragma unroll
-    for (uint32_t c = 0; c < kMaxHeadDim / 64; c++)
-        if (lane + 64 * c < hd) part[w][lane + 64 * c] = o[c];
-    __syncthreads();
-    for (uint32_t d = threadIdx.x; d < hd; d += blockDim.x)
-        out[(size_t)h * hd + d] = part[0][d] + part[1][d] + part[2][d] + part[3][d];
-}
-
-int launch_gqa_attn(hipStream_t s, const float *q, const float *kc, const float *vc, float *out, uint32_t n_heads,
-                    uint32_t n_kv, uint32_t hd, const uint32_t *pos_dev, uint32_t seq_host, uint32_t max_seq) {
-    const size_t lds = (size_t)max_seq * sizeof(float);
-    hipLaunchKernelGGL(gqa_attn_kernel, dim3(n_heads), dim3(256), lds, s, q, kc, vc, out, n_heads / n_kv, n_kv, hd,
-                       pos_dev, seq_host);
-    return check_launch("gqa_decode_attn");
-}
 
 // ------------------------------------------------------------ argmax
 // argmax_ct (sampler.rs:150-163): the last maximal index wins.
@@ -417,7 +352,8 @@ int yule_hip_gqa_decode_attn(yule_hip_backend *be, yule_buffer q, yule_buffer k_
         (rc = f32buf(be, v_cache, kv, &pv, "gqa_decode_attn (v_cache)")) ||
         (rc = f32buf(be, out, (size_t)n_heads * head_dim, &po, "gqa_decode_attn (out)")))
         return rc;
-    return launch_gqa_attn(be->stream, pq, pk, pv, po, n_heads, n_kv_heads, head_dim, nullptr, seq_len, seq_len);
+    if (head_dim % 4) return set_error(YULE_ERR_INVALID, "gqa_decode_attn: head_dim must be a multiple of 4");
+    return launch_gqa_attn(be->stream, pq, pk, pv, po, n_heads, n_kv_heads, head_dim, seq_len);
 }
 
 int yule_hip_argmax(yule_hip_backend *be, yule_buffer in, uint32_t n, yule_buffer out) {
@@ -460,6 +396,111 @@ int launch_embed_step(hipStream_t s, uint32_t dtype, const uint8_t *table, const
     hipLaunchKernelGGL(embed_step_kernel, dim3((dim + 255) / 256), dim3(256), 0, s, dtype, bs, bb, table, ctl, prompt,
                        vocab, dst, dim);
     return check_launch("embedding");
+}
+
+// Fused decode attention step for one layer: RoPE of q and of the new k
+// with the table row of the current position, the cache write of the new k
+// and v (model_runner.rs:654-669), then GQA attention over positions
+// 0..pos (model_runner.rs:679-758).  One workgroup per query head; the
+// first head of each KV group writes that group's cache row, and every
+// workgroup uses its own rotated copy of the new k / v for position pos, so
+// no workgroup reads a cache row another one is writing.  Scores: one lane
+// per position (full head-dim dot from float4 loads of the K row); softmax
+// over LDS; output: lanes over the head dimension, positions split across
+// 256/hd lane groups and combined through LDS.
+// Without a control block (ctl == nullptr) it is plain GQA attention of the
+// already-rotated q over cache rows 0..seq_host-1 (the ABI entry point).
+__global__ __launch_bounds__(256) void attn_step_kernel(const float *__restrict__ q, const float *__restrict__ k,
+                                                        const float *__restrict__ v, float *__restrict__ kc,
+                                                        float *__restrict__ vc, const float *__restrict__ cos_t,
+                                                        const float *__restrict__ sin_t,
+                                                        const uint32_t *__restrict__ ctl, float *__restrict__ out,
+                                                        uint32_t group, uint32_t n_kv, uint32_t hd,
+                                                        uint32_t seq_host) {
+    extern __shared__ float scores[];                 // [pos + 1]
+    __shared__ __align__(16) float qs[kMaxHeadDim], kn[kMaxHeadDim], vn[kMaxHeadDim];
+    __shared__ float part[256];
+    __shared__ float red[16];
+    const uint32_t h = blockIdx.x, kvh = h / group, kvs = n_kv * hd, half = hd / 2, tid = threadIdx.x;
+    const bool step = ctl != nullptr;
+    const uint32_t seq = step ? ctl[0] + 1 : seq_host;
+    const uint32_t pos = step ? seq - 1 : 0xFFFFFFFFu;   // row served from the local copy
+    const float *qh = q + (size_t)h * hd;
+    if (!step) {
+        for (uint32_t i = tid; i < hd; i += 256) qs[i] = qh[i];
+    }
+    const float *kh = step ? k + (size_t)kvh * hd : nullptr, *vh = step ? v + (size_t)kvh * hd : nullptr;
+    for (uint32_t i = tid; step && i < half; i += 256) {
+        const float c = cos_t[(size_t)pos * half + i], sn = sin_t[(size_t)pos * half + i];
+        float x0 = qh[2 * i], x1 = qh[2 * i + 1];
+        qs[2 * i] = x0 * c - x1 * sn;
+        qs[2 * i + 1] = x0 * sn + x1 * c;
+        x0 = kh[2 * i]; x1 = kh[2 * i + 1];
+        kn[2 * i] = x0 * c - x1 * sn;
+        kn[2 * i + 1] = x0 * sn + x1 * c;
+    }
+    for (uint32_t i = tid; step && i < hd; i += 256) vn[i] = vh[i];
+    __syncthreads();
+    if (step && h % group == 0) {
+        float *krow = kc + (size_t)pos * kvs + kvh * hd, *vrow = vc + (size_t)pos * kvs + kvh * hd;
+        for (uint32_t i = tid; i < hd; i += 256) { krow[i] = kn[i]; vrow[i] = vn[i]; }
+    }
+    const float scale = 1.0f / sqrtf((float)hd);
+    float m = -INFINITY;
+    for (uint32_t t = tid; t < seq; t += 256) {
+        const float4 *kr = reinterpret_cast<const float4 *>(t == pos ? kn : kc + (size_t)t * kvs + kvh * hd);
+        float acc = 0.f;
+        for (uint32_t c4 = 0; c4 < hd / 4; c4++) {
+            const float4 kv = kr[c4];
+            acc += qs[4 * c4] * kv.x;
+            acc += qs[4 * c4 + 1] * kv.y;
+            acc += qs[4 * c4 + 2] * kv.z;
+            acc += qs[4 * c4 + 3] * kv.w;
+        }
+        const float sc = acc * scale;
+        scores[t] = sc;
+        m = fmaxf(m, sc);
+    }
+    m = block_max(m, red);
+    float sum = 0.f;
+    for (uint32_t t = tid; t < seq; t += 256) {
+        const float e = expf(scores[t] - m);
+        scores[t] = e;
+        sum += e;
+    }
+    sum = block_sum(sum, red);   // its barriers also publish scores[]
+    const float inv = 1.0f / sum;
+    const uint32_t ng = 256 / hd, d = tid % hd, g = tid / hd;
+    float o = 0.f;
+    if (g < ng) {
+        for (uint32_t t = g; t < seq; t += ng) {
+            const float *vr = t == pos ? vn : vc + (size_t)t * kvs + kvh * hd;
+            o += (scores[t] * inv) * vr[d];
+        }
+    }
+    part[tid] = o;
+    __syncthreads();
+    if (tid < hd) {
+        float acc = 0.f;
+        for (uint32_t i = 0; i < ng; i++) acc += part[i * hd + tid];
+        out[(size_t)h * hd + tid] = acc;
+    }
+}
+
+int launch_attn_step(hipStream_t s, const float *q, const float *k, const float *v, float *kc, float *vc,
+                     const float *cos_t, const float *sin_t, const uint32_t *ctl, float *out, uint32_t n_heads,
+                     uint32_t n_kv, uint32_t hd, uint32_t max_seq) {
+    hipLaunchKernelGGL(attn_step_kernel, dim3(n_heads), dim3(256), (size_t)max_seq * sizeof(float), s, q, k, v, kc, vc,
+                       cos_t, sin_t, ctl, out, n_heads / n_kv, n_kv, hd, 0u);
+    return check_launch("attn_step");
+}
+
+int launch_gqa_attn(hipStream_t s, const float *q, const float *kc, const float *vc, float *out, uint32_t n_heads,
+                    uint32_t n_kv, uint32_t hd, uint32_t seq) {
+    hipLaunchKernelGGL(attn_step_kernel, dim3(n_heads), dim3(256), (size_t)seq * sizeof(float), s, q, nullptr, nullptr,
+                       const_cast<float *>(kc), const_cast<float *>(vc), nullptr, nullptr, nullptr, out,
+                       n_heads / n_kv, n_kv, hd, seq);
+    return check_launch("gqa_decode_attn");
 }
 
 // RoPE of q (in place) and k with the precomputed table row of the current

@@ -11,6 +11,7 @@
 // graph captured once replays every step, prefill and decode alike; the
 // argmax kernel writes the next token and advances the position.
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -116,10 +117,8 @@ int enqueue_step(yule_hip_runner *r) {
             if ((rc = launch_qmv(s, L.tk, L.wk, r->normed, r->k, kvd, r->dim))) return rc;
             if ((rc = launch_qmv(s, L.tv, L.wv, r->normed, r->v, kvd, r->dim))) return rc;
         }
-        if ((rc = launch_rope_kv(s, r->q, r->k, r->v, L.kc, L.vc, r->cos_t, r->sin_t, r->ctl, r->n_heads, r->n_kv,
-                                 r->hd)))
-            return rc;
-        if ((rc = launch_gqa_attn(s, r->q, L.kc, L.vc, r->attn, r->n_heads, r->n_kv, r->hd, r->ctl, 0, r->max_seq)))
+        if ((rc = launch_attn_step(s, r->q, r->k, r->v, L.kc, L.vc, r->cos_t, r->sin_t, r->ctl, r->attn, r->n_heads,
+                                   r->n_kv, r->hd, r->max_seq)))
             return rc;
         if ((rc = launch_qmv(s, L.to, L.wo, r->attn, r->proj, r->dim, qd))) return rc;
         if ((rc = launch_eltwise(s, 2, r->hidden, r->proj, r->hidden, r->dim))) return rc;
@@ -153,6 +152,14 @@ int ensure_graph(yule_hip_runner *r) {
     return hip_error(hipGraphInstantiate(&r->exec, r->graph, nullptr, nullptr, 0), "runner: graph instantiate");
 }
 
+// Replay the captured step, or (YULE_RUNNER_NO_GRAPH set, for tracing
+// profilers that do not follow graph launches) enqueue its kernels directly.
+int run_step(yule_hip_runner *r) {
+    static const bool direct = getenv("YULE_RUNNER_NO_GRAPH") != nullptr;
+    if (direct) return enqueue_step(r);
+    return hip_error(hipGraphLaunch(r->exec, r->be->stream), "runner: graph launch");
+}
+
 int set_ctl(yule_hip_runner *r, uint32_t pos, uint32_t token, uint32_t prompt_len) {
     // the pinned staging buffer may still feed a queued copy
     int rc = hip_error(hipStreamSynchronize(r->be->stream), "runner: synchronize");
@@ -176,7 +183,8 @@ int yule_hip_runner_create(yule_hip_backend *be, const yule_model_desc *d, yule_
     if (d->dim % d->n_heads || d->n_heads % d->n_kv_heads)
         return set_error(YULE_ERR_INVALID, "runner_create: dim/n_heads/n_kv_heads inconsistent");
     const uint32_t hd = d->dim / d->n_heads;
-    if (hd % 2 || hd > 256) return set_error(YULE_ERR_INVALID, "runner_create: head_dim must be even and <= 256");
+    if (hd % 4 || hd > 256)
+        return set_error(YULE_ERR_INVALID, "runner_create: head_dim must be a multiple of 4 and <= 256");
     if (d->max_seq > 16384) return set_error(YULE_ERR_INVALID, "runner_create: max_seq above 16384");
     auto *r = new yule_hip_runner();
     r->be = be;
@@ -269,7 +277,7 @@ int yule_hip_runner_decode_step(yule_hip_runner *r, uint32_t token, float *logit
     int rc;
     if ((rc = ensure_graph(r))) return rc;
     if ((rc = set_ctl(r, r->pos, token, 0))) return rc;
-    if ((rc = hip_error(hipGraphLaunch(r->exec, r->be->stream), "runner: graph launch"))) return rc;
+    if ((rc = run_step(r))) return rc;
     r->pos++;
     if (logits &&
         (rc = hip_error(hipMemcpyAsync(logits, r->logits, (size_t)r->vocab * 4, hipMemcpyDeviceToHost, r->be->stream),
@@ -305,12 +313,12 @@ int yule_hip_runner_generate_greedy(yule_hip_runner *r, const uint32_t *prompt, 
         return rc;
     if ((rc = set_ctl(r, 0, 0, n_prompt))) return rc;
     for (uint32_t i = 0; i < n_prompt; i++)
-        if ((rc = hip_error(hipGraphLaunch(r->exec, s), "runner: graph launch"))) return rc;
+        if ((rc = run_step(r))) return rc;
     hipEvent_t e0 = nullptr, e1 = nullptr;
     if ((rc = hip_error(hipEventCreate(&e0), "hipEventCreate")) || (rc = hip_error(hipEventCreate(&e1), "hipEventCreate")))
         goto done;
     if ((rc = hip_error(hipEventRecord(e0, s), "hipEventRecord"))) goto done;
-    for (uint32_t i = 0; i < n_decode && !rc; i++) rc = hip_error(hipGraphLaunch(r->exec, s), "runner: graph launch");
+    for (uint32_t i = 0; i < n_decode && !rc; i++) rc = run_step(r);
     if (rc || (rc = hip_error(hipEventRecord(e1, s), "hipEventRecord"))) goto done;
     if ((rc = hip_error(hipEventSynchronize(e1), "hipEventSynchronize"))) goto done;
     if (ms_per_decode_step) {
