@@ -28,8 +28,13 @@ def tiny():
     return SyntheticModel.generate(TINY_TEST, seed=3)
 
 
-def test_runner_logits_match_oracle_small(hip, tiny):
-    say("[runner] small model logits vs oracle")
+@pytest.mark.parametrize("fused", [True, False], ids=["fused", "unfused"])
+def test_runner_logits_match_oracle_small(hip, tiny, fused, monkeypatch):
+    """Both step sequences: fused (norm/SwiGLU staged into the matvec, residual
+    and argmax epilogues) and the plain kernel-per-operation sequence."""
+    say(f"[runner] small model logits vs oracle ({'fused' if fused else 'unfused'})")
+    if not fused:
+        monkeypatch.setenv("YULE_RUNNER_UNFUSED", "1")
     run = HipRunner(hip, tiny)
     ref, f64 = oracle.Runner(tiny, n_threads=4), NpForward(tiny)
     for t in synth.uniform_tokens(11, 40, tiny.cfg.vocab):

@@ -59,12 +59,31 @@ struct QmvSeg {
     uint32_t n_rows;
 };
 
+// Optional fusions of the streaming matvec: a transform applied to the
+// activation vector while it is staged, and an epilogue.
+constexpr uint32_t kXfNone = 0, kXfRmsNorm = 1, kXfSwiGlu = 2;
+constexpr uint32_t kEpiStore = 0, kEpiAdd = 1, kEpiArgmax = 2;
+struct QmvXf {
+    uint32_t mode = kXfNone;         // kXfRmsNorm: x*inv_rms*a; kXfSwiGlu: x*sigmoid(x)*a
+    const float *a = nullptr;        // norm weight or up vector, n_cols floats
+    float eps = 0.f;
+    uint32_t epi = kEpiStore;        // kEpiAdd: y += result; kEpiArgmax: store + atomicMax(*amax)
+    unsigned long long *amax = nullptr;
+    bool pair = false;               // gate/up pair: segment 0 output = silu(gate)*up
+};
+
 // Kernel launchers (device code in qmv.hip / ops.hip / attn.hip / gemm.hip).
 // Arguments are already validated; all enqueue on `stream`.
 int launch_qmv(hipStream_t stream, uint32_t dtype, const uint8_t *w, const float *x, float *y,
                uint32_t n_rows, uint32_t n_cols);
 int launch_qmv_multi(hipStream_t stream, uint32_t dtype, const QmvSeg *segs, uint32_t n_seg, const float *x,
                      uint32_t n_cols);
+// true when (dtype, n_cols) runs on the streaming kernel, i.e. fusions apply
+bool qmv_fusable(uint32_t dtype, uint32_t n_cols);
+// true when gate/up of this shape can run as one paired launch (xf.pair)
+bool qmv_pairable(uint32_t dtype, uint32_t n_cols);
+int launch_qmv_fused(hipStream_t stream, uint32_t dtype, const QmvSeg *segs, uint32_t n_seg, const float *x,
+                     uint32_t n_cols, const QmvXf &xf);
 int launch_dequant(hipStream_t stream, uint32_t dtype, const uint8_t *src, float *dst,
                    uint32_t n_blocks);
 // dequantize row token[0] (clamped to n_rows-1) of a [n_rows][dim] quantized
@@ -81,8 +100,10 @@ int launch_gqa_attn(hipStream_t stream, const float *q, const float *kc, const f
                     uint32_t n_kv, uint32_t hd, uint32_t seq);
 int launch_argmax(hipStream_t stream, const float *in, uint32_t n, uint32_t *out);
 // decode-runner steps driven by the device control block ctl = {pos, token, prompt_len}
+// (also zeroes *amax when non-null: the lm_head argmax slot of the step)
 int launch_embed_step(hipStream_t stream, uint32_t dtype, const uint8_t *table, const uint32_t *ctl,
-                      const uint32_t *prompt, uint32_t vocab, float *dst, uint32_t dim);
+                      const uint32_t *prompt, uint32_t vocab, float *dst, uint32_t dim, unsigned long long *amax);
+int launch_advance(hipStream_t stream, const unsigned long long *amax, uint32_t *ctl, uint32_t *out_tokens);
 int launch_rope_kv(hipStream_t stream, float *q, const float *k, const float *v, float *kc, float *vc,
                    const float *cos_t, const float *sin_t, const uint32_t *ctl, uint32_t nq, uint32_t nk,
                    uint32_t hd);

@@ -380,8 +380,10 @@ __device__ __forceinline__ uint32_t step_token(const uint32_t *ctl, const uint32
 
 __global__ void embed_step_kernel(uint32_t dtype, uint32_t bs, uint32_t bb, const uint8_t *__restrict__ table,
                                   const uint32_t *__restrict__ ctl, const uint32_t *__restrict__ prompt,
-                                  uint32_t vocab, float *__restrict__ dst, uint32_t dim) {
+                                  uint32_t vocab, float *__restrict__ dst, uint32_t dim,
+                                  unsigned long long *__restrict__ amax) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i == 0 && amax) *amax = 0ull;   // this step's lm_head argmax starts empty
     if (i >= dim) return;
     uint32_t t = step_token(ctl, prompt);
     t = t < vocab ? t : vocab - 1;   // host-checked tokens are in range; clamp keeps reads inside the table
@@ -390,11 +392,11 @@ __global__ void embed_step_kernel(uint32_t dtype, uint32_t bs, uint32_t bb, cons
 }
 
 int launch_embed_step(hipStream_t s, uint32_t dtype, const uint8_t *table, const uint32_t *ctl, const uint32_t *prompt,
-                      uint32_t vocab, float *dst, uint32_t dim) {
+                      uint32_t vocab, float *dst, uint32_t dim, unsigned long long *amax) {
     uint32_t bs, bb;
     if (!quant_geometry(dtype, &bs, &bb)) return set_error(YULE_ERR_UNSUPPORTED, "embedding: unsupported dtype");
     hipLaunchKernelGGL(embed_step_kernel, dim3((dim + 255) / 256), dim3(256), 0, s, dtype, bs, bb, table, ctl, prompt,
-                       vocab, dst, dim);
+                       vocab, dst, dim, amax);
     return check_launch("embedding");
 }
 
@@ -419,7 +421,7 @@ __global__ __launch_bounds__(256) void attn_step_kernel(const float *__restrict_
                                                         uint32_t seq_host) {
     extern __shared__ float scores[];                 // [pos + 1]
     __shared__ __align__(16) float qs[kMaxHeadDim], kn[kMaxHeadDim], vn[kMaxHeadDim];
-    __shared__ float part[256];
+    __shared__ __align__(16) float part[1024];          // ng * hd partial outputs (ng * hd = 1024)
     __shared__ float red[16];
     const uint32_t h = blockIdx.x, kvh = h / group, kvs = n_kv * hd, half = hd / 2, tid = threadIdx.x;
     const bool step = ctl != nullptr;
@@ -470,15 +472,38 @@ __global__ __launch_bounds__(256) void attn_step_kernel(const float *__restrict_
     }
     sum = block_sum(sum, red);   // its barriers also publish scores[]
     const float inv = 1.0f / sum;
-    const uint32_t ng = 256 / hd, d = tid % hd, g = tid / hd;
-    float o = 0.f;
+    // output: each lane owns 4 consecutive dims (float4 of V) and a
+    // residue class of positions; four independent accumulators keep four
+    // V loads in flight per lane
+    const uint32_t nd4 = hd / 4, ng = 256 / nd4, d4 = tid % nd4, g = tid / nd4;
+    float4 o[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) o[u] = make_float4(0.f, 0.f, 0.f, 0.f);
     if (g < ng) {
-        for (uint32_t t = g; t < seq; t += ng) {
+        uint32_t t = g;
+        for (; t + 3 * ng < seq; t += 4 * ng) {
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const uint32_t tt = t + u * ng;
+                const float *vr = tt == pos ? vn : vc + (size_t)tt * kvs + kvh * hd;
+                const float4 vv = reinterpret_cast<const float4 *>(vr)[d4];
+                const float p = scores[tt] * inv;
+                o[u].x += p * vv.x; o[u].y += p * vv.y; o[u].z += p * vv.z; o[u].w += p * vv.w;
+            }
+        }
+        for (; t < seq; t += ng) {
             const float *vr = t == pos ? vn : vc + (size_t)t * kvs + kvh * hd;
-            o += (scores[t] * inv) * vr[d];
+            const float4 vv = reinterpret_cast<const float4 *>(vr)[d4];
+            const float p = scores[t] * inv;
+            o[0].x += p * vv.x; o[0].y += p * vv.y; o[0].z += p * vv.z; o[0].w += p * vv.w;
         }
     }
-    part[tid] = o;
+    float4 acc4;
+    acc4.x = (o[0].x + o[1].x) + (o[2].x + o[3].x);
+    acc4.y = (o[0].y + o[1].y) + (o[2].y + o[3].y);
+    acc4.z = (o[0].z + o[1].z) + (o[2].z + o[3].z);
+    acc4.w = (o[0].w + o[1].w) + (o[2].w + o[3].w);
+    if (g < ng) reinterpret_cast<float4 *>(part)[g * nd4 + d4] = acc4;
     __syncthreads();
     if (tid < hd) {
         float acc = 0.f;
@@ -572,6 +597,21 @@ __global__ __launch_bounds__(1024) void argmax_advance_kernel(const float *__res
         out_tokens[pos] = bi;
         ctl[0] = pos + 1;
     }
+}
+
+// Advance the control block from the packed argmax key the lm_head matvec
+// left in *amax (low 32 bits: the winning row).
+__global__ void advance_kernel(const unsigned long long *__restrict__ amax, uint32_t *__restrict__ ctl,
+                               uint32_t *__restrict__ out_tokens) {
+    const uint32_t tok = (uint32_t)(*amax & 0xFFFFFFFFull), pos = ctl[0];
+    ctl[1] = tok;
+    out_tokens[pos] = tok;
+    ctl[0] = pos + 1;
+}
+
+int launch_advance(hipStream_t s, const unsigned long long *amax, uint32_t *ctl, uint32_t *out_tokens) {
+    hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, s, amax, ctl, out_tokens);
+    return check_launch("advance");
 }
 
 int launch_argmax_advance(hipStream_t s, const float *logits, uint32_t n, uint32_t *ctl, uint32_t *out_tokens) {

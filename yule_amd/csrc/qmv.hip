@@ -29,6 +29,8 @@
 // high nibbles masked in place) fold into the block scale.  Biased formats
 // (Q6_K q+32, Q8_0 q+128, Q4_0 nib-8) subtract bias * sum(x) per unit,
 // where sum(x) is computed once per column step.
+#include <type_traits>
+
 #include "blocks.h"
 #include "internal.h"
 
@@ -380,6 +382,14 @@ __device__ __forceinline__ float team_sum(float v) {
     return v;
 }
 
+// Order-preserving map of an f32 onto u32 (larger float -> larger key), so a
+// 64-bit max over (key << 32 | index) is argmax with the last maximal index
+// winning, as argmax_ct does (yule-infer/src/sampler.rs:150-163).
+__device__ __forceinline__ uint32_t argmax_key(float v) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
 // Up to kMaxSegs matrices sharing one activation vector (same n_cols and
 // format) run as one launch over their concatenated rows: Q/K/V, gate/up.
 struct Segs {
@@ -389,15 +399,25 @@ struct Segs {
     uint32_t total;
 };
 
-template <class F, int W, bool STAGE, int D>
+template <class R>
+struct RawPair {
+    R g, u;
+};
+
+// PAIR: segments 0 and 1 are the gate and up matrices (equal row counts);
+// a team computes row r of both and stores silu(g)*u into segment 0's
+// output (model_runner.rs:963-972), so SwiGLU costs nothing extra.
+template <class F, int W, bool STAGE, int D, bool PAIR = false>
 __global__ __launch_bounds__(256) void qmv_stream_kernel(const Segs sg, const float *__restrict__ x, uint32_t bpr,
-                                                         uint32_t early) {
+                                                         uint32_t early, const QmvXf xf) {
+    static_assert(!PAIR || W <= 64, "paired rows need single-wave teams");
     constexpr uint32_t RI = 256 / W;                  // rows per workgroup iteration
     constexpr uint32_t WPT = W >= 64 ? W / 64 : 1;    // waves per team
+    using Buf = typename std::conditional<PAIR, RawPair<typename F::Raw>, typename F::Raw>::type;
     extern __shared__ float xl[];
     __shared__ float part[2][4];
     const uint32_t tid = threadIdx.x, team = tid / W, t = tid % W;
-    const uint32_t units = bpr * F::UPB, n_rows = sg.total;
+    const uint32_t units = bpr * F::UPB, n_rows = PAIR ? sg.start[1] : sg.total;
     const size_t row_bytes = (size_t)bpr * F::BB;
     const bool active = t < units;
     const uint32_t k = active ? t / F::UPB : 0, sub = t % F::UPB;
@@ -416,36 +436,76 @@ __global__ __launch_bounds__(256) void qmv_stream_kernel(const Segs sg, const fl
         for (int i = 1; i < kMaxSegs; i++) s += row >= sg.start[i];
         return s;
     };
-    auto fetch = [&](uint32_t rbase) {
+    auto fetch = [&](uint32_t rbase) -> Buf {
         uint32_t row = rbase + team;
         row = uni(row < n_rows ? row : n_rows - 1);
-        const uint32_t s = seg_of(row);
-        const uint8_t *wb = sg.w[0] - (size_t)sg.start[0] * row_bytes;
+        if constexpr (PAIR) {
+            const size_t off = (size_t)row * row_bytes + (size_t)k * F::BB;
+            return {F::load(sg.w[0] + off, sub), F::load(sg.w[1] + off, sub)};
+        } else {
+            const uint32_t s = seg_of(row);
+            const uint8_t *wb = sg.w[0] - (size_t)sg.start[0] * row_bytes;
 #pragma unroll
-        for (int i = 1; i < kMaxSegs; i++) wb = s == (uint32_t)i ? sg.w[i] - (size_t)sg.start[i] * row_bytes : wb;
-        return F::load(wb + (size_t)row * row_bytes + (size_t)k * F::BB, sub);
+            for (int i = 1; i < kMaxSegs; i++)
+                wb = s == (uint32_t)i ? sg.w[i] - (size_t)sg.start[i] * row_bytes : wb;
+            return F::load(wb + (size_t)row * row_bytes + (size_t)k * F::BB, sub);
+        }
     };
+    unsigned long long best = 0;   // kEpiArgmax: packed (order key << 32 | row), max wins
     auto store = [&](uint32_t row, float v) {
         row = uni(row);
         const uint32_t s = seg_of(row);
         float *yb = sg.y[0] - sg.start[0];
 #pragma unroll
         for (int i = 1; i < kMaxSegs; i++) yb = s == (uint32_t)i ? sg.y[i] - sg.start[i] : yb;
+        if (xf.epi == kEpiAdd) v = yb[row] + v;   // residual + projection (model_runner.rs:782-784)
         yb[row] = v;
+        if (xf.epi == kEpiArgmax) {
+            const unsigned long long key = ((unsigned long long)argmax_key(v) << 32) | row;
+            best = key > best ? key : best;
+        }
     };
 
     // With `early`, the first rows' weight loads go out before the
     // activation vector is staged, so HBM latency overlaps the x load.
-    typename F::Raw buf[D];
+    Buf buf[D];
     if (early) {
 #pragma unroll
         for (int j = 0; j < D - 1; j++)
             if (r0 + j * stride < n_rows) buf[j] = fetch(r0 + j * stride);
     }
     if (STAGE) {
-        const uint32_t n4 = bpr * F::BS / 4;
-        for (uint32_t i = tid; i < n4; i += 256)
-            *reinterpret_cast<float4 *>(xl + lds_pad(4 * i)) = reinterpret_cast<const float4 *>(x)[i];
+        const uint32_t n = bpr * F::BS, n4 = n / 4;
+        const float4 *x4 = reinterpret_cast<const float4 *>(x), *a4 = reinterpret_cast<const float4 *>(xf.a);
+        float inv = 1.0f;
+        if (xf.mode == kXfRmsNorm) {
+            // rms_norm (model_runner.rs:246-275) computed by every workgroup
+            float ss = 0.f;
+            for (uint32_t i = tid; i < n4; i += 256) {
+                const float4 v = x4[i];
+                ss += v.x * v.x; ss += v.y * v.y; ss += v.z * v.z; ss += v.w * v.w;
+            }
+            ss = team_sum<64>(ss);
+            if ((tid & 63) == 0) part[0][tid >> 6] = ss;
+            __syncthreads();
+            ss = part[0][0] + part[0][1] + part[0][2] + part[0][3];
+            inv = 1.0f / sqrtf(ss / (float)n + xf.eps);
+        }
+        for (uint32_t i = tid; i < n4; i += 256) {
+            float4 v = x4[i];
+            if (xf.mode == kXfRmsNorm) {
+                const float4 wv = a4[i];
+                v.x = v.x * inv * wv.x; v.y = v.y * inv * wv.y; v.z = v.z * inv * wv.z; v.w = v.w * inv * wv.w;
+            } else if (xf.mode == kXfSwiGlu) {
+                // gate * sigmoid(gate) * up (model_runner.rs:967-972)
+                const float4 u = a4[i];
+                v.x = v.x * (1.0f / (1.0f + expf(-v.x))) * u.x;
+                v.y = v.y * (1.0f / (1.0f + expf(-v.y))) * u.y;
+                v.z = v.z * (1.0f / (1.0f + expf(-v.z))) * u.z;
+                v.w = v.w * (1.0f / (1.0f + expf(-v.w))) * u.w;
+            }
+            *reinterpret_cast<float4 *>(xl + lds_pad(4 * i)) = v;
+        }
         __syncthreads();
     }
     float xs[F::NX], aux[F::NAUX];
@@ -484,7 +544,31 @@ __global__ __launch_bounds__(256) void qmv_stream_kernel(const Segs sg, const fl
             if (r >= n_rows) break;
             const uint32_t rn = r + (D - 1) * stride;
             if (rn < n_rows) buf[(j + D - 1) % D] = fetch(rn);
-            finish(F::dot(buf[j], sub, xs, aux), r, it++);
+            if constexpr (PAIR) {
+                float g = F::dot(buf[j].g, sub, xs, aux), u = F::dot(buf[j].u, sub, xs, aux);
+                g = team_sum<W>(active ? g : 0.f);
+                u = team_sum<W>(active ? u : 0.f);
+                const uint32_t row = r + team;
+                if (t == 0 && row < n_rows) sg.y[0][row] = g * (1.0f / (1.0f + expf(-g))) * u;
+                it++;
+            } else {
+                finish(F::dot(buf[j], sub, xs, aux), r, it++);
+            }
+        }
+    }
+    if (xf.epi == kEpiArgmax) {   // uniform: one atomic per workgroup
+        __shared__ unsigned long long wbest[4];
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+            const unsigned long long o = __shfl_xor(best, off, 64);
+            best = o > best ? o : best;
+        }
+        if ((tid & 63) == 0) wbest[tid >> 6] = best;
+        __syncthreads();
+        if (tid == 0) {
+            unsigned long long b = wbest[0];
+            for (int i = 1; i < 4; i++) b = wbest[i] > b ? wbest[i] : b;
+            atomicMax(xf.amax, b);
         }
     }
 }
@@ -507,29 +591,39 @@ static int env_int(const char *name, int dflt) {
 }
 
 template <class F, int W, int D>
-static void launch_stream_d(hipStream_t s, const Segs &sg, const float *x, uint32_t bpr, uint32_t blocks) {
+static void launch_stream_d(hipStream_t s, const Segs &sg, const float *x, uint32_t bpr, uint32_t blocks,
+                            const QmvXf &xf) {
+    if constexpr (W <= 64) {
+        if (xf.pair) {
+            const size_t lds = (size_t)lds_pad(bpr * F::BS) * sizeof(float);
+            hipLaunchKernelGGL((qmv_stream_kernel<F, W, true, D, true>), dim3(blocks), dim3(256), lds, s, sg, x, bpr,
+                               0u, xf);
+            return;
+        }
+    }
     static const uint32_t early = (uint32_t)env_int("YULE_QMV_EARLY", 1) - 1;
     constexpr uint32_t RI = 256 / W;
-    if constexpr (RI >= 2) {
+    if (RI >= 2 || xf.mode != kXfNone) {
         const size_t lds = (size_t)lds_pad(bpr * F::BS) * sizeof(float);
-        hipLaunchKernelGGL((qmv_stream_kernel<F, W, true, D>), dim3(blocks), dim3(256), lds, s, sg, x, bpr, early);
+        hipLaunchKernelGGL((qmv_stream_kernel<F, W, true, D>), dim3(blocks), dim3(256), lds, s, sg, x, bpr, early, xf);
     } else {
-        hipLaunchKernelGGL((qmv_stream_kernel<F, W, false, D>), dim3(blocks), dim3(256), 0, s, sg, x, bpr, early);
+        hipLaunchKernelGGL((qmv_stream_kernel<F, W, false, D>), dim3(blocks), dim3(256), 0, s, sg, x, bpr, early, xf);
     }
 }
 
 template <class F, int W>
-static void launch_stream(hipStream_t s, const Segs &sg, const float *x, uint32_t bpr) {
+static void launch_stream(hipStream_t s, const Segs &sg, const float *x, uint32_t bpr, const QmvXf &xf) {
     constexpr uint32_t RI = 256 / W;
     static const int wg = env_int("YULE_QMV_WG_PER_CU", 4), depth = env_int("YULE_QMV_DEPTH", 2);
-    const uint32_t iters = (sg.total + RI - 1) / RI;
+    const uint32_t rows = xf.pair ? sg.start[1] : sg.total;
+    const uint32_t iters = (rows + RI - 1) / RI;
     const uint32_t cap = (uint32_t)(device_cus() * wg);
     const uint32_t blocks = iters < cap ? iters : cap;
     switch (depth) {
-    case 1: return launch_stream_d<F, W, 1>(s, sg, x, bpr, blocks);
-    case 3: return launch_stream_d<F, W, 3>(s, sg, x, bpr, blocks);
-    case 4: return launch_stream_d<F, W, 4>(s, sg, x, bpr, blocks);
-    default: return launch_stream_d<F, W, 2>(s, sg, x, bpr, blocks);
+    case 1: return launch_stream_d<F, W, 1>(s, sg, x, bpr, blocks, xf);
+    case 3: return launch_stream_d<F, W, 3>(s, sg, x, bpr, blocks, xf);
+    case 4: return launch_stream_d<F, W, 4>(s, sg, x, bpr, blocks, xf);
+    default: return launch_stream_d<F, W, 2>(s, sg, x, bpr, blocks, xf);
     }
 }
 
@@ -537,10 +631,16 @@ static void launch_stream(hipStream_t s, const Segs &sg, const float *x, uint32_
 constexpr uint32_t kMaxStageCols = 32768;
 
 template <class F>
-static void launch_fmt(hipStream_t s, const QmvSeg *segs, uint32_t n_seg, const float *x, uint32_t n_cols) {
-    const uint32_t bpr = n_cols / F::BS, units = bpr * F::UPB;
+static bool stream_ok(uint32_t n_cols) {
     static const bool v1 = getenv("YULE_QMV_V1") != nullptr;
-    if (!v1 && units <= 256 && n_cols <= kMaxStageCols) {
+    return !v1 && (n_cols / F::BS) * F::UPB <= 256 && n_cols <= kMaxStageCols;
+}
+
+template <class F>
+static int launch_fmt(hipStream_t s, const QmvSeg *segs, uint32_t n_seg, const float *x, uint32_t n_cols,
+                      const QmvXf &xf) {
+    const uint32_t bpr = n_cols / F::BS, units = bpr * F::UPB;
+    if (stream_ok<F>(n_cols)) {
         Segs sg{};
         uint32_t total = 0;
         for (uint32_t i = 0; i < kMaxSegs; i++) {
@@ -551,12 +651,14 @@ static void launch_fmt(hipStream_t s, const QmvSeg *segs, uint32_t n_seg, const 
         }
         for (uint32_t i = n_seg; i < kMaxSegs; i++) sg.start[i] = total;
         sg.total = total;
-        if (units <= 16) return launch_stream<F, 16>(s, sg, x, bpr);
-        if (units <= 32) return launch_stream<F, 32>(s, sg, x, bpr);
-        if (units <= 64) return launch_stream<F, 64>(s, sg, x, bpr);
-        if (units <= 128) return launch_stream<F, 128>(s, sg, x, bpr);
-        return launch_stream<F, 256>(s, sg, x, bpr);
+        if (units <= 16) return launch_stream<F, 16>(s, sg, x, bpr, xf), YULE_OK;
+        if (units <= 32) return launch_stream<F, 32>(s, sg, x, bpr, xf), YULE_OK;
+        if (units <= 64) return launch_stream<F, 64>(s, sg, x, bpr, xf), YULE_OK;
+        if (units <= 128) return launch_stream<F, 128>(s, sg, x, bpr, xf), YULE_OK;
+        return launch_stream<F, 256>(s, sg, x, bpr, xf), YULE_OK;
     }
+    if (xf.mode != kXfNone || xf.epi != kEpiStore)
+        return set_error(YULE_ERR_UNSUPPORTED, "quantized_matmul: fused transform needs the streaming kernel");
     for (uint32_t i = 0; i < n_seg; i++) {   // one column-looping launch per matrix
         switch (pick_team(units)) {
         case 64: launch_team<F, 64>(s, segs[i].w, x, segs[i].y, segs[i].n_rows, bpr); break;
@@ -564,19 +666,48 @@ static void launch_fmt(hipStream_t s, const QmvSeg *segs, uint32_t n_seg, const 
         default: launch_team<F, 16>(s, segs[i].w, x, segs[i].y, segs[i].n_rows, bpr); break;
         }
     }
+    return YULE_OK;
+}
+
+bool qmv_pairable(uint32_t dtype, uint32_t n_cols) {
+    if (!qmv_fusable(dtype, n_cols)) return false;
+    uint32_t bs, bb;
+    quant_geometry(dtype, &bs, &bb);
+    const uint32_t units = (n_cols / bs) * (dtype == YULE_DTYPE_Q4_K ? 4u : dtype == YULE_DTYPE_Q6_K ? 8u : 1u);
+    return units <= 64;
+}
+
+bool qmv_fusable(uint32_t dtype, uint32_t n_cols) {
+    switch (dtype) {
+    case YULE_DTYPE_Q4_K: return stream_ok<Q4K>(n_cols);
+    case YULE_DTYPE_Q6_K: return stream_ok<Q6K>(n_cols);
+    case YULE_DTYPE_Q8_0: return stream_ok<Q80>(n_cols);
+    case YULE_DTYPE_Q4_0: return stream_ok<Q40>(n_cols);
+    default: return false;
+    }
+}
+
+int launch_qmv_fused(hipStream_t s, uint32_t dtype, const QmvSeg *segs, uint32_t n_seg, const float *x,
+                     uint32_t n_cols, const QmvXf &xf) {
+    if (n_seg == 0 || n_seg > kMaxSegs) return set_error(YULE_ERR_INVALID, "quantized_matmul: bad segment count");
+    if (xf.epi == kEpiArgmax && n_seg != 1)
+        return set_error(YULE_ERR_INVALID, "quantized_matmul: argmax epilogue needs a single matrix");
+    if (xf.pair && (n_seg != 2 || segs[0].n_rows != segs[1].n_rows || !qmv_pairable(dtype, n_cols)))
+        return set_error(YULE_ERR_INVALID, "quantized_matmul: paired gate/up needs two equal single-wave matrices");
+    int rc;
+    switch (dtype) {
+    case YULE_DTYPE_Q4_K: rc = launch_fmt<Q4K>(s, segs, n_seg, x, n_cols, xf); break;
+    case YULE_DTYPE_Q6_K: rc = launch_fmt<Q6K>(s, segs, n_seg, x, n_cols, xf); break;
+    case YULE_DTYPE_Q8_0: rc = launch_fmt<Q80>(s, segs, n_seg, x, n_cols, xf); break;
+    case YULE_DTYPE_Q4_0: rc = launch_fmt<Q40>(s, segs, n_seg, x, n_cols, xf); break;
+    default: return set_error(YULE_ERR_UNSUPPORTED, "quantized_matmul: unsupported dtype");
+    }
+    return rc ? rc : check_launch("quantized_matmul");
 }
 
 int launch_qmv_multi(hipStream_t s, uint32_t dtype, const QmvSeg *segs, uint32_t n_seg, const float *x,
                      uint32_t n_cols) {
-    if (n_seg == 0 || n_seg > kMaxSegs) return set_error(YULE_ERR_INVALID, "quantized_matmul: bad segment count");
-    switch (dtype) {
-    case YULE_DTYPE_Q4_K: launch_fmt<Q4K>(s, segs, n_seg, x, n_cols); break;
-    case YULE_DTYPE_Q6_K: launch_fmt<Q6K>(s, segs, n_seg, x, n_cols); break;
-    case YULE_DTYPE_Q8_0: launch_fmt<Q80>(s, segs, n_seg, x, n_cols); break;
-    case YULE_DTYPE_Q4_0: launch_fmt<Q40>(s, segs, n_seg, x, n_cols); break;
-    default: return set_error(YULE_ERR_UNSUPPORTED, "quantized_matmul: unsupported dtype");
-    }
-    return check_launch("quantized_matmul");
+    return launch_qmv_fused(s, dtype, segs, n_seg, x, n_cols, QmvXf{});
 }
 
 int launch_qmv(hipStream_t s, uint32_t dtype, const uint8_t *w, const float *x, float *y, uint32_t n_rows,

@@ -38,6 +38,8 @@ struct yule_hip_runner {
     float *hidden, *normed, *q, *k, *v, *attn, *proj, *gate, *up, *ffn, *logits;
     uint32_t *ctl = nullptr, *prompt = nullptr, *tokens = nullptr;
     uint32_t *ctl_host = nullptr;  // pinned staging for ctl updates
+    unsigned long long *amax = nullptr;  // lm_head argmax slot (packed key | row)
+    bool fused = false;            // every matrix runs on the streaming matvec
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     uint32_t pos = 0;  // host mirror of ctl[0]
@@ -101,42 +103,104 @@ int upload_matrix(yule_hip_runner *r, const void *src, uint32_t dtype, uint32_t 
 }
 
 // One decode step for the token selected by ctl, entirely on r->be->stream.
+// Per layer, when every matrix runs on the streaming matvec (fusable):
+//   [rms_norm + Q/K/V] [RoPE + KV write + attention] [O + residual]
+//   [rms_norm + gate/up + SwiGLU] [down + residual]
+// (SwiGLU moves into the down launch's staging when gate/up cannot pair)
+// and at the end [rms_norm + lm_head + argmax] [advance]; otherwise the
+// same operations as separate kernels.
 int enqueue_step(yule_hip_runner *r) {
     hipStream_t s = r->be->stream;
     const uint32_t qd = r->n_heads * r->hd, kvd = r->n_kv * r->hd;
     int rc;
-    if ((rc = launch_embed_step(s, r->embd_t, r->embd, r->ctl, r->prompt, r->vocab, r->hidden, r->dim))) return rc;
+    const bool fuse = r->fused;
+    if ((rc = launch_embed_step(s, r->embd_t, r->embd, r->ctl, r->prompt, r->vocab, r->hidden, r->dim,
+                                fuse ? r->amax : nullptr)))
+        return rc;
     for (const auto &L : r->layers) {
         // attention block (model_runner.rs:619-784)
-        if ((rc = launch_rms_norm(s, r->hidden, L.attn_norm, r->normed, r->dim, r->eps))) return rc;
+        QmvXf norm;
+        norm.mode = kXfRmsNorm;
+        norm.a = L.attn_norm;
+        norm.eps = r->eps;
+        const float *xin = r->normed;
+        if (!fuse) {
+            if ((rc = launch_rms_norm(s, r->hidden, L.attn_norm, r->normed, r->dim, r->eps))) return rc;
+            norm = QmvXf{};
+        } else {
+            xin = r->hidden;
+        }
         if (L.tq == L.tk && L.tk == L.tv) {
             const QmvSeg segs[3] = {{L.wq, r->q, qd}, {L.wk, r->k, kvd}, {L.wv, r->v, kvd}};
-            if ((rc = launch_qmv_multi(s, L.tq, segs, 3, r->normed, r->dim))) return rc;
+            if ((rc = launch_qmv_fused(s, L.tq, segs, 3, xin, r->dim, norm))) return rc;
         } else {
-            if ((rc = launch_qmv(s, L.tq, L.wq, r->normed, r->q, qd, r->dim))) return rc;
-            if ((rc = launch_qmv(s, L.tk, L.wk, r->normed, r->k, kvd, r->dim))) return rc;
-            if ((rc = launch_qmv(s, L.tv, L.wv, r->normed, r->v, kvd, r->dim))) return rc;
+            const QmvSeg sq{L.wq, r->q, qd}, sk{L.wk, r->k, kvd}, sv{L.wv, r->v, kvd};
+            if ((rc = launch_qmv_fused(s, L.tq, &sq, 1, xin, r->dim, norm)) ||
+                (rc = launch_qmv_fused(s, L.tk, &sk, 1, xin, r->dim, norm)) ||
+                (rc = launch_qmv_fused(s, L.tv, &sv, 1, xin, r->dim, norm)))
+                return rc;
         }
         if ((rc = launch_attn_step(s, r->q, r->k, r->v, L.kc, L.vc, r->cos_t, r->sin_t, r->ctl, r->attn, r->n_heads,
                                    r->n_kv, r->hd, r->max_seq)))
             return rc;
-        if ((rc = launch_qmv(s, L.to, L.wo, r->attn, r->proj, r->dim, qd))) return rc;
-        if ((rc = launch_eltwise(s, 2, r->hidden, r->proj, r->hidden, r->dim))) return rc;
-        // feed-forward block (model_runner.rs:792-1004)
-        if ((rc = launch_rms_norm(s, r->hidden, L.ffn_norm, r->normed, r->dim, r->eps))) return rc;
-        if (L.tg == L.tu) {
-            const QmvSeg segs[2] = {{L.wg, r->gate, r->ff}, {L.wu, r->up, r->ff}};
-            if ((rc = launch_qmv_multi(s, L.tg, segs, 2, r->normed, r->dim))) return rc;
+        if (fuse) {
+            QmvXf add;
+            add.epi = kEpiAdd;
+            const QmvSeg so{L.wo, r->hidden, r->dim};
+            if ((rc = launch_qmv_fused(s, L.to, &so, 1, r->attn, qd, add))) return rc;
         } else {
-            if ((rc = launch_qmv(s, L.tg, L.wg, r->normed, r->gate, r->ff, r->dim))) return rc;
-            if ((rc = launch_qmv(s, L.tu, L.wu, r->normed, r->up, r->ff, r->dim))) return rc;
+            if ((rc = launch_qmv(s, L.to, L.wo, r->attn, r->proj, r->dim, qd))) return rc;
+            if ((rc = launch_eltwise(s, 2, r->hidden, r->proj, r->hidden, r->dim))) return rc;
         }
-        if ((rc = launch_eltwise(s, 3, r->gate, r->up, r->gate, r->ff))) return rc;
-        if ((rc = launch_qmv(s, L.td, L.wd, r->gate, r->ffn, r->dim, r->ff))) return rc;
-        if ((rc = launch_eltwise(s, 2, r->hidden, r->ffn, r->hidden, r->dim))) return rc;
+        // feed-forward block (model_runner.rs:792-1004)
+        norm = QmvXf{};
+        if (fuse) {
+            norm.mode = kXfRmsNorm;
+            norm.a = L.ffn_norm;
+            norm.eps = r->eps;
+        } else if ((rc = launch_rms_norm(s, r->hidden, L.ffn_norm, r->normed, r->dim, r->eps))) {
+            return rc;
+        }
+        const bool pair = fuse && L.tg == L.tu && qmv_pairable(L.tg, r->dim);
+        if (pair) {   // gate/up + SwiGLU in one launch; act lands in r->gate
+            norm.pair = true;
+            const QmvSeg segs[2] = {{L.wg, r->gate, r->ff}, {L.wu, r->up, r->ff}};
+            if ((rc = launch_qmv_fused(s, L.tg, segs, 2, xin, r->dim, norm))) return rc;
+        } else if (L.tg == L.tu) {
+            const QmvSeg segs[2] = {{L.wg, r->gate, r->ff}, {L.wu, r->up, r->ff}};
+            if ((rc = launch_qmv_fused(s, L.tg, segs, 2, xin, r->dim, norm))) return rc;
+        } else {
+            const QmvSeg sg{L.wg, r->gate, r->ff}, su{L.wu, r->up, r->ff};
+            if ((rc = launch_qmv_fused(s, L.tg, &sg, 1, xin, r->dim, norm)) ||
+                (rc = launch_qmv_fused(s, L.tu, &su, 1, xin, r->dim, norm)))
+                return rc;
+        }
+        if (fuse) {
+            QmvXf sw;
+            sw.mode = pair ? kXfNone : kXfSwiGlu;
+            sw.a = pair ? nullptr : r->up;
+            sw.epi = kEpiAdd;
+            const QmvSeg sd{L.wd, r->hidden, r->dim};
+            if ((rc = launch_qmv_fused(s, L.td, &sd, 1, r->gate, r->ff, sw))) return rc;
+        } else {
+            if ((rc = launch_eltwise(s, 3, r->gate, r->up, r->gate, r->ff))) return rc;
+            if ((rc = launch_qmv(s, L.td, L.wd, r->gate, r->ffn, r->dim, r->ff))) return rc;
+            if ((rc = launch_eltwise(s, 2, r->hidden, r->ffn, r->hidden, r->dim))) return rc;
+        }
     }
-    if ((rc = launch_rms_norm(s, r->hidden, r->out_norm, r->normed, r->dim, r->eps))) return rc;  // :1008-1016
-    if ((rc = launch_qmv(s, r->out_t, r->out_w, r->normed, r->logits, r->vocab, r->dim))) return rc;  // :1019-1025
+    if (fuse) {  // final norm + lm_head + argmax (model_runner.rs:1008-1025, sampler.rs:150-163)
+        QmvXf head;
+        head.mode = kXfRmsNorm;
+        head.a = r->out_norm;
+        head.eps = r->eps;
+        head.epi = kEpiArgmax;
+        head.amax = r->amax;
+        const QmvSeg so{r->out_w, r->logits, r->vocab};
+        if ((rc = launch_qmv_fused(s, r->out_t, &so, 1, r->hidden, r->dim, head))) return rc;
+        return launch_advance(s, r->amax, r->ctl, r->tokens);
+    }
+    if ((rc = launch_rms_norm(s, r->hidden, r->out_norm, r->normed, r->dim, r->eps))) return rc;
+    if ((rc = launch_qmv(s, r->out_t, r->out_w, r->normed, r->logits, r->vocab, r->dim))) return rc;
     return launch_argmax_advance(s, r->logits, r->vocab, r->ctl, r->tokens);
 }
 
@@ -241,6 +305,12 @@ int yule_hip_runner_create(yule_hip_backend *be, const yule_model_desc *d, yule_
         (rc = dev_alloc(r, (size_t)r->max_seq * 4, reinterpret_cast<void **>(&r->prompt))) ||
         (rc = dev_alloc(r, (size_t)r->max_seq * 4, reinterpret_cast<void **>(&r->tokens))))
         return fail(rc);
+    if ((rc = dev_alloc(r, sizeof(unsigned long long), reinterpret_cast<void **>(&r->amax)))) return fail(rc);
+    r->fused = getenv("YULE_RUNNER_UNFUSED") == nullptr && qmv_fusable(r->out_t, r->dim);
+    for (const auto &L : r->layers)
+        r->fused = r->fused && qmv_fusable(L.tq, r->dim) && qmv_fusable(L.tk, r->dim) && qmv_fusable(L.tv, r->dim) &&
+                   qmv_fusable(L.to, qd) && qmv_fusable(L.tg, r->dim) && qmv_fusable(L.tu, r->dim) &&
+                   qmv_fusable(L.td, r->ff);
     if ((rc = hip_error(hipHostMalloc(reinterpret_cast<void **>(&r->ctl_host), 4 * sizeof(uint32_t), 0),
                         "runner: pinned control block")))
         return fail(rc);
