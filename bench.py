@@ -210,6 +210,21 @@ def traffic_from_profiles():
     return None
 
 
+def profile_dominant(hip, n, copies):
+    """Dominant-kernel-only run for hardware-counter collection: N launches of
+    the Q4_K 14336x4096 matvec (kernel launches, no graph) cycling `copies`
+    weight copies, then one 64 MiB buffer copy whose counters calibrate the
+    bytes-per-KiB scale of FETCH_SIZE / WRITE_SIZE."""
+    L = Layer(hip, DType.Q4_K, [("ffn_gate", 14336, 4096)], copies, seed=11)
+    ms = hip.time_qmv_ops(L.ops_for_matrix("ffn_gate", n), 1, use_graph=False)
+    src, dst = hip.allocate(64 << 20), hip.allocate(64 << 20)
+    hip.copy_buffer(src, dst, 64 << 20)
+    hip.synchronize()
+    print(json.dumps({"launches": n, "us_per_launch": round(1e3 * ms / n, 3),
+                      "algo_bytes_per_launch": algo_bytes(DType.Q4_K, 14336, 4096),
+                      "calibration_copy_bytes": 64 << 20}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -220,6 +235,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true",
                     help="launch kernels one by one instead of replaying a HIP graph (for profilers)")
+    ap.add_argument("--profile-dominant", type=int, default=0, metavar="N",
+                    help="only run N launches of the dominant kernel (Q4_K 14336x4096 over rotating copies) and "
+                         "one 64 MiB device copy, for rocprofv3 --pmc runs; prints a JSON line")
     args = ap.parse_args()
     global USE_GRAPH
     USE_GRAPH = not args.no_graph
@@ -231,6 +249,9 @@ def main():
     from yule_amd.backend import HipBackend
     hip = HipBackend(0)
     info = hip.device_info()
+    if args.profile_dominant:
+        profile_dominant(hip, args.profile_dominant, args.copies)
+        return
     log(f"device: {info.name}, {info.compute_units} CUs, {info.memory_bytes / 2**30:.0f} GiB")
 
     log("generating Llama-3-8B Q4_K layer")
