@@ -255,6 +255,12 @@ typedef struct {
 int yule_hip_time_qmv_ops(yule_hip_backend *be, const yule_qmv_op *ops, uint32_t n_ops, uint32_t iters,
                           int use_graph, float *ms_total);
 
+/* Event timer on the backend stream: timer_start records a start event;
+ * timer_stop records a stop event after everything enqueued since, waits
+ * for it and writes the elapsed milliseconds. */
+int yule_hip_timer_start(yule_hip_backend *be);
+int yule_hip_timer_stop(yule_hip_backend *be, float *ms);
+
 #ifdef __cplusplus
 }
 #endif

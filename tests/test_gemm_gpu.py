@@ -1,0 +1,88 @@
+"""Prefill dequant-GEMM (yule_hip_quantized_gemm) on the MFMA units: each row
+of Y must equal the quantized matvec of the same row of X to the matvec bar
+(max|y - y_ref| <= 1e-3 * ||y_ref||_2 / sqrt(N), y_ref the f64 dot of the
+bit-exact dequantized weights with the bf16 row converted exactly to f32)."""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+from refgen import tolerance_bar
+from yule_amd import DType, synth
+from yule_amd.backend import YuleGpuError
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def bf16_bits(x: np.ndarray) -> np.ndarray:
+    """f32 -> bf16 (round to nearest even) as uint16."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def bf16_to_f32(b: np.ndarray) -> np.ndarray:
+    return (b.astype(np.uint32) << 16).view(np.float32)
+
+
+def run_gemm(hip, dt, w, xb, M, N, K):
+    hw, hx, hy = hip.upload(w), hip.upload(xb), hip.allocate(4 * M * N)
+    hip.quantized_gemm(hw, hx, hy, M, N, K, dt)
+    y = hip.download(hy, (M, N))
+    for h in (hw, hx, hy):
+        hip.free(h)
+    return y
+
+
+@pytest.mark.parametrize("dt", [DType.Q4_K, DType.Q6_K], ids=lambda d: d.name)
+@pytest.mark.parametrize("M,N,K", [(1, 128, 256), (7, 300, 512), (64, 256, 1024), (130, 129, 2048), (65, 200, 5632)])
+def test_gemm_rows_match_oracle(hip, dt, M, N, K):
+    say(f"[gemm] {dt.name} M={M} N={N} K={K}")
+    w = synth.gen_quant(dt, 50 + M, N, K)
+    xb = bf16_bits(synth.gauss(60 + K, (M, K)))
+    y = run_gemm(hip, dt, w, xb, M, N, K)
+    xf = bf16_to_f32(xb).reshape(M, K)
+    for m in range(M):
+        ref = oracle.qmv_f64(int(dt), w, xf[m], N, K)
+        assert np.max(np.abs(y[m] - ref)) <= tolerance_bar(ref), f"row {m}"
+
+
+@pytest.mark.parametrize("N,K", [(14336, 4096), (4096, 14336)])
+def test_gemm_config_shapes(hip, N, K):
+    """BASELINE configs[3] shapes at M=64, sampled rows vs the oracle; the
+    remaining rows against the GPU matvec of the same rows."""
+    dt, M = DType.Q4_K, 64
+    say(f"[gemm] Q4_K {N}x{K} M={M}")
+    w = synth.gen_quant(dt, 70, N, K)
+    xb = bf16_bits(synth.gauss(71, (M, K)))
+    y = run_gemm(hip, dt, w, xb, M, N, K)
+    xf = bf16_to_f32(xb).reshape(M, K)
+    for m in (0, 17, 63):
+        ref = oracle.qmv_f64(int(dt), w, xf[m], N, K)
+        assert np.max(np.abs(y[m] - ref)) <= tolerance_bar(ref), f"row {m}"
+    hw, hx, hy = hip.upload(w), hip.allocate(4 * K), hip.allocate(4 * N)
+    for m in range(0, M, 7):
+        hip.copy_to_device(xf[m], hx)
+        hip.quantized_matmul(hw, hx, hy, N, K, dt)
+        mv = hip.download(hy, N)
+        assert np.max(np.abs(y[m] - mv)) <= 2 * tolerance_bar(mv), f"row {m} vs matvec"
+    for h in (hw, hx, hy):
+        hip.free(h)
+
+
+def test_gemm_errors(hip):
+    w = synth.gen_quant(DType.Q4_K, 1, 16, 256)
+    hw, hx, hy = hip.upload(w), hip.allocate(2 * 256 * 4), hip.allocate(4 * 16 * 4)
+    with pytest.raises(YuleGpuError):
+        hip.quantized_gemm(hw, hx, hy, 4, 16, 256, DType.Q4_0)      # not on the MFMA path
+    with pytest.raises(YuleGpuError):
+        hip.quantized_gemm(hw, hx, hy, 5, 16, 256, DType.Q4_K)      # x too small
+    with pytest.raises(YuleGpuError):
+        hip.quantized_gemm(hw, hx, hx, 1, 16, 256, DType.Q4_K)      # x aliases y
+    for h in (hw, hx, hy):
+        hip.free(h)

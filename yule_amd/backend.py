@@ -62,6 +62,8 @@ _SIGS: dict[str, tuple] = {
     "yule_hip_runner_prefill": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p]),
     "yule_hip_runner_generate_greedy": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p,
                                                   C.POINTER(C.c_float)]),
+    "yule_hip_timer_start": (C.c_int, [C.c_void_p]),
+    "yule_hip_timer_stop": (C.c_int, [C.c_void_p, C.POINTER(C.c_float)]),
     "yule_hip_time_qmv_ops": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_int,
                                         C.POINTER(C.c_float)]),
 }
@@ -278,6 +280,15 @@ class HipBackend:
         arr = (QmvOp * len(ops))(*[mk(op) for op in ops])
         ms = C.c_float()
         self._check(self._lib.yule_hip_time_qmv_ops(self._be, arr, len(ops), iters, int(use_graph), C.byref(ms)))
+        return ms.value
+
+    def timer_start(self) -> None:
+        self._check(self._lib.yule_hip_timer_start(self._be))
+
+    def timer_stop(self) -> float:
+        """Milliseconds between timer_start and now, from events on the backend stream."""
+        ms = C.c_float()
+        self._check(self._lib.yule_hip_timer_stop(self._be, C.byref(ms)))
         return ms.value
 
     # -- conveniences ----------------------------------------------------------

@@ -32,6 +32,7 @@ struct yule_hip_backend {
     hipDeviceProp_t props{};
     std::mutex mu;  // guards `buffers`; ComputeBackend is Send + Sync
     std::unordered_map<uint64_t, yule::Buffer> buffers;
+    hipEvent_t timer[2] = {nullptr, nullptr};
 };
 
 namespace yule {

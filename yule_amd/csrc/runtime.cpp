@@ -121,6 +121,8 @@ int yule_hip_destroy(yule_hip_backend *be) {
     hipStreamSynchronize(be->stream);
     for (auto &kv : be->buffers) hipFree(kv.second.ptr);
     be->buffers.clear();
+    for (hipEvent_t e : be->timer)
+        if (e) hipEventDestroy(e);
     hipStreamDestroy(be->stream);
     delete be;
     return YULE_OK;
@@ -374,6 +376,24 @@ int yule_hip_time_qmv_ops(yule_hip_backend *be, const yule_qmv_op *ops, uint32_t
     if (graph) hipGraphDestroy(graph);
     if (!rc) *ms_total = ms;
     return rc;
+}
+
+int yule_hip_timer_start(yule_hip_backend *be) {
+    YULE_CHECK_BE(be);
+    int rc;
+    for (hipEvent_t &e : be->timer)
+        if (!e && (rc = hip_error(hipEventCreate(&e), "timer: event create"))) return rc;
+    return hip_error(hipEventRecord(be->timer[0], be->stream), "timer: record start");
+}
+
+int yule_hip_timer_stop(yule_hip_backend *be, float *ms) {
+    YULE_CHECK_BE(be);
+    if (!ms || !be->timer[0]) return set_error(YULE_ERR_INVALID, "timer_stop: no timer_start");
+    int rc;
+    if ((rc = hip_error(hipEventRecord(be->timer[1], be->stream), "timer: record stop")) ||
+        (rc = hip_error(hipEventSynchronize(be->timer[1]), "timer: synchronize")))
+        return rc;
+    return hip_error(hipEventElapsedTime(ms, be->timer[0], be->timer[1]), "timer: elapsed");
 }
 
 }  // extern "C"
