@@ -60,6 +60,21 @@ __device__ __forceinline__ uint32_t shr64(uint32_t hi, uint32_t lo, uint32_t s) 
 
 constexpr float kTwo24 = 16777216.0f;
 
+// Weight loads; YULE_QMV_NT=1 adds the nontemporal hint (measured slower
+// for this kernel on gfx950, so off by default).
+#ifndef YULE_QMV_NT
+#define YULE_QMV_NT 0
+#endif
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ldw16(const uint8_t *p) {
+    const u32x4 v = YULE_QMV_NT ? __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p))
+                                : *reinterpret_cast<const u32x4 *>(p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint32_t ldw4(const uint32_t *p) {
+    return YULE_QMV_NT ? __builtin_nontemporal_load(p) : *p;
+}
+
 // Activation accessors: float4 at element i (i % 4 == 0) of x, either from
 // global memory or from the LDS copy, which pads 4 floats after every 32 so
 // that lanes reading consecutive unit slices spread over the LDS banks.
@@ -92,9 +107,9 @@ struct Q4K {
     }
     __device__ static Raw load(const uint8_t *__restrict__ blk, uint32_t j) {
         Raw r;
-        r.h = *reinterpret_cast<const uint4 *>(blk);
-        r.qa = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * j);
-        r.qb = *reinterpret_cast<const uint4 *>(blk + 32 + 32 * j);
+        r.h = ldw16(blk);
+        r.qa = ldw16(blk + 16 + 32 * j);
+        r.qb = ldw16(blk + 32 + 32 * j);
         return r;
     }
     __device__ static float dot(const Raw &r, uint32_t j, const float *xs, const float *aux) {
@@ -165,8 +180,8 @@ struct Q6K {
         const uint32_t so = 192 + 8 * h + (p >> 1) + r.ma;   // scale bytes, from b0
         const uint32_t *ps = reinterpret_cast<const uint32_t *>(b0 + (so & ~3u));
 #pragma unroll
-        for (int i = 0; i < 3; i++) { r.a[i] = pa[i]; r.b[i] = pb[i]; r.h[i] = ph[i]; r.s[i] = ps[i]; }
-        r.d = *reinterpret_cast<const uint32_t *>(b0 + 208);
+        for (int i = 0; i < 3; i++) { r.a[i] = ldw4(pa + i); r.b[i] = ldw4(pb + i); r.h[i] = ldw4(ph + i); r.s[i] = ldw4(ps + i); }
+        r.d = ldw4(reinterpret_cast<const uint32_t *>(b0 + 208));
         return r;
     }
     __device__ static float dot(const Raw &r, uint32_t u, const float *xs, const float *aux) {
@@ -225,7 +240,7 @@ struct Q80 {
         r.ma = (uint32_t)(reinterpret_cast<uintptr_t>(blk) & 3u);
         const uint32_t *p = reinterpret_cast<const uint32_t *>(blk - r.ma);
 #pragma unroll
-        for (int i = 0; i < 9; i++) r.w[i] = p[i];
+        for (int i = 0; i < 9; i++) r.w[i] = ldw4(p + i);
         return r;
     }
     __device__ static float dot(const Raw &r, uint32_t, const float *xs, const float *aux) {
@@ -260,7 +275,7 @@ struct Q40 {
         r.ma = (uint32_t)(reinterpret_cast<uintptr_t>(blk) & 3u);
         const uint32_t *p = reinterpret_cast<const uint32_t *>(blk - r.ma);
 #pragma unroll
-        for (int i = 0; i < 5; i++) r.w[i] = p[i];
+        for (int i = 0; i < 5; i++) r.w[i] = ldw4(p + i);
         return r;
     }
     __device__ static float dot(const Raw &r, uint32_t, const float *xs, const float *aux) {
@@ -377,8 +392,15 @@ __device__ __forceinline__ float team_sum(float v) {
     v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
     v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
     v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+    if (W >= 64) {
+        // the four row sums straight into scalar registers (wave-uniform result)
+        const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+        const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+        const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+        const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+        return (r0 + r1) + (r2 + r3);
+    }
     if (W >= 32) v += __shfl_xor(v, 16, 64);
-    if (W >= 64) v += __shfl_xor(v, 32, 64);
     return v;
 }
 
@@ -466,22 +488,35 @@ __global__ __launch_bounds__(256) void qmv_stream_kernel(const Segs sg, const fl
         }
     };
 
-    // With `early`, the first rows' weight loads go out before the
-    // activation vector is staged, so HBM latency overlaps the x load.
+    // Prologue order: this thread's share of x is loaded into registers
+    // first, then the first rows' weight loads are issued, then x goes to
+    // LDS.  Loads complete in issue order, so waiting for x does not wait
+    // for the weights, and HBM latency overlaps the whole staging.
+    constexpr uint32_t kXPer = 8;   // float4 of x per thread held in flight (K <= 8192 in one pass)
     Buf buf[D];
-    if (early) {
-#pragma unroll
-        for (int j = 0; j < D - 1; j++)
-            if (r0 + j * stride < n_rows) buf[j] = fetch(r0 + j * stride);
-    }
     if (STAGE) {
         const uint32_t n = bpr * F::BS, n4 = n / 4;
         const float4 *x4 = reinterpret_cast<const float4 *>(x), *a4 = reinterpret_cast<const float4 *>(xf.a);
+        float4 xv[kXPer];
+#pragma unroll
+        for (uint32_t q = 0; q < kXPer; q++) {
+            const uint32_t i = tid + 256 * q;
+            if (i < n4) xv[q] = x4[i];
+        }
+#pragma unroll
+        for (int j = 0; j < D - 1; j++)
+            if (r0 + j * stride < n_rows) buf[j] = fetch(r0 + j * stride);
         float inv = 1.0f;
         if (xf.mode == kXfRmsNorm) {
             // rms_norm (model_runner.rs:246-275) computed by every workgroup
             float ss = 0.f;
-            for (uint32_t i = tid; i < n4; i += 256) {
+#pragma unroll
+            for (uint32_t q = 0; q < kXPer; q++)
+                if (tid + 256 * q < n4) {
+                    const float4 v = xv[q];
+                    ss += v.x * v.x; ss += v.y * v.y; ss += v.z * v.z; ss += v.w * v.w;
+                }
+            for (uint32_t i = tid + 256 * kXPer; i < n4; i += 256) {
                 const float4 v = x4[i];
                 ss += v.x * v.x; ss += v.y * v.y; ss += v.z * v.z; ss += v.w * v.w;
             }
@@ -491,8 +526,7 @@ __global__ __launch_bounds__(256) void qmv_stream_kernel(const Segs sg, const fl
             ss = part[0][0] + part[0][1] + part[0][2] + part[0][3];
             inv = 1.0f / sqrtf(ss / (float)n + xf.eps);
         }
-        for (uint32_t i = tid; i < n4; i += 256) {
-            float4 v = x4[i];
+        auto put = [&](uint32_t i, float4 v) {
             if (xf.mode == kXfRmsNorm) {
                 const float4 wv = a4[i];
                 v.x = v.x * inv * wv.x; v.y = v.y * inv * wv.y; v.z = v.z * inv * wv.z; v.w = v.w * inv * wv.w;
@@ -505,17 +539,20 @@ __global__ __launch_bounds__(256) void qmv_stream_kernel(const Segs sg, const fl
                 v.w = v.w * (1.0f / (1.0f + expf(-v.w))) * u.w;
             }
             *reinterpret_cast<float4 *>(xl + lds_pad(4 * i)) = v;
-        }
+        };
+#pragma unroll
+        for (uint32_t q = 0; q < kXPer; q++)
+            if (tid + 256 * q < n4) put(tid + 256 * q, xv[q]);
+        for (uint32_t i = tid + 256 * kXPer; i < n4; i += 256) put(i, x4[i]);
         __syncthreads();
-    }
-    float xs[F::NX], aux[F::NAUX];
-    if (STAGE) F::load_x(XLds{xl}, k, sub, xs, aux);
-    else F::load_x(XGlobal{x}, k, sub, xs, aux);
-    if (!early) {
+    } else {
 #pragma unroll
         for (int j = 0; j < D - 1; j++)
             if (r0 + j * stride < n_rows) buf[j] = fetch(r0 + j * stride);
     }
+    float xs[F::NX], aux[F::NAUX];
+    if (STAGE) F::load_x(XLds{xl}, k, sub, xs, aux);
+    else F::load_x(XGlobal{x}, k, sub, xs, aux);
 
     auto finish = [&](float acc, uint32_t rbase, uint32_t it) {
         const uint32_t row = rbase + team;
@@ -552,7 +589,14 @@ __global__ __launch_bounds__(256) void qmv_stream_kernel(const Segs sg, const fl
                 if (t == 0 && row < n_rows) sg.y[0][row] = g * (1.0f / (1.0f + expf(-g))) * u;
                 it++;
             } else {
+#ifdef YULE_QMV_FAKE_DOT
+                const uint32_t *rw = reinterpret_cast<const uint32_t *>(&buf[j]);
+                uint32_t hsh = 0;
+                for (uint32_t q = 0; q < sizeof(buf[j]) / 4; q++) hsh ^= rw[q];
+                finish(__builtin_bit_cast(float, hsh & 0x3F7FFFFFu) + xs[0], r, it++);
+#else
                 finish(F::dot(buf[j], sub, xs, aux), r, it++);
+#endif
             }
         }
     }
@@ -617,8 +661,12 @@ static void launch_stream(hipStream_t s, const Segs &sg, const float *x, uint32_
     static const int wg = env_int("YULE_QMV_WG_PER_CU", 4), depth = env_int("YULE_QMV_DEPTH", 2);
     const uint32_t rows = xf.pair ? sg.start[1] : sg.total;
     const uint32_t iters = (rows + RI - 1) / RI;
+    // persistent grid of at most `wg` workgroups per CU, sized so every
+    // workgroup walks the same number of row iterations (no ragged tail)
     const uint32_t cap = (uint32_t)(device_cus() * wg);
-    const uint32_t blocks = iters < cap ? iters : cap;
+    static const bool balance = env_int("YULE_QMV_BALANCE", 2) == 2;
+    const uint32_t per = (iters + cap - 1) / cap;
+    const uint32_t blocks = balance ? (iters + per - 1) / per : (iters < cap ? iters : cap);
     switch (depth) {
     case 1: return launch_stream_d<F, W, 1>(s, sg, x, bpr, blocks, xf);
     case 3: return launch_stream_d<F, W, 3>(s, sg, x, bpr, blocks, xf);
