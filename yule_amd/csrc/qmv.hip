@@ -437,7 +437,7 @@ __global__ __launch_bounds__(256) void qmv_stream_kernel(const Segs sg, const fl
     constexpr uint32_t WPT = W >= 64 ? W / 64 : 1;    // waves per team
     using Buf = typename std::conditional<PAIR, RawPair<typename F::Raw>, typename F::Raw>::type;
     extern __shared__ float xl[];
-    __shared__ float part[2][4];
+    __shared__ float part[1][4];
     const uint32_t tid = threadIdx.x, team = tid / W, t = tid % W;
     const uint32_t units = bpr * F::UPB, n_rows = PAIR ? sg.start[1] : sg.total;
     const size_t row_bytes = (size_t)bpr * F::BB;
@@ -474,8 +474,9 @@ __global__ __launch_bounds__(256) void qmv_stream_kernel(const Segs sg, const fl
         }
     };
     unsigned long long best = 0;   // kEpiArgmax: packed (order key << 32 | row), max wins
+    // `row` may differ across the lanes of a wave (ring flushes); callers
+    // with a wave-uniform row pass it through uni() first
     auto store = [&](uint32_t row, float v) {
-        row = uni(row);
         const uint32_t s = seg_of(row);
         float *yb = sg.y[0] - sg.start[0];
 #pragma unroll
@@ -554,20 +555,29 @@ __global__ __launch_bounds__(256) void qmv_stream_kernel(const Segs sg, const fl
     if (STAGE) F::load_x(XLds{xl}, k, sub, xs, aux);
     else F::load_x(XGlobal{x}, k, sub, xs, aux);
 
-    auto finish = [&](float acc, uint32_t rbase, uint32_t it) {
-        const uint32_t row = rbase + team;
+    // Teams wider than a wave park per-wave sums in a 16-slot LDS ring and
+    // flush eight row iterations per barrier (all loop control is uniform).
+    __shared__ float ring[16][4];
+    auto finish = [&](float acc, uint32_t rbase, uint32_t it, bool last) {
         acc = team_sum<(W < 64 ? W : 64)>(active ? acc : 0.f);
         if (WPT == 1) {
+            const uint32_t row = uni(rbase + team);
             if (t == 0 && row < n_rows) store(row, acc);
         } else {
-            const uint32_t wave = tid >> 6;
-            if ((tid & 63) == 0) part[it & 1][wave] = acc;
-            __syncthreads();
-            if (t == 0 && row < n_rows) {
-                float s = 0.f;
+            if ((tid & 63) == 0) ring[it & 15][tid >> 6] = acc;
+            if ((it & 7) == 7 || last) {
+                __syncthreads();
+                const uint32_t first = it & ~7u;
+                if (tid < 8 * RI) {
+                    const uint32_t iter = first + tid / RI, tm = tid % RI;
+                    const uint32_t row = r0 + iter * stride + tm;
+                    if (iter <= it && row < n_rows) {
+                        float s = 0.f;
 #pragma unroll
-                for (uint32_t i = 0; i < WPT; i++) s += part[it & 1][wave + i];
-                store(row, s);
+                        for (uint32_t i = 0; i < WPT; i++) s += ring[iter & 15][tm * WPT + i];
+                        store(row, s);
+                    }
+                }
             }
         }
     };
@@ -593,10 +603,11 @@ __global__ __launch_bounds__(256) void qmv_stream_kernel(const Segs sg, const fl
                 const uint32_t *rw = reinterpret_cast<const uint32_t *>(&buf[j]);
                 uint32_t hsh = 0;
                 for (uint32_t q = 0; q < sizeof(buf[j]) / 4; q++) hsh ^= rw[q];
-                finish(__builtin_bit_cast(float, hsh & 0x3F7FFFFFu) + xs[0], r, it++);
+                finish(__builtin_bit_cast(float, hsh & 0x3F7FFFFFu) + xs[0], r, it, r + stride >= n_rows);
 #else
-                finish(F::dot(buf[j], sub, xs, aux), r, it++);
+                finish(F::dot(buf[j], sub, xs, aux), r, it, r + stride >= n_rows);
 #endif
+                it++;
             }
         }
     }
@@ -637,40 +648,35 @@ static int env_int(const char *name, int dflt) {
 template <class F, int W, int D>
 static void launch_stream_d(hipStream_t s, const Segs &sg, const float *x, uint32_t bpr, uint32_t blocks,
                             const QmvXf &xf) {
+    const size_t lds = (size_t)lds_pad(bpr * F::BS) * sizeof(float);
     if constexpr (W <= 64) {
         if (xf.pair) {
-            const size_t lds = (size_t)lds_pad(bpr * F::BS) * sizeof(float);
             hipLaunchKernelGGL((qmv_stream_kernel<F, W, true, D, true>), dim3(blocks), dim3(256), lds, s, sg, x, bpr,
                                0u, xf);
             return;
         }
     }
-    static const uint32_t early = (uint32_t)env_int("YULE_QMV_EARLY", 1) - 1;
-    constexpr uint32_t RI = 256 / W;
-    if (RI >= 2 || xf.mode != kXfNone) {
-        const size_t lds = (size_t)lds_pad(bpr * F::BS) * sizeof(float);
-        hipLaunchKernelGGL((qmv_stream_kernel<F, W, true, D>), dim3(blocks), dim3(256), lds, s, sg, x, bpr, early, xf);
-    } else {
-        hipLaunchKernelGGL((qmv_stream_kernel<F, W, false, D>), dim3(blocks), dim3(256), 0, s, sg, x, bpr, early, xf);
-    }
+    hipLaunchKernelGGL((qmv_stream_kernel<F, W, true, D>), dim3(blocks), dim3(256), lds, s, sg, x, bpr, 0u, xf);
 }
+
+// LDS per CU on gfx950; the staged activation vector bounds how many
+// workgroups can be resident per CU.
+constexpr size_t kLdsPerCu = 160 * 1024;
 
 template <class F, int W>
 static void launch_stream(hipStream_t s, const Segs &sg, const float *x, uint32_t bpr, const QmvXf &xf) {
     constexpr uint32_t RI = 256 / W;
-    static const int wg = env_int("YULE_QMV_WG_PER_CU", 4), depth = env_int("YULE_QMV_DEPTH", 2);
+    static const int wg_env = env_int("YULE_QMV_WG_PER_CU", 4), depth = env_int("YULE_QMV_DEPTH", 2);
+    const size_t lds = (size_t)lds_pad(bpr * F::BS) * sizeof(float) + 512;
+    const int wg_lds = (int)(kLdsPerCu / lds);
+    const int wg = wg_env < wg_lds ? wg_env : (wg_lds > 0 ? wg_lds : 1);
     const uint32_t rows = xf.pair ? sg.start[1] : sg.total;
     const uint32_t iters = (rows + RI - 1) / RI;
-    // persistent grid of at most `wg` workgroups per CU, sized so every
-    // workgroup walks the same number of row iterations (no ragged tail)
     const uint32_t cap = (uint32_t)(device_cus() * wg);
-    static const bool balance = env_int("YULE_QMV_BALANCE", 2) == 2;
-    const uint32_t per = (iters + cap - 1) / cap;
-    const uint32_t blocks = balance ? (iters + per - 1) / per : (iters < cap ? iters : cap);
+    const uint32_t blocks = iters < cap ? iters : cap;
     switch (depth) {
     case 1: return launch_stream_d<F, W, 1>(s, sg, x, bpr, blocks, xf);
     case 3: return launch_stream_d<F, W, 3>(s, sg, x, bpr, blocks, xf);
-    case 4: return launch_stream_d<F, W, 4>(s, sg, x, bpr, blocks, xf);
     default: return launch_stream_d<F, W, 2>(s, sg, x, bpr, blocks, xf);
     }
 }
