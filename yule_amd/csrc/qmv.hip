@@ -33,10 +33,9 @@
 
 #include "blocks.h"
 #include "internal.h"
+#include "qmv_common.h"
 
 namespace yule {
-
-typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ float mix_lo(uint32_t v, float x, float acc) {
     h2_t h = __builtin_bit_cast(h2_t, v);
@@ -46,9 +45,6 @@ __device__ __forceinline__ float mix_hi(uint32_t v, float x, float acc) {
     h2_t h = __builtin_bit_cast(h2_t, v);
     return __builtin_fmaf((float)h.y, x, acc);
 }
-__device__ __forceinline__ float f16_bits(uint32_t b) {
-    return (float)__builtin_bit_cast(_Float16, (uint16_t)(b & 0xFFFFu));
-}
 // dword of bytes [s, s+4) of the little-endian pair {hi:lo}, s in 0..3
 __device__ __forceinline__ uint32_t align_bytes(uint32_t hi, uint32_t lo, uint32_t s) {
     return __builtin_amdgcn_alignbyte(hi, lo, s);
@@ -57,8 +53,6 @@ __device__ __forceinline__ uint32_t align_bytes(uint32_t hi, uint32_t lo, uint32
 __device__ __forceinline__ uint32_t shr64(uint32_t hi, uint32_t lo, uint32_t s) {
     return (uint32_t)((((uint64_t)hi << 32) | lo) >> s);
 }
-
-constexpr float kTwo24 = 16777216.0f;
 
 // Weight loads; YULE_QMV_NT=1 adds the nontemporal hint (measured slower
 // for this kernel on gfx950, so off by default).
@@ -378,7 +372,7 @@ static uint32_t pick_team(uint32_t units) {
 }
 
 // ---------------------------------------------------------------- streaming kernel
-// Rows stream through persistent workgroups.  A team of W lanes (16..256)
+// Rows stream through persistent workgroups.  A team of W lanes (16..512)
 // covers a whole row, one unit per lane, so each lane's activation slice is
 // loaded into registers once for the life of the workgroup; the team then
 // walks rows row0, row0 + stride, ... with the next row's blocks already in
@@ -404,23 +398,6 @@ __device__ __forceinline__ float team_sum(float v) {
     return v;
 }
 
-// Order-preserving map of an f32 onto u32 (larger float -> larger key), so a
-// 64-bit max over (key << 32 | index) is argmax with the last maximal index
-// winning, as argmax_ct does (yule-infer/src/sampler.rs:150-163).
-__device__ __forceinline__ uint32_t argmax_key(float v) {
-    const uint32_t u = __builtin_bit_cast(uint32_t, v);
-    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
-// Up to kMaxSegs matrices sharing one activation vector (same n_cols and
-// format) run as one launch over their concatenated rows: Q/K/V, gate/up.
-struct Segs {
-    const uint8_t *w[kMaxSegs];
-    float *y[kMaxSegs];
-    uint32_t start[kMaxSegs];   // first concatenated row of each segment (unused: = total)
-    uint32_t total;
-};
-
 template <class R>
 struct RawPair {
     R g, u;
@@ -429,15 +406,16 @@ struct RawPair {
 // PAIR: segments 0 and 1 are the gate and up matrices (equal row counts);
 // a team computes row r of both and stores silu(g)*u into segment 0's
 // output (model_runner.rs:963-972), so SwiGLU costs nothing extra.
-template <class F, int W, bool STAGE, int D, bool PAIR = false>
-__global__ __launch_bounds__(256) void qmv_stream_kernel(const Segs sg, const float *__restrict__ x, uint32_t bpr,
-                                                         uint32_t early, const QmvXf xf) {
+template <class F, int W, int D, int NT, bool PAIR = false>
+__global__ __launch_bounds__(NT) void qmv_stream_kernel(const Segs sg, const float *__restrict__ x, uint32_t bpr,
+                                                        const QmvXf xf) {
     static_assert(!PAIR || W <= 64, "paired rows need single-wave teams");
-    constexpr uint32_t RI = 256 / W;                  // rows per workgroup iteration
+    constexpr uint32_t RI = NT / W;                   // rows per workgroup iteration
+    constexpr uint32_t NWV = NT / 64;                 // waves per workgroup
     constexpr uint32_t WPT = W >= 64 ? W / 64 : 1;    // waves per team
     using Buf = typename std::conditional<PAIR, RawPair<typename F::Raw>, typename F::Raw>::type;
     extern __shared__ float xl[];
-    __shared__ float part[1][4];
+    __shared__ float part[NWV];
     const uint32_t tid = threadIdx.x, team = tid / W, t = tid % W;
     const uint32_t units = bpr * F::UPB, n_rows = PAIR ? sg.start[1] : sg.total;
     const size_t row_bytes = (size_t)bpr * F::BB;
@@ -495,13 +473,13 @@ __global__ __launch_bounds__(256) void qmv_stream_kernel(const Segs sg, const fl
     // for the weights, and HBM latency overlaps the whole staging.
     constexpr uint32_t kXPer = 8;   // float4 of x per thread held in flight (K <= 8192 in one pass)
     Buf buf[D];
-    if (STAGE) {
+    {
         const uint32_t n = bpr * F::BS, n4 = n / 4;
         const float4 *x4 = reinterpret_cast<const float4 *>(x), *a4 = reinterpret_cast<const float4 *>(xf.a);
         float4 xv[kXPer];
 #pragma unroll
         for (uint32_t q = 0; q < kXPer; q++) {
-            const uint32_t i = tid + 256 * q;
+            const uint32_t i = tid + NT * q;
             if (i < n4) xv[q] = x4[i];
         }
 #pragma unroll
@@ -513,18 +491,20 @@ __global__ __launch_bounds__(256) void qmv_stream_kernel(const Segs sg, const fl
             float ss = 0.f;
 #pragma unroll
             for (uint32_t q = 0; q < kXPer; q++)
-                if (tid + 256 * q < n4) {
+                if (tid + NT * q < n4) {
                     const float4 v = xv[q];
                     ss += v.x * v.x; ss += v.y * v.y; ss += v.z * v.z; ss += v.w * v.w;
                 }
-            for (uint32_t i = tid + 256 * kXPer; i < n4; i += 256) {
+            for (uint32_t i = tid + NT * kXPer; i < n4; i += NT) {
                 const float4 v = x4[i];
                 ss += v.x * v.x; ss += v.y * v.y; ss += v.z * v.z; ss += v.w * v.w;
             }
             ss = team_sum<64>(ss);
-            if ((tid & 63) == 0) part[0][tid >> 6] = ss;
+            if ((tid & 63) == 0) part[tid >> 6] = ss;
             __syncthreads();
-            ss = part[0][0] + part[0][1] + part[0][2] + part[0][3];
+            ss = 0.f;
+#pragma unroll
+            for (uint32_t i = 0; i < NWV; i++) ss += part[i];
             inv = 1.0f / sqrtf(ss / (float)n + xf.eps);
         }
         auto put = [&](uint32_t i, float4 v) {
@@ -543,21 +523,16 @@ __global__ __launch_bounds__(256) void qmv_stream_kernel(const Segs sg, const fl
         };
 #pragma unroll
         for (uint32_t q = 0; q < kXPer; q++)
-            if (tid + 256 * q < n4) put(tid + 256 * q, xv[q]);
-        for (uint32_t i = tid + 256 * kXPer; i < n4; i += 256) put(i, x4[i]);
+            if (tid + NT * q < n4) put(tid + NT * q, xv[q]);
+        for (uint32_t i = tid + NT * kXPer; i < n4; i += NT) put(i, x4[i]);
         __syncthreads();
-    } else {
-#pragma unroll
-        for (int j = 0; j < D - 1; j++)
-            if (r0 + j * stride < n_rows) buf[j] = fetch(r0 + j * stride);
     }
     float xs[F::NX], aux[F::NAUX];
-    if (STAGE) F::load_x(XLds{xl}, k, sub, xs, aux);
-    else F::load_x(XGlobal{x}, k, sub, xs, aux);
+    F::load_x(XLds{xl}, k, sub, xs, aux);
 
     // Teams wider than a wave park per-wave sums in a 16-slot LDS ring and
     // flush eight row iterations per barrier (all loop control is uniform).
-    __shared__ float ring[16][4];
+    __shared__ float ring[16][NWV];
     auto finish = [&](float acc, uint32_t rbase, uint32_t it, bool last) {
         acc = team_sum<(W < 64 ? W : 64)>(active ? acc : 0.f);
         if (WPT == 1) {
@@ -612,7 +587,7 @@ __global__ __launch_bounds__(256) void qmv_stream_kernel(const Segs sg, const fl
         }
     }
     if (xf.epi == kEpiArgmax) {   // uniform: one atomic per workgroup
-        __shared__ unsigned long long wbest[4];
+        __shared__ unsigned long long wbest[NWV];
 #pragma unroll
         for (int off = 32; off >= 1; off >>= 1) {
             const unsigned long long o = __shfl_xor(best, off, 64);
@@ -622,63 +597,53 @@ __global__ __launch_bounds__(256) void qmv_stream_kernel(const Segs sg, const fl
         __syncthreads();
         if (tid == 0) {
             unsigned long long b = wbest[0];
-            for (int i = 1; i < 4; i++) b = wbest[i] > b ? wbest[i] : b;
+            for (uint32_t i = 1; i < NWV; i++) b = wbest[i] > b ? wbest[i] : b;
             atomicMax(xf.amax, b);
         }
     }
 }
 
-static int g_cus = 0;
-static int device_cus() {
-    if (!g_cus) {
-        int dev = 0, n = 0;
-        (void)hipGetDevice(&dev);
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-        g_cus = n;
-    }
-    return g_cus;
-}
-
-static int env_int(const char *name, int dflt) {
-    const char *e = getenv(name);
-    const int v = e ? atoi(e) : dflt;
-    return v > 0 ? v : dflt;
-}
-
-template <class F, int W, int D>
+template <class F, int W, int D, int NT>
 static void launch_stream_d(hipStream_t s, const Segs &sg, const float *x, uint32_t bpr, uint32_t blocks,
                             const QmvXf &xf) {
     const size_t lds = (size_t)lds_pad(bpr * F::BS) * sizeof(float);
     if constexpr (W <= 64) {
         if (xf.pair) {
-            hipLaunchKernelGGL((qmv_stream_kernel<F, W, true, D, true>), dim3(blocks), dim3(256), lds, s, sg, x, bpr,
-                               0u, xf);
+            hipLaunchKernelGGL((qmv_stream_kernel<F, W, D, NT, true>), dim3(blocks), dim3(NT), lds, s, sg, x, bpr,
+                               xf);
             return;
         }
     }
-    hipLaunchKernelGGL((qmv_stream_kernel<F, W, true, D>), dim3(blocks), dim3(256), lds, s, sg, x, bpr, 0u, xf);
+    hipLaunchKernelGGL((qmv_stream_kernel<F, W, D, NT>), dim3(blocks), dim3(NT), lds, s, sg, x, bpr, xf);
 }
 
-// LDS per CU on gfx950; the staged activation vector bounds how many
-// workgroups can be resident per CU.
-constexpr size_t kLdsPerCu = 160 * 1024;
-
-template <class F, int W>
-static void launch_stream(hipStream_t s, const Segs &sg, const float *x, uint32_t bpr, const QmvXf &xf) {
-    constexpr uint32_t RI = 256 / W;
-    static const int wg_env = env_int("YULE_QMV_WG_PER_CU", 4), depth = env_int("YULE_QMV_DEPTH", 2);
+// Workgroup shape: NT threads (RI = NT / W teams) share one LDS copy of the
+// activation vector; about 16 waves per CU are resident (4 per SIMD, the
+// VGPR limit), as NT-thread workgroups up to the LDS each copy takes.
+template <class F, int W, int NT>
+static void launch_stream_nt(hipStream_t s, const Segs &sg, const float *x, uint32_t bpr, const QmvXf &xf) {
+    constexpr uint32_t RI = NT / W;
+    static const int waves_env = env_int("YULE_QMV_WAVES_PER_CU", 16);
     const size_t lds = (size_t)lds_pad(bpr * F::BS) * sizeof(float) + 512;
     const int wg_lds = (int)(kLdsPerCu / lds);
-    const int wg = wg_env < wg_lds ? wg_env : (wg_lds > 0 ? wg_lds : 1);
+    const int wg_waves = waves_env / (NT / 64) > 0 ? waves_env / (NT / 64) : 1;
+    const int wg = wg_waves < wg_lds ? wg_waves : (wg_lds > 0 ? wg_lds : 1);
     const uint32_t rows = xf.pair ? sg.start[1] : sg.total;
     const uint32_t iters = (rows + RI - 1) / RI;
     const uint32_t cap = (uint32_t)(device_cus() * wg);
     const uint32_t blocks = iters < cap ? iters : cap;
-    switch (depth) {
-    case 1: return launch_stream_d<F, W, 1>(s, sg, x, bpr, blocks, xf);
-    case 3: return launch_stream_d<F, W, 3>(s, sg, x, bpr, blocks, xf);
-    default: return launch_stream_d<F, W, 2>(s, sg, x, bpr, blocks, xf);
-    }
+    launch_stream_d<F, W, 2, NT>(s, sg, x, bpr, blocks, xf);
+}
+
+template <class F, int W>
+static void launch_stream(hipStream_t s, const Segs &sg, const float *x, uint32_t bpr, const QmvXf &xf) {
+    static const int nt_narrow = env_int("YULE_QMV_NT", 256), nt_wide = env_int("YULE_QMV_NT_WIDE", 1024);
+    const int nt = W >= 512 ? 1024 : W >= 128 ? nt_wide : nt_narrow;
+    if (nt >= 1024) return launch_stream_nt<F, W, 1024>(s, sg, x, bpr, xf);
+    if constexpr (W >= 512) return;   // unreachable: 512-lane teams only run in 1024-thread workgroups
+    else
+    if (nt >= 512) return launch_stream_nt<F, W, 512>(s, sg, x, bpr, xf);
+    else launch_stream_nt<F, W, 256>(s, sg, x, bpr, xf);
 }
 
 // Largest activation vector staged in LDS by the streaming kernel (floats).
@@ -687,7 +652,7 @@ constexpr uint32_t kMaxStageCols = 32768;
 template <class F>
 static bool stream_ok(uint32_t n_cols) {
     static const bool v1 = getenv("YULE_QMV_V1") != nullptr;
-    return !v1 && (n_cols / F::BS) * F::UPB <= 256 && n_cols <= kMaxStageCols;
+    return !v1 && (n_cols / F::BS) * F::UPB <= 512 && n_cols <= kMaxStageCols;
 }
 
 template <class F>
@@ -709,7 +674,8 @@ static int launch_fmt(hipStream_t s, const QmvSeg *segs, uint32_t n_seg, const f
         if (units <= 32) return launch_stream<F, 32>(s, sg, x, bpr, xf), YULE_OK;
         if (units <= 64) return launch_stream<F, 64>(s, sg, x, bpr, xf), YULE_OK;
         if (units <= 128) return launch_stream<F, 128>(s, sg, x, bpr, xf), YULE_OK;
-        return launch_stream<F, 256>(s, sg, x, bpr, xf), YULE_OK;
+        if (units <= 256) return launch_stream<F, 256>(s, sg, x, bpr, xf), YULE_OK;
+        return launch_stream<F, 512>(s, sg, x, bpr, xf), YULE_OK;
     }
     if (xf.mode != kXfNone || xf.epi != kEpiStore)
         return set_error(YULE_ERR_UNSUPPORTED, "quantized_matmul: fused transform needs the streaming kernel");

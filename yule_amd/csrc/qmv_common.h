@@ -1,0 +1,55 @@
+// qmv_common.h — pieces shared by the matvec kernels (qmv.hip).
+#pragma once
+
+#include <cstdlib>
+
+#include "internal.h"
+
+namespace yule {
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float f16_bits(uint32_t b) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(b & 0xFFFFu));
+}
+constexpr float kTwo24 = 16777216.0f;
+
+// Order-preserving map of an f32 onto u32 (larger float -> larger key), so a
+// 64-bit max over (key << 32 | index) is argmax with the last maximal index
+// winning, as argmax_ct does (yule-infer/src/sampler.rs:150-163).
+__device__ __forceinline__ uint32_t argmax_key(float v) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Up to kMaxSegs matrices sharing one activation vector (same n_cols and
+// format) run as one launch over their concatenated rows: Q/K/V, gate/up.
+struct Segs {
+    const uint8_t *w[kMaxSegs];
+    float *y[kMaxSegs];
+    uint32_t start[kMaxSegs];   // first concatenated row of each segment (unused: = total)
+    uint32_t total;
+};
+
+static inline int device_cus() {
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0, n = 0;
+        (void)hipGetDevice(&dev);
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus = n;
+    }
+    return cus;
+}
+
+// positive integer from the environment, else dflt (tuning knobs)
+static inline int env_int(const char *name, int dflt) {
+    const char *e = getenv(name);
+    const int v = e ? atoi(e) : dflt;
+    return v > 0 ? v : dflt;
+}
+
+// LDS per CU on gfx950
+constexpr size_t kLdsPerCu = 160 * 1024;
+
+}  // namespace yule
