@@ -4,11 +4,14 @@
 // (yule-infer/src/model_runner.rs:1075-1081); each row of Y equals one
 // quantized_matmul of the corresponding row of X (parity target).
 //
-// Exactness: weights enter the MFMA as f16 holding exact integers and every
-// scale is applied in f32, so the only roundings are f32 accumulations.
-//  * Q4_K, w = d*sc*q - dmin*mn: the B operand is sc*q (integers <= 945,
-//    exact in f16; bf16 would round them).  A 16x16 tile accumulates one
-//    super-block (256 k) into a temporary, then final += d * tmp in f32.
+// Exactness: weights enter the MFMA as f16 holding exact integers (times a
+// power of two) and every scale is applied in f32, so the only roundings are
+// f32 accumulations.
+//  * Q4_K, w = d*sc*q - dmin*mn: the B operand is sc*q*2^-14 (sc*q <= 945,
+//    exact in f16), made with one v_pk_mul_f16 per two weights: the nibble
+//    pair masked into a dword is the f16 denormal pair q*2^-24, times
+//    (sc*2^10, sc*2^10).  A 16x16 tile accumulates one super-block (256 k)
+//    into a temporary, then final += (d*2^14) * tmp in f32.
 //    The min term sum_sub (dmin*mn)*(sum of x over the sub-block) is a
 //    second, small MFMA product over K/32 sub-blocks with both operands
 //    split into hi + lo f16 pairs (dmin*mn is an exact 17-bit f32 value);
@@ -16,215 +19,304 @@
 //  * Q6_K, w = d*sc*(q-32): the B operand is sc*(q-32) (|.| <= 4064; exact
 //    up to 2048, above that rounded to the nearest even integer, i.e.
 //    < 2.5e-4 relative on those few weights), d applied per super-block.
-//  * X: bf16 -> f16 is exact for every bf16 in f16's normal range.
+//  * X: bf16 -> f16 is exact for every bf16 in f16's normal range.  A pre-pass
+//    converts X once per call (not once per weight tile) and stores each group
+//    of four k in the order {0,2,1,3}, the order in which the dword nibble
+//    masks deliver weights, so neither side is shuffled in the main loop.
 //
-// Tiling: a 256-thread workgroup computes a 128 (m) x 128 (r) tile; each of
-// its four waves a 64 x 64 sub-tile of 4 x 4 MFMA 16x16x32 tiles.  Per step
-// of 128 k (half a super-block) the workgroup dequantizes its 128 weight
-// rows into LDS as f16 and converts its 128 x 128 X tile into LDS; rows are
-// padded by 16 bytes so the ds_read_b128 operand loads avoid bank conflicts.
+#include <mutex>
 #include <string>
 
-#include "internal.h"
+#include "qmv_common.h"
 
 namespace yule {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-constexpr int GBM = 128, GBN = 128, GBK = 128;
-constexpr int LDW = GBK + 8;   // padded row stride in halves
+// Tiling: a 256-thread workgroup computes a BM (m) x 128 (r) tile; each of
+// its four waves a BM/2 x 64 sub-tile of MFMA 16x16x32 tiles.  K advances in
+// stages of 64 (a quarter super-block): X and weight bytes of stage s+2 are
+// loaded into registers while stage s runs on the MFMAs out of one LDS buffer
+// and stage s+1 is dequantized into the other, one barrier per stage.  LDS
+// rows are padded to 72 halves (36 dwords: 16 consecutive rows of a
+// ds_read_b128 land on distinct banks).
+constexpr int GBN = 128, GSK = 64, GLD = GSK + 8;
 
 __device__ __forceinline__ _Float16 bf16_to_f16(uint16_t b) {
     return (_Float16)__builtin_bit_cast(float, (uint32_t)b << 16);
 }
 
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pk_scale(uint32_t pair, h2v s) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2v, pair) * s);
+}
+
 // n bytes starting at p (only 2-byte aligned) as n/4 little-endian dwords,
-// read through 4-byte-aligned loads (the backend pads every allocation).
+// from the raw 4-byte-aligned window raw[] (the backend pads every allocation).
 template <int N>
-__device__ __forceinline__ void load_words(const uint8_t *p, uint32_t *out) {
-    const uint32_t mis = (uint32_t)(reinterpret_cast<uintptr_t>(p) & 3u);
+__device__ __forceinline__ void load_raw(const uint8_t *p, uint32_t *raw, uint32_t &mis) {
+    mis = (uint32_t)(reinterpret_cast<uintptr_t>(p) & 3u);
     const uint32_t *w = reinterpret_cast<const uint32_t *>(p - mis);
-    uint32_t raw[N / 4 + 1];
 #pragma unroll
     for (int i = 0; i < N / 4 + 1; i++) raw[i] = w[i];
+}
+template <int N>
+__device__ __forceinline__ void align_raw(const uint32_t *raw, uint32_t mis, uint32_t *out) {
 #pragma unroll
     for (int i = 0; i < N / 4; i++) out[i] = __builtin_amdgcn_alignbyte(raw[i + 1], raw[i], mis);
 }
 
-// sum over each 32-column sub-block of X, split into f16 hi + lo:
-// xs_hi/lo[m][j] for j < K/32
-__global__ void xsum_kernel(const uint16_t *__restrict__ x, _Float16 *__restrict__ hi, _Float16 *__restrict__ lo,
-                            uint32_t M, uint32_t K) {
+// X pre-pass, one thread per (row m, 32-column sub-block j): bf16 -> f16 with
+// each group of four k stored as {0,2,1,3}; optionally the sub-block sums of
+// X split into f16 hi + lo (the Q4_K min term).
+__global__ void gemm_xprep_kernel(const uint16_t *__restrict__ x, _Float16 *__restrict__ xh,
+                                  _Float16 *__restrict__ hi, _Float16 *__restrict__ lo, uint32_t M, uint32_t K) {
     const uint32_t nsub = K / 32;
     const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (uint64_t)M * nsub) return;
     const uint32_t m = (uint32_t)(i / nsub), j = (uint32_t)(i % nsub);
-    const uint16_t *p = x + (size_t)m * K + 32 * j;
+    const size_t o = (size_t)m * K + 32 * j;
+    const uint4 *p = reinterpret_cast<const uint4 *>(x + o);
+    uint4 *q = reinterpret_cast<uint4 *>(xh + o);
     float s = 0.f;
 #pragma unroll
-    for (int c = 0; c < 32; c++) s += __builtin_bit_cast(float, (uint32_t)p[c] << 16);
-    const _Float16 h = (_Float16)s;
-    hi[i] = h;
-    lo[i] = (_Float16)(s - (float)h);
+    for (int c = 0; c < 4; c++) {   // 8 elements: two groups of four
+        const uint4 v = p[c];
+        const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+        uint16_t e[8];
+#pragma unroll
+        for (int t = 0; t < 4; t++) { e[2 * t] = (uint16_t)(wv[t] & 0xFFFFu); e[2 * t + 1] = (uint16_t)(wv[t] >> 16); }
+#pragma unroll
+        for (int t = 0; t < 8; t++) s += __builtin_bit_cast(float, (uint32_t)e[t] << 16);
+        const int perm[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+        uint32_t outw[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+            outw[t] = (uint32_t)__builtin_bit_cast(uint16_t, bf16_to_f16(e[perm[2 * t]])) |
+                      ((uint32_t)__builtin_bit_cast(uint16_t, bf16_to_f16(e[perm[2 * t + 1]])) << 16);
+        q[c] = make_uint4(outw[0], outw[1], outw[2], outw[3]);
+    }
+    if (hi) {
+        const _Float16 h = (_Float16)s;
+        hi[i] = h;
+        lo[i] = (_Float16)(s - (float)h);
+    }
 }
 
-template <uint32_t DT>
-__global__ __launch_bounds__(256) void gemm_kernel(const uint8_t *__restrict__ w, const uint16_t *__restrict__ x,
-                                                   float *__restrict__ y, const _Float16 *__restrict__ xs_hi,
-                                                   const _Float16 *__restrict__ xs_lo, uint32_t M, uint32_t N,
-                                                   uint32_t K) {
-    constexpr uint32_t BB = DT == YULE_DTYPE_Q4_K ? 144 : 210;
-    __shared__ __align__(16) _Float16 sx[GBM * LDW];
-    __shared__ __align__(16) _Float16 sw[GBN * LDW];
-    __shared__ float sd[GBN];
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t wm = wave >> 1, wn = wave & 1;
-    const uint32_t m0 = blockIdx.y * GBM, r0 = blockIdx.x * GBN;
-    const uint32_t bpr = K / 256;
-    const size_t row_bytes = (size_t)bpr * BB;
+// Per-stage register staging of one thread: XCH 16-byte chunks of X and the
+// thread's weight bytes (Q4_K: header + 16 qs bytes; Q6_K: raw dword windows
+// of 32 ql bytes, 32 qh bytes, two scales and d).
+template <uint32_t DT, int XCH>
+struct GemmRegs {
+    uint4 x[XCH];
+    uint4 h, q;
+    uint32_t ql[9], qh[9], sc[2], d[2];
+    uint32_t mql, mqh, msc, md;
+};
 
-    floatx4 acc[4][4], tmp[4][4];
+// Split-K: workgroup z of gridDim.z takes super-blocks [kb_lo, kb_hi) and,
+// when gridDim.z > 1, writes its partial tile to y + z*M*N (summed in a
+// fixed order by gemm_reduce_kernel, so results do not depend on timing).
+// Q4_K runs two waves per SIMD (the register budget holds with a few spilled
+// bytes); Q6_K's larger dequant state keeps it at one.
+template <uint32_t DT, int BM>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DT == YULE_DTYPE_Q4_K ? 2 : 1))) void gemm_kernel(
+    const uint8_t *__restrict__ w, const _Float16 *__restrict__ xh, float *__restrict__ y,
+    const _Float16 *__restrict__ xs_hi, const _Float16 *__restrict__ xs_lo, uint32_t M, uint32_t N, uint32_t K) {
+    constexpr bool Q4 = DT == YULE_DTYPE_Q4_K;
+    constexpr uint32_t BB = Q4 ? 144 : 210;
+    constexpr int TM = BM / 32;                 // 16-row MFMA tiles per wave along m
+    constexpr int XCH = BM * GSK / 8 / 256;     // 16-byte X chunks per thread per stage
+    __shared__ __align__(16) _Float16 sx[2][BM * GLD];
+    __shared__ __align__(16) _Float16 sw[2][GBN * GLD];
+    __shared__ float sd[2][GBN];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t wm = wave >> 1, wn = wave & 1u;
+    const uint32_t m0 = blockIdx.y * BM, r0 = blockIdx.x * GBN;
+    const uint32_t bpr = K / 256;
+    const uint32_t kb_lo = (uint32_t)((uint64_t)bpr * blockIdx.z / gridDim.z);
+    const uint32_t kb_hi = (uint32_t)((uint64_t)bpr * (blockIdx.z + 1) / gridDim.z);
+    const uint32_t S = 4 * (kb_hi - kb_lo);     // stages of this split (>= 4)
+    const size_t row_bytes = (size_t)bpr * BB;
+    if (gridDim.z > 1) y += (size_t)blockIdx.z * M * N;
+
+    floatx4 acc[TM][4], tmp[TM][4];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++) { acc[i][j] = floatx4{0, 0, 0, 0}; tmp[i][j] = floatx4{0, 0, 0, 0}; }
 
-    // weight-dequant role: two threads per weight row, 64 weights each
-    const uint32_t wr = tid >> 1, part = tid & 1;
+    // weight role: two threads per weight row, 32 weights of the stage each
+    const uint32_t wr = tid >> 1, part = tid & 1u;
     const bool wrow_ok = r0 + wr < N;
     const uint8_t *wrow = w + (size_t)(wrow_ok ? r0 + wr : 0) * row_bytes;
 
-    for (uint32_t kb = 0; kb < bpr; kb++) {
-        for (uint32_t hs = 0; hs < 2; hs++) {   // the two 128-k halves of super-block kb
-            const uint32_t k0 = kb * 256 + hs * 128;
-            // ---- X tile -> LDS (bf16 -> f16, exact)
+    auto load_stage = [&](uint32_t s, GemmRegs<DT, XCH> &R) {
+        const uint32_t kb = kb_lo + (s >> 2), st = s & 3u, k0 = kb * 256u + st * GSK;
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const uint32_t idx = tid + 256 * i;            // 2048 chunks of 8 halves
-                const uint32_t mr = idx >> 4, c8 = idx & 15;
-                uint4 v = make_uint4(0, 0, 0, 0);
-                if (m0 + mr < M) v = *reinterpret_cast<const uint4 *>(x + (size_t)(m0 + mr) * K + k0 + 8 * c8);
-                half8 h;
-                const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+        for (int i = 0; i < XCH; i++) {
+            const uint32_t idx = tid + 256u * i, row = idx >> 3, c = idx & 7u;
+            const uint32_t m = m0 + row < M ? m0 + row : M - 1u;
+            R.x[i] = *reinterpret_cast<const uint4 *>(xh + (size_t)m * K + k0 + 8u * c);
+        }
+        const uint8_t *blk = wrow + (size_t)kb * BB;
+        if constexpr (Q4) {
+            R.h = *reinterpret_cast<const uint4 *>(blk);
+            R.q = *reinterpret_cast<const uint4 *>(blk + 16u + 32u * st + 16u * part);
+        } else {
+            const uint32_t h = st >> 1, g = 2u * (st & 1u) + part;
+            load_raw<32>(blk + 64u * h + 32u * part, R.ql, R.mql);
+            load_raw<32>(blk + 128u + 32u * h, R.qh, R.mqh);
+            load_raw<4>(blk + 192u + 8u * h + 2u * g, R.sc, R.msc);
+            load_raw<4>(blk + 208u, R.d, R.md);
+        }
+    };
+
+    auto dequant_stage = [&](uint32_t s, const GemmRegs<DT, XCH> &R, int b) {
+        const uint32_t kb = s >> 2, st = s & 3u;   // kb relative to the split (LDS slot parity only)
 #pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    h[2 * q] = bf16_to_f16((uint16_t)(wv[q] & 0xFFFFu));
-                    h[2 * q + 1] = bf16_to_f16((uint16_t)(wv[q] >> 16));
-                }
-                *reinterpret_cast<half8 *>(sx + mr * LDW + 8 * c8) = h;
+        for (int i = 0; i < XCH; i++) {
+            const uint32_t idx = tid + 256u * i, row = idx >> 3, c = idx & 7u;
+            *reinterpret_cast<uint4 *>(sx[b] + row * GLD + 8u * c) = m0 + row < M ? R.x[i] : make_uint4(0, 0, 0, 0);
+        }
+        _Float16 *dst = sw[b] + wr * GLD;
+        uint4 o[4];
+        if constexpr (Q4) {
+            // 6-bit scales of sub-blocks 2st (low nibbles) and 2st+1 (high),
+            // get_scale_min_k4 (dequant.rs:176-190)
+            const uint4 hd = R.h;
+            const uint32_t sh = (st & 1u) << 4;
+            const bool low = st < 2;
+            const uint32_t A = low ? hd.y : hd.w;
+            const uint32_t mA = low ? 0x3F3Fu : 0x0F0Fu, mB = low ? 0u : 0x3030u;
+            const uint32_t scs = ((A >> sh) & mA) | ((hd.y >> (sh + 2)) & mB);
+            const _Float16 f0 = (_Float16)(float)((scs & 0xFFu) * 1024u);
+            const _Float16 f1 = (_Float16)(float)((scs >> 8) * 1024u);
+            const h2v S0 = {f0, f0}, S1 = {f1, f1};
+            const uint32_t q[4] = {R.q.x, R.q.y, R.q.z, R.q.w};
+            uint32_t lo[8], hi[8];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t v = q[i], v4 = v >> 4;
+                lo[2 * i] = pk_scale(v & 0x000F000Fu, S0);
+                lo[2 * i + 1] = pk_scale((v >> 8) & 0x000F000Fu, S0);
+                hi[2 * i] = pk_scale(v4 & 0x000F000Fu, S1);
+                hi[2 * i + 1] = pk_scale((v4 >> 8) & 0x000F000Fu, S1);
             }
-            // ---- W tile -> LDS as exact integer f16
-            const uint8_t *blk = wrow + (size_t)kb * BB;
-            _Float16 *dst = sw + wr * LDW;
-            if constexpr (DT == YULE_DTYPE_Q4_K) {
-                // this thread: qs group j = 2*hs + part -> sub-blocks 2j (low) and 2j+1 (high)
-                const uint32_t j = 2 * hs + part;
-                uint32_t hd[4], qs[8];
-                const uint4 h4 = *reinterpret_cast<const uint4 *>(blk);
-                hd[0] = h4.x; hd[1] = h4.y; hd[2] = h4.z; hd[3] = h4.w;
-                const uint4 qa = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * j);
-                const uint4 qb = *reinterpret_cast<const uint4 *>(blk + 32 + 32 * j);
-                qs[0] = qa.x; qs[1] = qa.y; qs[2] = qa.z; qs[3] = qa.w;
-                qs[4] = qb.x; qs[5] = qb.y; qs[6] = qb.z; qs[7] = qb.w;
-                const uint8_t *sb = reinterpret_cast<const uint8_t *>(hd) + 4;
-                uint32_t sc0, sc1;
-                const uint32_t s0 = 2 * j, s1 = 2 * j + 1;
-                sc0 = s0 < 4 ? (sb[s0] & 63u) : ((sb[s0 + 4] & 0xFu) | ((uint32_t)(sb[s0 - 4] >> 6) << 4));
-                sc1 = s1 < 4 ? (sb[s1] & 63u) : ((sb[s1 + 4] & 0xFu) | ((uint32_t)(sb[s1 - 4] >> 6) << 4));
-                const _Float16 f0 = (_Float16)(float)sc0, f1 = (_Float16)(float)sc1;
-                half8 lo8, hi8;
+            o[0] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+            o[1] = make_uint4(lo[4], lo[5], lo[6], lo[7]);
+            o[2] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+            o[3] = make_uint4(hi[4], hi[5], hi[6], hi[7]);
+            if (!wrow_ok) o[0] = o[1] = o[2] = o[3] = make_uint4(0, 0, 0, 0);
+            // this thread's 16 bytes: k = 16 part + 0..15 (low), 32 + 16 part + 0..15 (high)
+            *reinterpret_cast<uint4 *>(dst + 16u * part) = o[0];
+            *reinterpret_cast<uint4 *>(dst + 16u * part + 8u) = o[1];
+            *reinterpret_cast<uint4 *>(dst + 32u + 16u * part) = o[2];
+            *reinterpret_cast<uint4 *>(dst + 32u + 16u * part + 8u) = o[3];
+            if (st == 0 && part == 0) sd[kb & 1u][wr] = wrow_ok ? f16_bits(hd.x) * 16384.0f : 0.f;
+        } else {
+            // Q6_K (dequant.rs:340-372): k = 32 part + l, quarter g = 2(st&1)+part of half st/2
+            uint32_t ql[8], qh[8], scw[1], dw[1];
+            align_raw<32>(R.ql, R.mql, ql);
+            align_raw<32>(R.qh, R.mqh, qh);
+            align_raw<4>(R.sc, R.msc, scw);
+            align_raw<4>(R.d, R.md, dw);
+            const uint32_t g = 2u * (st & 1u) + part, nib = 4u * (st & 1u), qsh = 2u * g;
+            const int sc0 = (int)(int8_t)(scw[0] & 0xFFu), sc1 = (int)(int8_t)((scw[0] >> 8) & 0xFFu);
+            const int perm[4] = {0, 2, 1, 3};
+            uint32_t outw[16];
 #pragma unroll
-                for (int c = 0; c < 4; c++) {   // 4 chunks of 8 bytes -> 8 low + 8 high weights each
+            for (int t = 0; t < 16; t++) {   // output dword t = positions 2t, 2t+1
+                uint16_t hv[2];
 #pragma unroll
-                    for (int b = 0; b < 8; b++) {
-                        const uint32_t byte = (qs[2 * c + b / 4] >> (8 * (b & 3))) & 0xFFu;
-                        lo8[b] = (_Float16)(float)(byte & 0xFu) * f0;
-                        hi8[b] = (_Float16)(float)(byte >> 4) * f1;
-                    }
-                    *reinterpret_cast<half8 *>(dst + 64 * part + 8 * c) = wrow_ok ? lo8 : half8{};
-                    *reinterpret_cast<half8 *>(dst + 64 * part + 32 + 8 * c) = wrow_ok ? hi8 : half8{};
+                for (int e = 0; e < 2; e++) {
+                    const uint32_t pos = 2 * t + e, l = (pos & ~3u) + perm[pos & 3u];
+                    const uint32_t qlb = (ql[l / 4] >> (8 * (l & 3))) & 0xFFu;
+                    const uint32_t qhb = (qh[l / 4] >> (8 * (l & 3))) & 0xFFu;
+                    const int q = (int)(((qlb >> nib) & 0xFu) | (((qhb >> qsh) & 3u) << 4)) - 32;
+                    hv[e] = __builtin_bit_cast(uint16_t, (_Float16)(float)((l < 16 ? sc0 : sc1) * q));
                 }
-                if (part == 0) sd[wr] = wrow_ok ? (float)__builtin_bit_cast(_Float16, (uint16_t)(hd[0] & 0xFFFFu)) : 0.f;
-            } else {
-                // Q6_K half hs: part 0 -> quarters g = 0, 2 (ql[0..31]); part 1 -> g = 1, 3 (ql[32..63])
-                uint32_t ql[8], qh[8], scw[2], dw[1];
-                load_words<32>(blk + 64 * hs + 32 * part, ql);
-                load_words<32>(blk + 128 + 32 * hs, qh);
-                load_words<8>(blk + 192 + 8 * hs, scw);
-                load_words<4>(blk + 208, dw);
-                const int8_t *sc = reinterpret_cast<const int8_t *>(scw);
-                const uint32_t ga = part, gb = part + 2;          // quarters from low / high nibbles
-                const uint32_t sha = 2 * ga, shb = 2 * gb;        // qh bit pair position
-#pragma unroll
-                for (int c = 0; c < 4; c++) {                     // l = 8c .. 8c+7
-                    half8 va, vb;
-#pragma unroll
-                    for (int b = 0; b < 8; b++) {
-                        const uint32_t l = 8 * c + b;
-                        const uint32_t qlb = (ql[l / 4] >> (8 * (l & 3))) & 0xFFu;
-                        const uint32_t qhb = (qh[l / 4] >> (8 * (l & 3))) & 0xFFu;
-                        const int qa = (int)((qlb & 0xFu) | (((qhb >> sha) & 3u) << 4)) - 32;
-                        const int qb = (int)((qlb >> 4) | (((qhb >> shb) & 3u) << 4)) - 32;
-                        const uint32_t is = l / 16;
-                        va[b] = (_Float16)(float)(sc[is + 2 * ga] * qa);
-                        vb[b] = (_Float16)(float)(sc[is + 2 * gb] * qb);
-                    }
-                    *reinterpret_cast<half8 *>(dst + 32 * ga + 8 * c) = wrow_ok ? va : half8{};
-                    *reinterpret_cast<half8 *>(dst + 32 * gb + 8 * c) = wrow_ok ? vb : half8{};
-                }
-                if (part == 0) sd[wr] = wrow_ok ? (float)__builtin_bit_cast(_Float16, (uint16_t)(dw[0] & 0xFFFFu)) : 0.f;
+                outw[t] = (uint32_t)hv[0] | ((uint32_t)hv[1] << 16);
             }
-            __syncthreads();
-            // ---- MFMA over the 128-k step
 #pragma unroll
-            for (int ks = 0; ks < GBK / 32; ks++) {
-                half8 a[4], b[4];
+            for (int c = 0; c < 4; c++) {
+                const uint4 v = wrow_ok ? make_uint4(outw[4 * c], outw[4 * c + 1], outw[4 * c + 2], outw[4 * c + 3])
+                                        : make_uint4(0, 0, 0, 0);
+                *reinterpret_cast<uint4 *>(dst + 32u * part + 8u * c) = v;
+            }
+            if (st == 0 && part == 0) sd[kb & 1u][wr] = wrow_ok ? f16_bits(dw[0]) : 0.f;
+        }
+    };
+
+    auto compute = [&](int b) {
 #pragma unroll
-                for (int i = 0; i < 4; i++)
-                    a[i] = *reinterpret_cast<const half8 *>(sx + (wm * 64 + i * 16 + (lane & 15)) * LDW + ks * 32 +
-                                                           8 * (lane >> 4));
+        for (int ks = 0; ks < GSK / 32; ks++) {
+            half8 a[TM], bw[4];
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+                a[i] = *reinterpret_cast<const half8 *>(sx[b] + (wm * (BM / 2) + i * 16 + (lane & 15u)) * GLD +
+                                                        ks * 32 + 8u * (lane >> 4));
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                bw[j] = *reinterpret_cast<const half8 *>(sw[b] + (wn * 64 + j * 16 + (lane & 15u)) * GLD + ks * 32 +
+                                                         8u * (lane >> 4));
+#pragma unroll
+            for (int i = 0; i < TM; i++)
 #pragma unroll
                 for (int j = 0; j < 4; j++)
-                    b[j] = *reinterpret_cast<const half8 *>(sw + (wn * 64 + j * 16 + (lane & 15)) * LDW + ks * 32 +
-                                                           8 * (lane >> 4));
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-#pragma unroll
-                    for (int j = 0; j < 4; j++)
-                        tmp[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], tmp[i][j], 0, 0, 0);
-            }
-            if (hs == 1) {   // super-block done: final += d[r] * tmp
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const float dr = sd[wn * 64 + j * 16 + (lane & 15)];
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        acc[i][j] += dr * tmp[i][j];
-                        tmp[i][j] = floatx4{0, 0, 0, 0};
-                    }
-                }
-            }
-            __syncthreads();
+                    tmp[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], bw[j], tmp[i][j], 0, 0, 0);
         }
+    };
+    auto block_done = [&](uint32_t kb) {   // final += d[r] * super-block partial
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float dr = sd[kb & 1u][wn * 64 + j * 16 + (lane & 15u)];
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+                acc[i][j] += dr * tmp[i][j];
+                tmp[i][j] = floatx4{0, 0, 0, 0};
+            }
+        }
+    };
+
+    GemmRegs<DT, XCH> R0, R1;
+    load_stage(0, R0);
+    load_stage(1, R1);
+    dequant_stage(0, R0, 0);
+    load_stage(2 < S ? 2 : S - 1, R0);
+    __syncthreads();
+    for (uint32_t s = 0; s < S; s += 2) {   // S = 4 * bpr is even
+        compute(0);
+        dequant_stage(s + 1, R1, 1);
+        load_stage(s + 3 < S ? s + 3 : S - 1, R1);
+        __syncthreads();
+        compute(1);
+        if (((s + 1) & 3u) == 3u) block_done((s + 1) >> 2);
+        if (s + 2 < S) {
+            dequant_stage(s + 2, R0, 0);
+            load_stage(s + 4 < S ? s + 4 : S - 1, R0);
+        }
+        __syncthreads();
     }
 
-    if constexpr (DT == YULE_DTYPE_Q4_K) {
+    if constexpr (Q4) {
         // min term: acc -= sum_j xsum[m][j] * (dmin*mn)[r][j] over the K/32
         // sub-blocks; a k-step of 32 covers 4 super-blocks, lane quarter q
         // takes super-block 4*kk + q, i.e. its 8 sub-blocks.
         const uint32_t nsub = K / 32;
-        for (uint32_t kk = 0; kk < bpr; kk += 4) {
-            const uint32_t sbk = kk + (lane >> 4);          // super-block of this lane's 8 sub-blocks
+        for (uint32_t kk = kb_lo; kk < kb_hi; kk += 4) {
+            const uint32_t sbk = kk + (lane >> 4);
             half8 bh[4], bl[4];
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const uint32_t r = r0 + wn * 64 + j * 16 + (lane & 15);
+                const uint32_t r = r0 + wn * 64 + j * 16 + (lane & 15u);
                 half8 h = {}, l = {};
-                if (r < N && sbk < bpr) {
+                if (r < N && sbk < kb_hi) {
                     const uint8_t *blk = w + (size_t)r * row_bytes + (size_t)sbk * BB;
                     const uint4 h4 = *reinterpret_cast<const uint4 *>(blk);
-                    const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(h4.x >> 16));
+                    const float dmin = f16_bits(h4.x >> 16);
                     const uint32_t hd[3] = {h4.y, h4.z, h4.w};
                     const uint8_t *q = reinterpret_cast<const uint8_t *>(hd);
 #pragma unroll
@@ -241,10 +333,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(const uint8_t *__restrict__ w
                 bl[j] = l;
             }
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint32_t m = m0 + wm * 64 + i * 16 + (lane & 15);
+            for (int i = 0; i < TM; i++) {
+                const uint32_t m = m0 + wm * (BM / 2) + i * 16 + (lane & 15u);
                 half8 ah = {}, al = {};
-                if (m < M && sbk < bpr) {
+                if (m < M && sbk < kb_hi) {
                     ah = *reinterpret_cast<const half8 *>(xs_hi + (size_t)m * nsub + 8 * sbk);
                     al = *reinterpret_cast<const half8 *>(xs_lo + (size_t)m * nsub + 8 * sbk);
                 }
@@ -260,23 +352,33 @@ __global__ __launch_bounds__(256) void gemm_kernel(const uint8_t *__restrict__ w
 
     // ---- store: lane holds rows 4*(lane/16)+e of column lane%16 of each tile
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const uint32_t r = r0 + wn * 64 + j * 16 + (lane & 15);
+            const uint32_t r = r0 + wn * 64 + j * 16 + (lane & 15u);
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                const uint32_t m = m0 + wm * 64 + i * 16 + 4 * (lane >> 4) + e;
+                const uint32_t m = m0 + wm * (BM / 2) + i * 16 + 4 * (lane >> 4) + e;
                 if (m < M && r < N) y[(size_t)m * N + r] = acc[i][j][e];
             }
         }
+}
+
+// y[i] = sum over z of part[z][i], z ascending
+__global__ void gemm_reduce_kernel(const float *__restrict__ part, float *__restrict__ y, uint64_t n, uint32_t ks) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    float s = part[i];
+    for (uint32_t z = 1; z < ks; z++) s += part[(uint64_t)z * n + i];
+    y[i] = s;
 }
 
 }  // namespace yule
 
 using namespace yule;
 
-// Per-backend scratch for the sub-block sums of X (grown on demand).
+// Per-backend scratch: X in f16 (permuted) and its sub-block sums (grown on
+// demand; one backend at a time).
 namespace {
 struct GemmScratch {
     yule_hip_backend *be = nullptr;
@@ -285,6 +387,31 @@ struct GemmScratch {
 };
 GemmScratch g_scratch;
 std::mutex g_scratch_mu;
+
+// Split count: none once the tiles alone fill every CU; below that, as many
+// splits as fit in one round of resident workgroups (two per CU), so that
+// small-M launches keep all CUs busy without a partial second round.
+uint32_t gemm_splits(uint32_t m, uint32_t n, uint32_t k) {
+    const uint32_t bm = m <= 64 ? 64 : 128;
+    const uint32_t tiles = ((n + GBN - 1) / GBN) * ((m + bm - 1) / bm);
+    const uint32_t cus = (uint32_t)device_cus();
+    if (tiles >= cus) return 1;
+    uint32_t ks = 2 * cus / tiles;
+    const uint32_t bpr = k / 256;
+    return ks < 1 ? 1 : ks > bpr ? bpr : ks;
+}
+
+template <uint32_t DT>
+void launch_gemm(hipStream_t s, const uint8_t *w, const _Float16 *xh, float *y, const _Float16 *xs_hi,
+                 const _Float16 *xs_lo, uint32_t m, uint32_t n, uint32_t k, uint32_t ks) {
+    if (m <= 64) {
+        hipLaunchKernelGGL((gemm_kernel<DT, 64>), dim3((n + GBN - 1) / GBN, (m + 63) / 64, ks), dim3(256), 0, s, w,
+                           xh, y, xs_hi, xs_lo, m, n, k);
+    } else {
+        hipLaunchKernelGGL((gemm_kernel<DT, 128>), dim3((n + GBN - 1) / GBN, (m + 127) / 128, ks), dim3(256), 0, s, w,
+                           xh, y, xs_hi, xs_lo, m, n, k);
+    }
+}
 }  // namespace
 
 extern "C" int yule_hip_quantized_gemm(yule_hip_backend *be, yule_buffer weights, yule_buffer x_bf16, yule_buffer y,
@@ -305,33 +432,39 @@ extern "C" int yule_hip_quantized_gemm(yule_hip_backend *be, yule_buffer weights
     if (x_bf16 == y) return set_error(YULE_ERR_INVALID, "quantized_gemm: x and y alias");
     if (!m || !n_rows) return YULE_OK;
     if (!n_cols) return launch_fill(be->stream, (float *)py, 0.f, (uint64_t)m * n_rows);
-    _Float16 *xs_hi = nullptr, *xs_lo = nullptr;
-    if (dtype == YULE_DTYPE_Q4_K) {
-        const size_t need = (size_t)m * (n_cols / 32) * 2 * sizeof(_Float16) + 256;
-        std::lock_guard<std::mutex> lk(g_scratch_mu);
-        if (g_scratch.be != be || g_scratch.size < need) {
-            if (g_scratch.p) {
-                hipStreamSynchronize(be->stream);
-                hipFree(g_scratch.p);
-            }
-            g_scratch = GemmScratch{};
-            if ((rc = hip_error(hipMalloc(&g_scratch.p, need), "quantized_gemm: scratch"))) return rc;
-            g_scratch.be = be;
-            g_scratch.size = need;
+    const bool q4 = dtype == YULE_DTYPE_Q4_K;
+    const uint32_t ks = gemm_splits(m, n_rows, n_cols);
+    const size_t n_x = (size_t)m * n_cols, n_sub = (size_t)m * (n_cols / 32), n_y = (size_t)m * n_rows;
+    const size_t part_bytes = ks > 1 ? ((ks * n_y * sizeof(float) + 255) & ~(size_t)255) : 0;
+    const size_t need = part_bytes + (n_x + (q4 ? 2 * n_sub : 0)) * sizeof(_Float16) + 256;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch.be != be || g_scratch.size < need) {
+        if (g_scratch.p) {
+            (void)hipStreamSynchronize(g_scratch.be ? g_scratch.be->stream : be->stream);
+            (void)hipFree(g_scratch.p);
         }
-        xs_hi = static_cast<_Float16 *>(g_scratch.p);
-        xs_lo = xs_hi + (size_t)m * (n_cols / 32);
-        const uint64_t nx = (uint64_t)m * (n_cols / 32);
-        hipLaunchKernelGGL(xsum_kernel, dim3((unsigned)((nx + 255) / 256)), dim3(256), 0, be->stream,
-                           (const uint16_t *)px, xs_hi, xs_lo, m, n_cols);
-        if ((rc = check_launch("quantized_gemm: x sums"))) return rc;
-        hipLaunchKernelGGL(gemm_kernel<YULE_DTYPE_Q4_K>, dim3((n_rows + GBN - 1) / GBN, (m + GBM - 1) / GBM),
-                           dim3(256), 0, be->stream, (const uint8_t *)pw, (const uint16_t *)px, (float *)py, xs_hi,
-                           xs_lo, m, n_rows, n_cols);
-    } else {
-        hipLaunchKernelGGL(gemm_kernel<YULE_DTYPE_Q6_K>, dim3((n_rows + GBN - 1) / GBN, (m + GBM - 1) / GBM),
-                           dim3(256), 0, be->stream, (const uint8_t *)pw, (const uint16_t *)px, (float *)py, nullptr,
-                           nullptr, m, n_rows, n_cols);
+        g_scratch = GemmScratch{};
+        if ((rc = hip_error(hipMalloc(&g_scratch.p, need), "quantized_gemm: scratch"))) return rc;
+        g_scratch.be = be;
+        g_scratch.size = need;
     }
-    return check_launch("quantized_gemm");
+    float *part = ks > 1 ? static_cast<float *>(g_scratch.p) : nullptr;
+    _Float16 *xh = reinterpret_cast<_Float16 *>(static_cast<uint8_t *>(g_scratch.p) + part_bytes);
+    _Float16 *xs_hi = q4 ? xh + n_x : nullptr, *xs_lo = q4 ? xs_hi + n_sub : nullptr;
+    hipLaunchKernelGGL(gemm_xprep_kernel, dim3((unsigned)((n_sub + 255) / 256)), dim3(256), 0, be->stream,
+                       (const uint16_t *)px, xh, xs_hi, xs_lo, m, n_cols);
+    if ((rc = check_launch("quantized_gemm: x pre-pass"))) return rc;
+    float *out = ks > 1 ? part : (float *)py;
+    if (q4)
+        launch_gemm<YULE_DTYPE_Q4_K>(be->stream, (const uint8_t *)pw, xh, out, xs_hi, xs_lo, m, n_rows, n_cols, ks);
+    else
+        launch_gemm<YULE_DTYPE_Q6_K>(be->stream, (const uint8_t *)pw, xh, out, nullptr, nullptr, m, n_rows, n_cols,
+                                     ks);
+    if ((rc = check_launch("quantized_gemm"))) return rc;
+    if (ks > 1) {
+        hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)((n_y + 255) / 256)), dim3(256), 0, be->stream, part,
+                           (float *)py, (uint64_t)n_y, ks);
+        rc = check_launch("quantized_gemm: split-K reduction");
+    }
+    return rc;
 }
