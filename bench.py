@@ -254,6 +254,35 @@ def profile_dominant(hip, n, copies):
                       "calibration_copy_bytes": 64 << 20}), flush=True)
 
 
+def profile_gemm(hip, n):
+    """N launches of the Q4_K 14336x4096 prefill GEMM at M = 2048 (BASELINE
+    configs[3]), for rocprofv3 kernel-trace and MFMA counter runs."""
+    M, n_rows, n_cols = 2048, 14336, 4096
+    w = hip.upload(synth.gen_quant(DType.Q4_K, 81, n_rows, n_cols))
+    xb = (synth.gauss(82, (M, n_cols)).view(np.uint32) >> 16).astype(np.uint16)
+    hx, hy = hip.upload(xb), hip.allocate(4 * M * n_rows)
+    hip.timer_start()
+    for _ in range(n):
+        hip.quantized_gemm(w, hx, hy, M, n_rows, n_cols, DType.Q4_K)
+    ms = hip.timer_stop() / n
+    print(json.dumps({"launches": n, "us_per_call": round(ms * 1e3, 1),
+                      "TFLOP/s": round(2.0 * M * n_rows * n_cols / (ms * 1e-3) / 1e12, 1)}), flush=True)
+
+
+def profile_decode(hip, n):
+    """N greedy decode steps of the TinyLlama-shaped model after a 16-token
+    prompt, with the runner's kernels launched one by one (tracing profilers
+    do not follow graph replays)."""
+    os.environ["YULE_RUNNER_NO_GRAPH"] = "1"   # read by the runner at its first step
+    from yule_amd.backend import HipRunner
+    from yule_amd.model import TINYLLAMA, SyntheticModel
+    model = SyntheticModel.generate(TINYLLAMA, seed=0)
+    run = HipRunner(hip, model)
+    toks, ms = run.generate_greedy(synth.uniform_tokens(1, 16, TINYLLAMA.vocab), n)
+    run.close()
+    print(json.dumps({"steps": n, "ms_per_step_ungraphed": round(ms, 4)}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -267,6 +296,10 @@ def main():
     ap.add_argument("--profile-dominant", type=int, default=0, metavar="N",
                     help="only run N launches of the dominant kernel (Q4_K 14336x4096 over rotating copies) and "
                          "one 64 MiB device copy, for rocprofv3 --pmc runs; prints a JSON line")
+    ap.add_argument("--profile-gemm", type=int, default=0, metavar="N",
+                    help="only run N calls of the Q4_K 14336x4096 prefill GEMM at M=2048 (for rocprofv3)")
+    ap.add_argument("--profile-decode", type=int, default=0, metavar="N",
+                    help="only run N TinyLlama decode steps with kernels launched one by one (for rocprofv3)")
     args = ap.parse_args()
     global USE_GRAPH
     USE_GRAPH = not args.no_graph
@@ -280,6 +313,12 @@ def main():
     info = hip.device_info()
     if args.profile_dominant:
         profile_dominant(hip, args.profile_dominant, args.copies)
+        return
+    if args.profile_gemm:
+        profile_gemm(hip, args.profile_gemm)
+        return
+    if args.profile_decode:
+        profile_decode(hip, args.profile_decode)
         return
     log(f"device: {info.name}, {info.compute_units} CUs, {info.memory_bytes / 2**30:.0f} GiB")
 
@@ -302,7 +341,7 @@ def main():
     dom_bytes = algo_bytes(DType.Q4_K, 14336, 4096)
     roofline = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(),
-                "kernel": "qmv_kernel<Q4K,64,8> 14336x4096", "avg_launch_us": round(us, 3),
+                "kernel": "qmv_stream_kernel<Q4K,64,2,256> 14336x4096", "avg_launch_us": round(us, 3),
                 "algo_bytes_per_launch": dom_bytes}
     log(f"dominant kernel Q4_K 14336x4096: {us:.2f} us/launch, {gbs:.1f} GB/s")
 
