@@ -22,8 +22,8 @@ HERE = Path(__file__).resolve().parent
 LIB = HERE / "build" / "liboracle.so"
 REF_Q4K_ASM = HERE / "_ref" / "libyule_q4k_asm.so"
 
-F32, F16, Q4_0, Q8_0, Q4_K, Q6_K = 0, 1, 2, 8, 12, 14
-GEOM = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
+F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, Q8_K = 0, 1, 2, 8, 12, 13, 14, 15
+GEOM = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210), Q8_K: (256, 292)}
 
 _lib = None
 _u8p = C.POINTER(C.c_uint8)
@@ -54,9 +54,10 @@ def lib() -> C.CDLL:
         L.yo_f16_to_f32.argtypes = [C.c_uint16]
         L.yo_f16_to_f32.restype = C.c_float
         L.yo_extract_q4k_scales_mins.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p]
-        for n in ("yo_dequant_q4_0", "yo_dequant_q8_0", "yo_dequant_q4_k", "yo_dequant_q6_k"):
+        for n in ("yo_dequant_q4_0", "yo_dequant_q8_0", "yo_dequant_q4_k", "yo_dequant_q6_k", "yo_dequant_q5_k",
+                  "yo_dequant_q8_k"):
             getattr(L, n).argtypes = [C.c_void_p, C.c_void_p]
-        for n in ("yo_vec_dot_q4_0", "yo_vec_dot_q8_0", "yo_vec_dot_q4_k", "yo_vec_dot_q6_k"):
+        for n in ("yo_vec_dot_q4_0", "yo_vec_dot_q8_0", "yo_vec_dot_q4_k", "yo_vec_dot_q6_k", "yo_vec_dot_q5_k"):
             getattr(L, n).argtypes = [C.c_void_p, C.c_void_p]
             getattr(L, n).restype = C.c_float
         L.yo_dequant_rows.argtypes = [C.c_int, C.c_void_p, C.c_size_t, C.c_void_p]

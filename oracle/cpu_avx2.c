@@ -98,6 +98,39 @@ __attribute__((target("avx2,fma"))) static float dot_q4_k(const uint8_t *blk, co
     return sum;
 }
 
+/* avx2.rs:238-303 — per sub-block, 4 groups of 8 weights (5-bit levels built
+ * in scalar), FMA into one accumulator and add into another, hsum each */
+__attribute__((target("avx2,fma"))) static float dot_q5_k(const uint8_t *blk, const float *act) {
+    float d = f16le(blk), dmin = f16le(blk + 2);
+    uint8_t sc[8], mn[8];
+    yo_extract_q4k_scales_mins(blk + 4, sc, mn);
+    const uint8_t *qh = blk + 16;
+    float sum = 0.0f;
+    for (int j = 0; j < 4; j++) {
+        const uint8_t *ql = blk + 48 + 32 * j;
+        const uint8_t u1 = (uint8_t)(1u << (2 * j)), u2 = (uint8_t)(2u << (2 * j));
+        for (int half = 0; half < 2; half++) {
+            const int k = 2 * j + half;
+            float scale = d * (float)sc[k], mins = dmin * (float)mn[k];
+            __m256 dacc = _mm256_setzero_ps(), sacc = _mm256_setzero_ps();
+            for (int g = 0; g < 4; g++) {
+                float w[8];
+                for (int l = 0; l < 8; l++) {
+                    const int idx = 8 * g + l;
+                    const int q = half ? (ql[idx] >> 4) + ((qh[idx] & u2) ? 16 : 0)
+                                       : (ql[idx] & 0x0F) + ((qh[idx] & u1) ? 16 : 0);
+                    w[l] = (float)q;
+                }
+                const __m256 a = _mm256_loadu_ps(act + 64 * j + 32 * half + 8 * g);
+                dacc = _mm256_fmadd_ps(_mm256_loadu_ps(w), a, dacc);
+                sacc = _mm256_add_ps(sacc, a);
+            }
+            sum += scale * hsum(dacc) - mins * hsum(sacc);
+        }
+    }
+    return sum;
+}
+
 /* avx2.rs:305-337 — the AVX2 Q6_K body is the scalar loop */
 static float dot_q6_k(const uint8_t *blk, const float *act) { return yo_vec_dot_q6_k(blk, act); }
 
@@ -110,6 +143,7 @@ int yo_vec_dot_block(int dtype, const uint8_t *blk, const float *act, float *res
         case YO_Q4_0: *res = dot_q4_0(blk, act); return 0;
         case YO_Q4_K: *res = dot_q4_k(blk, act); return 0;
         case YO_Q6_K: *res = dot_q6_k(blk, act); return 0;
+        case YO_Q5_K: *res = dot_q5_k(blk, act); return 0;
         default: break;
         }
     }

@@ -30,7 +30,7 @@
 int yo_block_size(int dtype) {
     switch (dtype) {                      /* dtype.rs:99-118 */
     case YO_Q4_0: case YO_Q8_0: return 32;
-    case YO_Q4_K: case YO_Q6_K: return 256;
+    case YO_Q4_K: case YO_Q5_K: case YO_Q6_K: case YO_Q8_K: return 256;
     case YO_F32: case YO_F16: return 1;
     default: return 0;
     }
@@ -41,7 +41,9 @@ int yo_block_bytes(int dtype) {
     case YO_Q4_0: return 18;
     case YO_Q8_0: return 34;
     case YO_Q4_K: return 144;
+    case YO_Q5_K: return 176;
     case YO_Q6_K: return 210;
+    case YO_Q8_K: return 292;
     case YO_F32: return 4;
     case YO_F16: return 2;
     default: return 0;
@@ -112,6 +114,34 @@ void yo_dequant_q4_k(const uint8_t *blk, float *out) {
         float scale1 = d * (float)sc[2 * j + 1], min1 = dmin * (float)mn[2 * j + 1];
         for (int l = 0; l < 32; l++) out[64 * j + 32 + l] = (float)(qs[l] >> 4) * scale1 - min1;
     }
+}
+
+/* dequant.rs:297-338 — Q4_K's layout plus a 5th bit per weight from qh[32]
+ * (bit 2j for the low-nibble sub-block of group j, bit 2j+1 for the high);
+ * q*(d*sc) - dmin*mn as two separately rounded ops */
+void yo_dequant_q5_k(const uint8_t *blk, float *out) {
+    float d = read_f16(blk), dmin = read_f16(blk + 2);
+    uint8_t sc[8], mn[8];
+    yo_extract_q4k_scales_mins(blk + 4, sc, mn);
+    const uint8_t *qh = blk + 16;
+    for (int j = 0; j < 4; j++) {
+        const uint8_t *ql = blk + 48 + 32 * j;
+        const uint8_t u1 = (uint8_t)(1u << (2 * j)), u2 = (uint8_t)(2u << (2 * j));
+        float d1 = d * (float)sc[2 * j], m1 = dmin * (float)mn[2 * j];
+        for (int l = 0; l < 32; l++)
+            out[64 * j + l] = (float)((ql[l] & 0x0F) + ((qh[l] & u1) ? 16 : 0)) * d1 - m1;
+        float d2 = d * (float)sc[2 * j + 1], m2 = dmin * (float)mn[2 * j + 1];
+        for (int l = 0; l < 32; l++)
+            out[64 * j + 32 + l] = (float)((ql[l] >> 4) + ((qh[l] & u2) ? 16 : 0)) * d2 - m2;
+    }
+}
+
+/* dequant.rs:376-384 — f32 d (little-endian) at 0, 256 int8 at 4; the
+ * 32-byte bsums tail is not read */
+void yo_dequant_q8_k(const uint8_t *blk, float *out) {
+    float d;
+    memcpy(&d, blk, 4);
+    for (int i = 0; i < 256; i++) out[i] = (float)(int8_t)blk[4 + i] * d;
 }
 
 /* the four 6-bit quants of position l in a Q6_K half, dequant.rs:358-361 */
@@ -199,13 +229,43 @@ float yo_vec_dot_q6_k(const uint8_t *blk, const float *act) {
     return sum;
 }
 
-/* dequant.rs:1232-1275 (the four hot-path formats plus F32/F16 scalars) */
+/* dequant.rs:1088-1140 — per sub-block: scale*dot - min*sum(act) */
+float yo_vec_dot_q5_k(const uint8_t *blk, const float *act) {
+    float d = read_f16(blk), dmin = read_f16(blk + 2);
+    uint8_t sc[8], mn[8];
+    yo_extract_q4k_scales_mins(blk + 4, sc, mn);
+    const uint8_t *qh = blk + 16;
+    float sum = 0.0f;
+    for (int j = 0; j < 4; j++) {
+        const uint8_t *ql = blk + 48 + 32 * j;
+        const uint8_t u1 = (uint8_t)(1u << (2 * j)), u2 = (uint8_t)(2u << (2 * j));
+        float scale0 = d * (float)sc[2 * j], min0 = dmin * (float)mn[2 * j];
+        float dot0 = 0.0f, asum0 = 0.0f;
+        for (int l = 0; l < 32; l++) {
+            dot0 += (float)((ql[l] & 0x0F) + ((qh[l] & u1) ? 16 : 0)) * act[64 * j + l];
+            asum0 += act[64 * j + l];
+        }
+        sum += scale0 * dot0 - min0 * asum0;
+        float scale1 = d * (float)sc[2 * j + 1], min1 = dmin * (float)mn[2 * j + 1];
+        float dot1 = 0.0f, asum1 = 0.0f;
+        for (int l = 0; l < 32; l++) {
+            dot1 += (float)((ql[l] >> 4) + ((qh[l] & u2) ? 16 : 0)) * act[64 * j + 32 + l];
+            asum1 += act[64 * j + 32 + l];
+        }
+        sum += scale1 * dot1 - min1 * asum1;
+    }
+    return sum;
+}
+
+/* dequant.rs:1232-1275 (the hot-path formats and Q5_K/Q8_K plus F32/F16 scalars) */
 int yo_dequant_block(int dtype, const uint8_t *blk, float *out) {
     switch (dtype) {
     case YO_Q4_0: yo_dequant_q4_0(blk, out); return 0;
     case YO_Q8_0: yo_dequant_q8_0(blk, out); return 0;
     case YO_Q4_K: yo_dequant_q4_k(blk, out); return 0;
     case YO_Q6_K: yo_dequant_q6_k(blk, out); return 0;
+    case YO_Q5_K: yo_dequant_q5_k(blk, out); return 0;
+    case YO_Q8_K: yo_dequant_q8_k(blk, out); return 0;
     case YO_F16: out[0] = read_f16(blk); return 0;
     case YO_F32: memcpy(out, blk, 4); return 0;
     default: return -1;
@@ -227,7 +287,8 @@ int yo_vec_dot_block_scalar(int dtype, const uint8_t *blk, const float *act, flo
     case YO_Q8_0: *res = yo_vec_dot_q8_0(blk, act); return 0;
     case YO_Q4_K: *res = yo_vec_dot_q4_k(blk, act); return 0;
     case YO_Q6_K: *res = yo_vec_dot_q6_k(blk, act); return 0;
-    default: return -1;
+    case YO_Q5_K: *res = yo_vec_dot_q5_k(blk, act); return 0;
+    default: return -1;   /* Q8_K: no vec_dot in the reference (scalar.rs:4-22) */
     }
 }
 

@@ -30,7 +30,9 @@ enum {
     YO_Q4_0 = 2,
     YO_Q8_0 = 8,
     YO_Q4_K = 12,
+    YO_Q5_K = 13,
     YO_Q6_K = 14,
+    YO_Q8_K = 15,
 };
 
 /* block geometry, yule-core/src/dtype.rs:62-118 (0 = unsupported here) */
@@ -44,10 +46,13 @@ void yo_dequant_q4_0(const uint8_t *blk, float *out);                /* :77-86 *
 void yo_dequant_q8_0(const uint8_t *blk, float *out);                /* :142-150 */
 void yo_dequant_q4_k(const uint8_t *blk, float *out);                /* :260-290 */
 void yo_dequant_q6_k(const uint8_t *blk, float *out);                /* :346-372 */
+void yo_dequant_q5_k(const uint8_t *blk, float *out);                /* :297-338 */
+void yo_dequant_q8_k(const uint8_t *blk, float *out);                /* :376-384 */
 float yo_vec_dot_q4_0(const uint8_t *blk, const float *act);         /* :902-913 */
 float yo_vec_dot_q8_0(const uint8_t *blk, const float *act);         /* :916-926 */
 float yo_vec_dot_q4_k(const uint8_t *blk, const float *act);         /* :929-972 */
 float yo_vec_dot_q6_k(const uint8_t *blk, const float *act);         /* :976-1009 */
+float yo_vec_dot_q5_k(const uint8_t *blk, const float *act);         /* :1088-1140 */
 /* dequant_block / vec_dot_block dispatch, dequant.rs:1232-1282. Returns 0 ok, -1 unsupported. */
 int yo_dequant_block(int dtype, const uint8_t *blk, float *out);
 int yo_dequant_rows(int dtype, const uint8_t *w, size_t n_blocks, float *out);

@@ -2,7 +2,7 @@
 independent helpers the oracle tests use.
 
 `xorshift_blocks` reproduces the block/activation streams of
-yule-core/src/simd/avx2.rs:346-573 (xorshift64 <<13 >>7 <<17, fixed headers,
+yule-core/src/simd/avx2.rs:346-573 (Q5_K: :510-540) (xorshift64 <<13 >>7 <<17, fixed headers,
 activations (r % 1000)/500 - 1) so parity runs on the same inputs the
 reference's AVX2-vs-scalar tests use.
 """
@@ -61,6 +61,16 @@ def xorshift_blocks(fmt: str, count: int):
             b = np.zeros(144, np.uint8)
             b[0], b[1], b[2], b[3] = 0x00, 0x38, 0x66, 0x2E
             for i in range(4, 144):
+                b[i] = g.next() & 0xFF
+            for i in range(4, 16):
+                b[i] = g.next() % 64
+            yield b, g.act(256)
+    elif fmt == "q5_k":
+        g = XorShift(888)
+        for _ in range(count):
+            b = np.zeros(176, np.uint8)
+            b[0], b[1], b[2], b[3] = 0x00, 0x38, 0x66, 0x2E
+            for i in range(4, 176):
                 b[i] = g.next() & 0xFF
             for i in range(4, 16):
                 b[i] = g.next() % 64

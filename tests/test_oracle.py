@@ -184,8 +184,81 @@ def test_q6k_vec_dot_vs_f64():
             assert abs(oracle.vec_dot(oracle.Q6_K, blk, act, scalar) - f64) < 1e-3 * max(1.0, abs(f64))
 
 
+# ------------------------------------------------------------------ Q5_K
+def q5k_from_q4k(q4: np.ndarray, qh: np.ndarray) -> np.ndarray:
+    """Q5_K block with a Q4_K block's header and quants plus 32 qh bytes
+    (layouts: dequant.rs:255-290 vs :292-338)."""
+    b = np.zeros(176, np.uint8)
+    b[0:16] = q4[0:16]
+    b[16:48] = qh
+    b[48:176] = q4[16:144]
+    return b
+
+
+def test_q5k_reference_kat():
+    k = K["q5_k_dequant"]
+    b = np.zeros(176, np.uint8)
+    b[0:2] = hexb(k["d_hex"])
+    b[2:4] = hexb(k["dmin_hex"])
+    b[4] = k["scale0_byte"]
+    b[48] = k["qs48"]
+    assert oracle.dequant(oracle.Q5_K, b)[0] == k["expect_w0"]
+    b[16] = 1
+    assert oracle.dequant(oracle.Q5_K, b)[0] == k["qh16_bit0_expect_w0"]
+
+
+def test_q5k_without_high_bits_is_q4k():
+    """With qh = 0 a Q5_K block is exactly the Q4_K block of the same header
+    and quants (both dequant and vec_dot); the 5th bits then add exactly
+    16 * d * sc to one weight each: bit b of qh[l] moves only weight
+    64*(b//2) + 32*(b%2) + l."""
+    for blk4, act in xorshift_blocks("q4_k", 40):
+        b5 = q5k_from_q4k(blk4, np.zeros(32, np.uint8))
+        ref = oracle.dequant(oracle.Q4_K, blk4)
+        assert np.array_equal(oracle.dequant(oracle.Q5_K, b5).view(np.uint32), ref.view(np.uint32))
+        assert oracle.vec_dot(oracle.Q5_K, b5, act, True) == oracle.vec_dot(oracle.Q4_K, blk4, act, True)
+    blk4 = next(xorshift_blocks("q4_k", 1))[0]
+    d = oracle.f16_to_f32(int(blk4[0]) | (int(blk4[1]) << 8))
+    sc, _ = oracle.extract_q4k_scales_mins(blk4[4:16])
+    base = q5k_from_q4k(blk4, np.zeros(32, np.uint8))
+    ref = oracle.dequant(oracle.Q5_K, base).astype(np.float64)
+    for l in (0, 7, 31):
+        for bit in range(8):
+            b = base.copy()
+            b[16 + l] |= 1 << bit
+            diff = oracle.dequant(oracle.Q5_K, b).astype(np.float64) - ref
+            idx = np.nonzero(diff)[0]
+            w = 64 * (bit // 2) + 32 * (bit % 2) + l
+            assert list(idx) == [w], (l, bit, idx)
+            assert abs(diff[w] - 16.0 * d * float(sc[bit])) <= 1e-6 * max(1.0, abs(ref[w]) + 16 * d * sc[bit])
+
+
+def test_q5k_vec_dot_vs_f64():
+    for blk, act in xorshift_blocks("q5_k", 200):
+        f64 = float(np.dot(oracle.dequant(oracle.Q5_K, blk).astype(np.float64), act.astype(np.float64)))
+        for scalar in (True, False):
+            assert abs(oracle.vec_dot(oracle.Q5_K, blk, act, scalar) - f64) < 1e-3 * max(1.0, abs(f64))
+
+
+# ------------------------------------------------------------------ Q8_K
+@pytest.mark.parametrize("d", [1.0, 0.5, -0.03125, 3.0e-8, 1.0e30, 2.0 ** -149])
+def test_q8k_closed_form(d):
+    """Every int8 value at several f32 scales: w = (i8)q * d (dequant.rs:376-384);
+    the bsums tail is not read; there is no Q8_K vec_dot (simd/scalar.rs:4-22)."""
+    b = np.zeros(292, np.uint8)
+    b[0:4] = np.frombuffer(np.float32(d).tobytes(), np.uint8)
+    b[4:260] = np.arange(256, dtype=np.uint8)
+    want = (np.arange(256, dtype=np.uint8).view(np.int8).astype(np.float32) * np.float32(d)).astype(np.float32)
+    got = oracle.dequant(oracle.Q8_K, b)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    b[260:292] = 0xAB
+    assert np.array_equal(oracle.dequant(oracle.Q8_K, b).view(np.uint32), want.view(np.uint32))
+    with pytest.raises(ValueError):
+        oracle.vec_dot(oracle.Q8_K, b, np.ones(256, np.float32))
+
+
 @pytest.mark.parametrize("fmt,dt", [("q8_0", oracle.Q8_0), ("q4_0", oracle.Q4_0), ("q4_k", oracle.Q4_K),
-                                    ("q6_k", oracle.Q6_K)])
+                                    ("q5_k", oracle.Q5_K), ("q6_k", oracle.Q6_K)])
 def test_avx2_vs_scalar_reference_generators(fmt, dt):
     """The reference's differential tests (avx2.rs:346-573), same seeds and tolerances."""
     g = K["xorshift_generators"][fmt]
@@ -205,7 +278,7 @@ def test_qmv_two_row_kat():
         assert np.all(np.abs(y - np.array(k["expect"])) < k["tol"])
 
 
-@pytest.mark.parametrize("dt", [oracle.Q4_0, oracle.Q8_0, oracle.Q4_K, oracle.Q6_K])
+@pytest.mark.parametrize("dt", [oracle.Q4_0, oracle.Q8_0, oracle.Q4_K, oracle.Q5_K, oracle.Q6_K])
 def test_qmv_threaded_matches_f64(dt):
     """Threaded AVX2 qmv and the single-thread scalar qmv vs f64 dots (300 rows,
     so the >=128-row thread split is exercised)."""

@@ -11,7 +11,8 @@
 namespace yule {
 
 // One thread per output weight, exactly the reference's f32 operation order
-// (no contraction): dequant.rs:77-86, 142-150, 260-290, 346-372.
+// (no contraction): dequant.rs:77-86, 142-150, 260-290, 297-338, 346-372,
+// 376-384.
 __device__ __forceinline__ float f16_exact(const uint8_t *p) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)(p[0] | (p[1] << 8)));
 }
@@ -55,6 +56,28 @@ __device__ inline float dequant_one(uint32_t dtype, const uint8_t *__restrict__ 
         const int q = (int)v - 32;
         const int8_t sc = (int8_t)blk[192 + 8 * half + l / 16 + 2 * g];
         return d * (float)sc * (float)q;
+    }
+    case YULE_DTYPE_Q5_K: {
+        // Q4_K's header and qs with a 5th bit per weight from qh[32]:
+        // bit 2j (low-nibble sub-block) or 2j+1 (high) of qh[l]
+        const float d = f16_exact(blk), dmin = f16_exact(blk + 2);
+        const uint32_t j = e / 64, hi = (e / 32) & 1u, l = e & 31u, sb = 2 * j + hi;
+        const uint8_t *q = blk + 4;
+        uint32_t sc, mn;
+        if (sb < 4) { sc = q[sb] & 63u; mn = q[sb + 4] & 63u; }
+        else {
+            sc = (q[sb + 4] & 0xFu) | ((uint32_t)(q[sb - 4] >> 6) << 4);
+            mn = (uint32_t)(q[sb + 4] >> 4) | ((uint32_t)(q[sb] >> 6) << 4);
+        }
+        const uint8_t qs = blk[48 + 32 * j + l];
+        const uint32_t v = (hi ? (qs >> 4) : (qs & 0x0Fu)) + (((blk[16 + l] >> sb) & 1u) << 4);
+        const float scale = d * (float)sc, mnv = dmin * (float)mn;
+        return (float)v * scale - mnv;
+    }
+    case YULE_DTYPE_Q8_K: {
+        const uint32_t db = (uint32_t)blk[0] | ((uint32_t)blk[1] << 8) | ((uint32_t)blk[2] << 16) |
+                            ((uint32_t)blk[3] << 24);
+        return (float)(int8_t)blk[4 + e] * __builtin_bit_cast(float, db);
     }
     default:
         return 0.f;

@@ -139,6 +139,107 @@ struct Q4K {
     }
 };
 
+// ---------------------------------------------------------------- Q5_K
+// 176 B: d f16 @0, dmin f16 @2, scales[12] @4, qh[32] @16, qs[128] @48
+// (dequant.rs:292-338).  Q4_K's units (group j = sub-blocks 2j, 2j+1) with
+// a 5th bit per weight: bit 2j (low nibble) / 2j+1 (high) of qh[l].  The bit
+// is merged into the f16-denormal halves: bit 4 of a low-nibble half (+16),
+// bit 8 of a high-nibble half, whose x16 is already in place (+16*16).
+struct Q5K {
+    static constexpr uint32_t BS = 256, BB = 176, UPB = 4, NX = 64, NAUX = 2;
+    struct Raw { uint4 h, ha, hb, qa, qb; };
+    template <class X>
+    __device__ static void load_x(const X &x, uint32_t k, uint32_t j, float *xs, float *aux) {
+        Q4K::load_x(x, k, j, xs, aux);
+    }
+    __device__ static Raw load(const uint8_t *__restrict__ blk, uint32_t j) {
+        Raw r;
+        r.h = ldw16(blk);
+        r.ha = ldw16(blk + 16);
+        r.hb = ldw16(blk + 32);
+        r.qa = ldw16(blk + 48 + 32 * j);
+        r.qb = ldw16(blk + 64 + 32 * j);
+        return r;
+    }
+    __device__ static float dot(const Raw &r, uint32_t j, const float *xs, const float *aux) {
+        const float d = f16_bits(r.h.x), dmin = f16_bits(r.h.x >> 16);
+        const uint32_t sh = (j & 1u) << 4;
+        const bool low = j < 2;
+        const uint32_t A = low ? r.h.y : r.h.w, Am = low ? r.h.z : (r.h.w >> 4);
+        const uint32_t mA = low ? 0x3F3Fu : 0x0F0Fu, mB = low ? 0u : 0x3030u;
+        const uint32_t scs = ((A >> sh) & mA) | ((r.h.y >> (sh + 2)) & mB);
+        const uint32_t mns = ((Am >> sh) & mA) | ((r.h.z >> (sh + 2)) & mB);
+        const uint32_t q[8] = {r.qa.x, r.qa.y, r.qa.z, r.qa.w, r.qb.x, r.qb.y, r.qb.z, r.qb.w};
+        const uint32_t hq[8] = {r.ha.x, r.ha.y, r.ha.z, r.ha.w, r.hb.x, r.hb.y, r.hb.z, r.hb.w};
+        float alo = 0.f, ahi = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t w = q[i], s = w >> 8;
+            const uint32_t hb = hq[i] >> (2 * j), hs = hb >> 8;   // bit 0: low, bit 1: high nibble's 5th bit
+            const uint32_t a = (w & 0x000F000Fu) | ((hb & 0x00010001u) << 4);
+            const uint32_t b = (s & 0x000F000Fu) | ((hs & 0x00010001u) << 4);
+            const uint32_t c = (w & 0x00F000F0u) | ((hb & 0x00020002u) << 7);
+            const uint32_t e = (s & 0x00F000F0u) | ((hs & 0x00020002u) << 7);
+            alo = mix_lo(a, xs[4 * i + 0], alo);
+            alo = mix_lo(b, xs[4 * i + 1], alo);
+            alo = mix_hi(a, xs[4 * i + 2], alo);
+            alo = mix_hi(b, xs[4 * i + 3], alo);
+            ahi = mix_lo(c, xs[32 + 4 * i + 0], ahi);
+            ahi = mix_lo(e, xs[32 + 4 * i + 1], ahi);
+            ahi = mix_hi(c, xs[32 + 4 * i + 2], ahi);
+            ahi = mix_hi(e, xs[32 + 4 * i + 3], ahi);
+        }
+        const float sc0 = (float)(scs & 0xFFu), sc1 = (float)(scs >> 8);
+        const float mn0 = (float)(mns & 0xFFu), mn1 = (float)(mns >> 8);
+        const float t = sc0 * alo + (sc1 * 0.0625f) * ahi;
+        return (d * kTwo24) * t - dmin * (mn0 * aux[0] + mn1 * aux[1]);
+    }
+};
+
+// ---------------------------------------------------------------- Q8_K
+// 292 B: d f32 @0, qs int8[256] @4, bsums[16] @260 (not read;
+// dequant.rs:374-384).  Rows are a multiple of 4 bytes, so every block is
+// dword aligned.  Unit u = quants 32u..32u+31, read as q ^ 0x80 = q + 128
+// into f16-denormal halves, minus 128 * sum(x).
+struct Q8K {
+    static constexpr uint32_t BS = 256, BB = 292, UPB = 8, NX = 32, NAUX = 1;
+    struct Raw { uint32_t d, w[8]; };
+    template <class X>
+    __device__ static void load_x(const X &x, uint32_t k, uint32_t u, float *xs, float *aux) {
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            float4 v = x(k * 256 + u * 32 + 4 * i);
+            xs[4 * i] = v.x; xs[4 * i + 1] = v.y; xs[4 * i + 2] = v.z; xs[4 * i + 3] = v.w;
+        }
+#pragma unroll
+        for (int i = 0; i < 32; i++) s += xs[i];
+        aux[0] = s;
+    }
+    __device__ static Raw load(const uint8_t *__restrict__ blk, uint32_t u) {
+        Raw r;
+        const uint32_t *p = reinterpret_cast<const uint32_t *>(blk);
+        r.d = ldw4(p);
+#pragma unroll
+        for (int i = 0; i < 8; i++) r.w[i] = ldw4(p + 1 + 8 * u + i);
+        return r;
+    }
+    __device__ static float dot(const Raw &r, uint32_t, const float *xs, const float *aux) {
+        const float d = __builtin_bit_cast(float, r.d);
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t q = r.w[i] ^ 0x80808080u;   // q + 128
+            const uint32_t ev = q & 0x00FF00FFu, od = (q >> 8) & 0x00FF00FFu;
+            acc = mix_lo(ev, xs[4 * i + 0], acc);
+            acc = mix_lo(od, xs[4 * i + 1], acc);
+            acc = mix_hi(ev, xs[4 * i + 2], acc);
+            acc = mix_hi(od, xs[4 * i + 3], acc);
+        }
+        return d * (acc * kTwo24 - 128.f * aux[0]);
+    }
+};
+
 // ---------------------------------------------------------------- Q6_K
 // 210 B: ql[128] @0, qh[64] @128, scales i8[16] @192, d f16 @208
 // (dequant.rs:340-372).  Unit u (0..7) = half h = u/4, positions
@@ -693,14 +794,18 @@ bool qmv_pairable(uint32_t dtype, uint32_t n_cols) {
     if (!qmv_fusable(dtype, n_cols)) return false;
     uint32_t bs, bb;
     quant_geometry(dtype, &bs, &bb);
-    const uint32_t units = (n_cols / bs) * (dtype == YULE_DTYPE_Q4_K ? 4u : dtype == YULE_DTYPE_Q6_K ? 8u : 1u);
+    const uint32_t units = (n_cols / bs) * (dtype == YULE_DTYPE_Q4_K || dtype == YULE_DTYPE_Q5_K   ? 4u
+                                            : dtype == YULE_DTYPE_Q6_K || dtype == YULE_DTYPE_Q8_K ? 8u
+                                                                                                  : 1u);
     return units <= 64;
 }
 
 bool qmv_fusable(uint32_t dtype, uint32_t n_cols) {
     switch (dtype) {
     case YULE_DTYPE_Q4_K: return stream_ok<Q4K>(n_cols);
+    case YULE_DTYPE_Q5_K: return stream_ok<Q5K>(n_cols);
     case YULE_DTYPE_Q6_K: return stream_ok<Q6K>(n_cols);
+    case YULE_DTYPE_Q8_K: return stream_ok<Q8K>(n_cols);
     case YULE_DTYPE_Q8_0: return stream_ok<Q80>(n_cols);
     case YULE_DTYPE_Q4_0: return stream_ok<Q40>(n_cols);
     default: return false;
@@ -717,7 +822,9 @@ int launch_qmv_fused(hipStream_t s, uint32_t dtype, const QmvSeg *segs, uint32_t
     int rc;
     switch (dtype) {
     case YULE_DTYPE_Q4_K: rc = launch_fmt<Q4K>(s, segs, n_seg, x, n_cols, xf); break;
+    case YULE_DTYPE_Q5_K: rc = launch_fmt<Q5K>(s, segs, n_seg, x, n_cols, xf); break;
     case YULE_DTYPE_Q6_K: rc = launch_fmt<Q6K>(s, segs, n_seg, x, n_cols, xf); break;
+    case YULE_DTYPE_Q8_K: rc = launch_fmt<Q8K>(s, segs, n_seg, x, n_cols, xf); break;
     case YULE_DTYPE_Q8_0: rc = launch_fmt<Q80>(s, segs, n_seg, x, n_cols, xf); break;
     case YULE_DTYPE_Q4_0: rc = launch_fmt<Q40>(s, segs, n_seg, x, n_cols, xf); break;
     default: return set_error(YULE_ERR_UNSUPPORTED, "quantized_matmul: unsupported dtype");

@@ -55,7 +55,9 @@ bool quant_geometry(uint32_t dtype, uint32_t *bs, uint32_t *bb) {
     case YULE_DTYPE_Q4_0: *bs = 32; *bb = 18; return true;
     case YULE_DTYPE_Q8_0: *bs = 32; *bb = 34; return true;
     case YULE_DTYPE_Q4_K: *bs = 256; *bb = 144; return true;
+    case YULE_DTYPE_Q5_K: *bs = 256; *bb = 176; return true;
     case YULE_DTYPE_Q6_K: *bs = 256; *bb = 210; return true;
+    case YULE_DTYPE_Q8_K: *bs = 256; *bb = 292; return true;
     default: return false;
     }
 }

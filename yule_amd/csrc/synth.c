@@ -151,6 +151,66 @@ static void quant_q4_k(const float *x, uint8_t *b) {
             b[16 + 32 * j + l] = (uint8_t)(lev[64 * j + l] | (lev[64 * j + 32 + l] << 4));
 }
 
+/* Q5_K (176 B / 256): Q4_K's scheme with 32 levels; the 5th bit of weight
+ * 64j+l (low-nibble sub-block 2j) is bit 2j of qh[l], of weight 64j+32+l
+ * bit 2j+1 (dequant.rs:292-338). */
+static void quant_q5_k(const float *x, uint8_t *b) {
+    float scale[8], mins[8], smax = 0.0f, mmax = 0.0f;
+    for (int s = 0; s < 8; s++) {
+        float lo = 0.0f, hi = -INFINITY;
+        for (int i = 0; i < 32; i++) { lo = fminf(lo, x[32 * s + i]); hi = fmaxf(hi, x[32 * s + i]); }
+        scale[s] = (hi - lo) / 31.0f;
+        mins[s] = -lo;
+        smax = fmaxf(smax, scale[s]);
+        mmax = fmaxf(mmax, mins[s]);
+    }
+    put_f16(b, smax / 63.0f);
+    put_f16(b + 2, mmax / 63.0f);
+    float D = f16_val((uint16_t)(b[0] | (b[1] << 8))), DM = f16_val((uint16_t)(b[2] | (b[3] << 8)));
+    uint8_t sc[8], mn[8];
+    for (int s = 0; s < 8; s++) {
+        sc[s] = (uint8_t)(D > 0.0f ? clampi((int)lrintf(scale[s] / D), 0, 63) : 0);
+        mn[s] = (uint8_t)(DM > 0.0f ? clampi((int)lrintf(mins[s] / DM), 0, 63) : 0);
+    }
+    uint8_t *q = b + 4;
+    for (int j = 0; j < 4; j++) {
+        q[j] = (uint8_t)((sc[j] & 63) | ((sc[j + 4] >> 4) << 6));
+        q[j + 4] = (uint8_t)((mn[j] & 63) | ((mn[j + 4] >> 4) << 6));
+        q[j + 8] = (uint8_t)((sc[j + 4] & 0xF) | ((mn[j + 4] & 0xF) << 4));
+    }
+    uint8_t lev[256];
+    for (int s = 0; s < 8; s++) {
+        float es = D * (float)sc[s], em = DM * (float)mn[s];
+        for (int i = 0; i < 32; i++)
+            lev[32 * s + i] = (uint8_t)(es > 0.0f ? clampi((int)lrintf((x[32 * s + i] + em) / es), 0, 31) : 0);
+    }
+    uint8_t *qh = b + 16;
+    memset(qh, 0, 32);
+    for (int j = 0; j < 4; j++)
+        for (int l = 0; l < 32; l++) {
+            const uint8_t a = lev[64 * j + l], c = lev[64 * j + 32 + l];
+            b[48 + 32 * j + l] = (uint8_t)((a & 15) | ((c & 15) << 4));
+            qh[l] |= (uint8_t)(((a >> 4) << (2 * j)) | ((c >> 4) << (2 * j + 1)));
+        }
+}
+
+/* Q8_K (292 B / 256): f32 d = amax/127 (little-endian), 256 int8 quants,
+ * then 16 int16 sums of consecutive 16 quants (ggml's bsums; dequant.rs
+ * does not read them). */
+static void quant_q8_k(const float *x, uint8_t *b) {
+    float amax = 0.0f;
+    for (int i = 0; i < 256; i++) amax = fmaxf(amax, fabsf(x[i]));
+    const float d = amax / 127.0f, id = d != 0.0f ? 1.0f / d : 0.0f;
+    memcpy(b, &d, 4);
+    for (int i = 0; i < 256; i++) b[4 + i] = (uint8_t)(int8_t)clampi((int)lrintf(x[i] * id), -128, 127);
+    for (int g = 0; g < 16; g++) {
+        int sum = 0;
+        for (int i = 0; i < 16; i++) sum += (int8_t)b[4 + 16 * g + i];
+        const int16_t s16 = (int16_t)sum;
+        memcpy(b + 260 + 2 * g, &s16, 2);
+    }
+}
+
 /* Q6_K (210 B / 256): 16 sub-blocks of 16 with int8 scales relative to an
  * f16 d; 6-bit quants biased by 32, split into ql nibbles and qh pairs in
  * the layout of dequant.rs:340-372. */
@@ -189,7 +249,9 @@ static int geom(int dtype, int *bs, int *bb) {
     case 2: *bs = 32; *bb = 18; return 0;
     case 8: *bs = 32; *bb = 34; return 0;
     case 12: *bs = 256; *bb = 144; return 0;
+    case 13: *bs = 256; *bb = 176; return 0;
     case 14: *bs = 256; *bb = 210; return 0;
+    case 15: *bs = 256; *bb = 292; return 0;
     default: return -1;
     }
 }
@@ -199,7 +261,9 @@ static void quant_block(int dtype, const float *x, uint8_t *b) {
     case 2: quant_q4_0(x, b); break;
     case 8: quant_q8_0(x, b); break;
     case 12: quant_q4_k(x, b); break;
+    case 13: quant_q5_k(x, b); break;
     case 14: quant_q6_k(x, b); break;
+    case 15: quant_q8_k(x, b); break;
     }
 }
 

@@ -5,13 +5,15 @@ from enum import IntEnum
 
 
 class DType(IntEnum):
-    """GGUF type ids, dtype.rs:21-33 (the values cross the C ABI)."""
+    """GGUF type ids, dtype.rs:21-35 (the values cross the C ABI)."""
     F32 = 0
     F16 = 1
     Q4_0 = 2
     Q8_0 = 8
     Q4_K = 12
+    Q5_K = 13
     Q6_K = 14
+    Q8_K = 15
 
 
 # (weights per block, bytes per block): dtype.rs:62-118
@@ -19,7 +21,9 @@ GEOMETRY = {
     DType.Q4_0: (32, 18),
     DType.Q8_0: (32, 34),
     DType.Q4_K: (256, 144),
+    DType.Q5_K: (256, 176),
     DType.Q6_K: (256, 210),
+    DType.Q8_K: (256, 292),
 }
 QUANTIZED = tuple(GEOMETRY)
 
