@@ -37,6 +37,8 @@ extern "C" {
 #define YULE_ERR_NO_DEVICE 3   /* no usable gfx950 device */
 #define YULE_ERR_OOM 4         /* device allocation failed */
 #define YULE_ERR_HIP 5         /* HIP runtime error */
+#define YULE_ERR_PARSE 6       /* malformed GGUF file (YuleError::Parse and friends) */
+#define YULE_ERR_IO 7          /* file could not be opened or mapped */
 
 #define YULE_DTYPE_F32 0
 #define YULE_DTYPE_F16 1
@@ -238,6 +240,46 @@ int yule_hip_runner_prefill(yule_hip_runner *r, const uint32_t *tokens, uint32_t
  * tokens/s method: 1000 / ms). */
 int yule_hip_runner_generate_greedy(yule_hip_runner *r, const uint32_t *prompt, uint32_t n_prompt,
                                     uint32_t n_decode, uint32_t *out_tokens, float *ms_per_decode_step);
+
+/* ---- GGUF v3 files (yule-core/src/gguf.rs) ---- */
+
+typedef struct yule_gguf yule_gguf;
+
+/* TensorInfo (yule-core/src/tensor.rs) of one tensor of a mapped file. */
+typedef struct {
+    const char *name;     /* owned by the yule_gguf */
+    uint32_t dtype;       /* GGUF type id (dtype.rs:155-190) */
+    uint32_t n_dims;
+    uint64_t dims[8];     /* GGUF order: dims[0] is the row length; unused = 1 */
+    uint64_t offset;      /* relative to the data section */
+    uint64_t size_bytes;
+    const void *data;     /* mapped bytes, valid until yule_hip_gguf_close */
+} yule_gguf_tensor;
+
+/* GgufParser::parse_file (gguf.rs:255-432): read-only mapping, magic and
+ * version 3, the reference's limits (strings <= 1 MiB, <= 100k tensors and
+ * metadata pairs, arrays <= 10M, <= 8 dims), data section at the header end
+ * rounded up to general.alignment (default 32), tensors inside the file and
+ * not overlapping.  Errors: YULE_ERR_IO, YULE_ERR_PARSE. */
+int yule_hip_gguf_open(const char *path, yule_gguf **out);
+int yule_hip_gguf_close(yule_gguf *g);
+int yule_hip_gguf_header(const yule_gguf *g, uint32_t *version, uint64_t *alignment, uint64_t *data_offset,
+                         uint64_t *n_tensors, uint64_t *n_kv);
+int yule_hip_gguf_tensor(const yule_gguf *g, uint64_t index, yule_gguf_tensor *out);
+int yule_hip_gguf_find(const yule_gguf *g, const char *name, yule_gguf_tensor *out);
+/* metadata lookups with GgufValue::as_u32 / as_f64 / as_str semantics
+ * (gguf.rs:50-90); YULE_ERR_INVALID when absent or of another type */
+int yule_hip_gguf_get_u32(const yule_gguf *g, const char *key, uint32_t *out);
+int yule_hip_gguf_get_f64(const yule_gguf *g, const char *key, double *out);
+int yule_hip_gguf_get_str(const yule_gguf *g, const char *key, const char **out);
+int yule_hip_gguf_get_array_len(const yule_gguf *g, const char *key, uint64_t *out);
+
+/* yule_hip_runner_create from a GGUF file of a dense Llama model
+ * (general.architecture llama or mistral): llama.* metadata and blk.N.*
+ * tensor names (weight_loader.rs:78-199), RunnerConfig defaults
+ * (model_runner.rs:384-465).  max_seq 0 takes llama.context_length. */
+int yule_hip_runner_create_from_gguf(yule_hip_backend *be, const char *path, uint32_t max_seq,
+                                     yule_hip_runner **out);
 
 /* ---- timing helpers for harnesses (no trait counterpart) ---- */
 

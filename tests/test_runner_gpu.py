@@ -114,3 +114,61 @@ def test_tinyllama_greedy_tokens_match_golden(hip, tinyllama):
                     f"(oracle top-2 margin there {g['top2_margin'][i]:.3g})")
     say(f"[runner] TinyLlama decode {ms:.3f} ms/step = {1000 / ms:.0f} tok/s")
     run.close()
+
+
+def test_runner_from_gguf_matches_in_memory(hip, tiny, tmp_path):
+    """yule_hip_runner_create_from_gguf over the model written as GGUF gives
+    bit-identical logits and tokens to the runner built from host arrays."""
+    say("[runner] small model from GGUF vs in-memory")
+    p = tmp_path / "tiny.gguf"
+    tiny.to_gguf(p)
+    a, b = HipRunner(hip, tiny), HipRunner.from_gguf(hip, p, max_seq=tiny.cfg.max_seq)
+    assert b.vocab == tiny.cfg.vocab
+    for t in synth.uniform_tokens(14, 12, tiny.cfg.vocab):
+        assert np.array_equal(a.decode_step(int(t)), b.decode_step(int(t)))
+    a.reset(), b.reset()
+    prompt = synth.uniform_tokens(15, 10, tiny.cfg.vocab)
+    assert np.array_equal(a.generate_greedy(prompt, 20)[0], b.generate_greedy(prompt, 20)[0])
+    a.close(), b.close()
+
+
+def test_runner_from_gguf_tied_output_and_errors(hip, tiny, tmp_path):
+    """No output.weight: the logits come from token_embd.weight
+    (weight_loader.rs:166-170); an unsupported architecture and a missing
+    tensor are refused before anything is uploaded."""
+    say("[runner] GGUF tied embeddings / errors")
+    from yule_amd.gguf import TensorEntry, model_metadata, write_gguf
+    from yule_amd.model import SyntheticModel as SM, Tensor
+    tied = dict(tiny.tensors)
+    e = tied["token_embd.weight"]
+    tied["output.weight"] = Tensor("output.weight", e.dtype, e.shape, e.data)
+    ref = HipRunner(hip, SM(tiny.cfg, tied, tiny.scheme, tiny.seed))
+    ents = [TensorEntry(t.name, int(t.dtype), t.shape, t.data) for n, t in tiny.tensors.items() if n != "output.weight"]
+    p = tmp_path / "tied.gguf"
+    write_gguf(p, model_metadata(tiny.cfg), ents)
+    run = HipRunner.from_gguf(hip, p)          # max_seq from llama.context_length
+    for t in (1, 2, 3):
+        assert np.array_equal(ref.decode_step(t), run.decode_step(t))
+    ref.close(), run.close()
+    q = tmp_path / "arch.gguf"
+    write_gguf(q, model_metadata(tiny.cfg, arch="mamba"), ents)
+    with pytest.raises(YuleGpuError, match="architecture"):
+        HipRunner.from_gguf(hip, q)
+    r = tmp_path / "missing.gguf"
+    write_gguf(r, model_metadata(tiny.cfg), [x for x in ents if x.name != "blk.1.ffn_up.weight"])
+    with pytest.raises(YuleGpuError, match="blk.1.ffn_up.weight"):
+        HipRunner.from_gguf(hip, r)
+
+
+def test_tinyllama_from_gguf_greedy_matches_golden(hip, tinyllama, tmp_path):
+    """The TinyLlama-shaped Q4_K_M model through a GGUF file: the full
+    128 + 256 greedy stream equals the golden one."""
+    g = json.loads((GOLDEN / "e2e_tinyllama_greedy.json").read_text())
+    say("[runner] TinyLlama from GGUF greedy vs golden")
+    p = tmp_path / "tinyllama.gguf"
+    tinyllama.to_gguf(p)
+    run = HipRunner.from_gguf(hip, p, max_seq=tinyllama.cfg.max_seq)
+    toks, _ = run.generate_greedy(np.array(g["prompt"], np.uint32), g["n_decode"])
+    assert [int(t) for t in toks] == g["tokens"]
+    run.close()
+    p.unlink()

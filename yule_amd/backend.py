@@ -62,6 +62,16 @@ _SIGS: dict[str, tuple] = {
     "yule_hip_runner_prefill": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p]),
     "yule_hip_runner_generate_greedy": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p,
                                                   C.POINTER(C.c_float)]),
+    "yule_hip_gguf_open": (C.c_int, [C.c_char_p, C.POINTER(C.c_void_p)]),
+    "yule_hip_gguf_close": (C.c_int, [C.c_void_p]),
+    "yule_hip_gguf_header": (C.c_int, [C.c_void_p, C.POINTER(C.c_uint32)] + [C.POINTER(C.c_uint64)] * 4),
+    "yule_hip_gguf_tensor": (C.c_int, [C.c_void_p, C.c_uint64, C.c_void_p]),
+    "yule_hip_gguf_find": (C.c_int, [C.c_void_p, C.c_char_p, C.c_void_p]),
+    "yule_hip_gguf_get_u32": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(C.c_uint32)]),
+    "yule_hip_gguf_get_f64": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(C.c_double)]),
+    "yule_hip_gguf_get_str": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(C.c_char_p)]),
+    "yule_hip_gguf_get_array_len": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(C.c_uint64)]),
+    "yule_hip_runner_create_from_gguf": (C.c_int, [C.c_void_p, C.c_char_p, C.c_uint32, C.POINTER(C.c_void_p)]),
     "yule_hip_timer_start": (C.c_int, [C.c_void_p]),
     "yule_hip_timer_stop": (C.c_int, [C.c_void_p, C.POINTER(C.c_float)]),
     "yule_hip_time_qmv_ops": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_int,
@@ -353,6 +363,21 @@ class HipRunner:
         backend._check(self._lib.yule_hip_runner_create(backend.raw, C.byref(desc), C.byref(r)))
         self._r = r
         self.vocab = cfg.vocab
+
+    @classmethod
+    def from_gguf(cls, backend: HipBackend, path, max_seq: int = 0) -> "HipRunner":
+        """Runner over a GGUF file (yule_hip_runner_create_from_gguf); max_seq
+        0 takes the file's context_length."""
+        from .gguf import GgufFile
+        with GgufFile(path) as g:
+            vocab = g.get_u32("tokenizer.ggml.vocab_size") or g.get_array_len("tokenizer.ggml.tokens") or 0
+        self = cls.__new__(cls)
+        self._be, self._lib = backend, backend._lib
+        r = C.c_void_p()
+        backend._check(self._lib.yule_hip_runner_create_from_gguf(backend.raw, str(path).encode(), max_seq,
+                                                                  C.byref(r)))
+        self._r, self.vocab = r, vocab
+        return self
 
     def close(self):
         if getattr(self, "_r", None):

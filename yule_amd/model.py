@@ -81,6 +81,13 @@ class SyntheticModel:
         embd = self.tensors["token_embd.weight"]
         return self.weight_bytes - embd.data.nbytes + matrix_bytes(embd.dtype, 1, c.dim)
 
+    def to_gguf(self, path, arch: str = "llama") -> int:
+        """Write the model as a GGUF v3 file (llama.* metadata, GGUF tensor
+        names and [cols, rows] shapes); returns the data-section offset."""
+        from .gguf import TensorEntry, model_metadata, write_gguf
+        ents = [TensorEntry(t.name, int(t.dtype), tuple(t.shape), t.data) for t in self.tensors.values()]
+        return write_gguf(path, model_metadata(self.cfg, arch, f"synthetic-{self.scheme}-{self.seed}"), ents)
+
     def digest(self) -> str:
         h = hashlib.sha256()
         for name in sorted(self.tensors):
