@@ -164,7 +164,12 @@ int yule_hip_silu_mul(yule_hip_backend *be, yule_buffer gate, yule_buffer up, yu
  * (yule-infer/src/model_runner.rs:679-758, shaders/multihead_attn.comp):
  * for each query head h (kv head h / (n_heads/n_kv_heads)):
  *   s_t = q_h . K_t / sqrt(hd); p = softmax(s); out_h = sum_t p_t V_t
- * k_cache/v_cache: [seq][n_kv_heads*head_dim] f32 rows, t < seq_len. */
+ * k_cache/v_cache: [seq][n_kv_heads*head_dim] f32 rows, t < seq_len.
+ * head_dim a multiple of 4, <= 256; seq_len <= 262144.  From 512 positions
+ * (environment YULE_ATTN_SPLIT_MIN) it runs split-KV (flash-decoding,
+ * shaders/flash_decode_split.comp + flash_decode_reduce.comp) when a KV
+ * head serves <= 8 query heads; above 16384 positions that is required.
+ * The split partials live in a backend-owned workspace. */
 int yule_hip_gqa_decode_attn(yule_hip_backend *be, yule_buffer q, yule_buffer k_cache,
                              yule_buffer v_cache, yule_buffer out, uint32_t n_heads,
                              uint32_t n_kv_heads, uint32_t head_dim, uint32_t seq_len);

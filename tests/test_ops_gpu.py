@@ -141,10 +141,10 @@ def test_gqa_decode_attn(hip, hd, nh, nkv, seq):
         with pytest.raises(YuleGpuError):           # head_dim must be a multiple of 4 here
             hip.gqa_decode_attn(hip.upload(q), hip.upload(kc), hip.upload(vc), hip.allocate(16), 2, 1, 2, 2)
         return
-    q, kc, vc = synth.gauss(8, nh * hd), synth.gauss(9, (seq, nkv * hd)), synth.gauss(10, (seq, nkv * hd))
-    hq, hk, hv, ho = hip.upload(q), hip.upload(kc), hip.upload(vc), hip.allocate(4 * nh * hd)
-    hip.gqa_decode_attn(hq, hk, hv, ho, nh, nkv, hd, seq)
-    got = hip.download(ho, nh * hd)
+    run_gqa_case(hip, hd, nh, nkv, seq)
+
+
+def gqa_ref(q, kc, vc, nh, nkv, hd):
     want = np.zeros(nh * hd)
     for h in range(nh):
         kv = h // (nh // nkv)
@@ -153,9 +153,53 @@ def test_gqa_decode_attn(hip, hd, nh, nkv, seq):
         p = np.exp(s - s.max())
         p /= p.sum()
         want[h * hd:(h + 1) * hd] = p @ vc[:, kv * hd:(kv + 1) * hd]
-    assert close(got, want, 1e-5)
+    return want
+
+
+def run_gqa_case(hip, hd, nh, nkv, seq, tol=1e-5):
+    q, kc, vc = synth.gauss(8, nh * hd), synth.gauss(9, (seq, nkv * hd)), synth.gauss(10, (seq, nkv * hd))
+    hq, hk, hv, ho = hip.upload(q), hip.upload(kc), hip.upload(vc), hip.allocate(4 * nh * hd)
+    hip.gqa_decode_attn(hq, hk, hv, ho, nh, nkv, hd, seq)
+    got = hip.download(ho, nh * hd)
     for h in (hq, hk, hv, ho):
         hip.free(h)
+    want = gqa_ref(q, kc, vc, nh, nkv, hd)
+    err = np.max(np.abs(got - want))
+    assert err <= tol, f"max error {err:.3g}"
+
+
+@pytest.mark.parametrize("hd,nh,nkv,seq", [(64, 8, 2, 1), (64, 8, 2, 65), (64, 32, 4, 384), (128, 32, 8, 1000),
+                                          (80, 8, 2, 77), (32, 4, 4, 33), (64, 24, 8, 300), (64, 40, 8, 500),
+                                          (256, 16, 2, 129), (128, 56, 8, 257), (64, 4, 4, 700)])
+def test_gqa_decode_attn_split_forced(hip, hd, nh, nkv, seq, monkeypatch):
+    """The split-KV path (per-chunk max / sum / partial output, then the
+    combine) at every group size 1..8 and every chunk length, forced on
+    short sequences."""
+    say(f"[ops] split gqa_decode_attn hd={hd} heads={nh}/{nkv} seq={seq}")
+    monkeypatch.setenv("YULE_ATTN_SPLIT_MIN", "1")
+    run_gqa_case(hip, hd, nh, nkv, seq)
+
+
+@pytest.mark.parametrize("hd,nh,nkv,seq", [(64, 32, 4, 5000), (128, 32, 8, 9000), (64, 32, 4, 20000),
+                                          (128, 64, 8, 17000)])
+def test_gqa_decode_attn_long(hip, hd, nh, nkv, seq):
+    """Long contexts: split-KV by default from 512 positions; above 16384
+    (the one-workgroup-per-head kernel's LDS limit) it is the only path."""
+    say(f"[ops] long gqa_decode_attn hd={hd} heads={nh}/{nkv} seq={seq}")
+    run_gqa_case(hip, hd, nh, nkv, seq)
+
+
+def test_gqa_decode_attn_limits(hip):
+    """More than 8 query heads per KV head: the per-head kernel up to 16384
+    positions, refused above; above 262144 positions refused for any shape."""
+    say("[ops] gqa_decode_attn limits")
+    run_gqa_case(hip, 64, 32, 2, 2000)
+    h = hip.allocate(4 * 64 * 32)
+    with pytest.raises(YuleGpuError, match="8 query heads"):
+        hip.gqa_decode_attn(h, h, h, h, 32, 2, 64, 16385)
+    with pytest.raises(YuleGpuError, match="262144"):
+        hip.gqa_decode_attn(h, h, h, h, 32, 4, 64, 262145)
+    hip.free(h)
 
 
 def test_argmax_kats(hip):

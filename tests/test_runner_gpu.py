@@ -28,13 +28,18 @@ def tiny():
     return SyntheticModel.generate(TINY_TEST, seed=3)
 
 
-@pytest.mark.parametrize("fused", [True, False], ids=["fused", "unfused"])
-def test_runner_logits_match_oracle_small(hip, tiny, fused, monkeypatch):
+@pytest.mark.parametrize("fused,split_min", [(True, None), (False, None), (True, "1"), (True, "20")],
+                         ids=["fused", "unfused", "split", "split-from-20"])
+def test_runner_logits_match_oracle_small(hip, tiny, fused, split_min, monkeypatch):
     """Both step sequences: fused (norm/SwiGLU staged into the matvec, residual
-    and argmax epilogues) and the plain kernel-per-operation sequence."""
-    say(f"[runner] small model logits vs oracle ({'fused' if fused else 'unfused'})")
+    and argmax epilogues) and the plain kernel-per-operation sequence; and
+    attention split-KV on every step, or from position 19 on (the runner
+    switching graphs mid-sequence)."""
+    say(f"[runner] small model logits vs oracle ({'fused' if fused else 'unfused'}, split from {split_min})")
     if not fused:
         monkeypatch.setenv("YULE_RUNNER_UNFUSED", "1")
+    if split_min:
+        monkeypatch.setenv("YULE_ATTN_SPLIT_MIN", split_min)
     run = HipRunner(hip, tiny)
     ref, f64 = oracle.Runner(tiny, n_threads=4), NpForward(tiny)
     for t in synth.uniform_tokens(11, 40, tiny.cfg.vocab):
@@ -172,3 +177,25 @@ def test_tinyllama_from_gguf_greedy_matches_golden(hip, tinyllama, tmp_path):
     assert [int(t) for t in toks] == g["tokens"]
     run.close()
     p.unlink()
+
+
+def test_runner_long_context_split(hip):
+    """A 2,600-position context (split-KV attention from position 511 on):
+    greedy tokens identical to the oracle's over a 2,500-token prompt and 100
+    decode steps."""
+    from dataclasses import replace
+    say("[runner] long context (2600) greedy vs oracle")
+    m = SyntheticModel.generate(replace(TINY_TEST, max_seq=2600), seed=4)
+    prompt = synth.uniform_tokens(16, 2500, m.cfg.vocab)
+    run = HipRunner(hip, m)
+    toks, _ = run.generate_greedy(prompt, 100)
+    ref = oracle.Runner(m, n_threads=1)
+    for t in prompt:
+        logits = ref.forward(int(t))
+    want = []
+    for i in range(101):
+        want.append(oracle.argmax(logits))
+        if i < 100:
+            logits = ref.forward(want[-1])
+    assert list(toks) == want
+    run.close()

@@ -377,16 +377,7 @@ __global__ void gemm_reduce_kernel(const float *__restrict__ part, float *__rest
 
 using namespace yule;
 
-// Per-backend scratch: X in f16 (permuted) and its sub-block sums (grown on
-// demand; one backend at a time).
 namespace {
-struct GemmScratch {
-    yule_hip_backend *be = nullptr;
-    void *p = nullptr;
-    size_t size = 0;
-};
-GemmScratch g_scratch;
-std::mutex g_scratch_mu;
 
 // Split count: none once the tiles alone fill every CU; below that, as many
 // splits as fit in one round of resident workgroups (two per CU), so that
@@ -437,19 +428,11 @@ extern "C" int yule_hip_quantized_gemm(yule_hip_backend *be, yule_buffer weights
     const size_t n_x = (size_t)m * n_cols, n_sub = (size_t)m * (n_cols / 32), n_y = (size_t)m * n_rows;
     const size_t part_bytes = ks > 1 ? ((ks * n_y * sizeof(float) + 255) & ~(size_t)255) : 0;
     const size_t need = part_bytes + (n_x + (q4 ? 2 * n_sub : 0)) * sizeof(_Float16) + 256;
-    std::lock_guard<std::mutex> lk(g_scratch_mu);
-    if (g_scratch.be != be || g_scratch.size < need) {
-        if (g_scratch.p) {
-            (void)hipStreamSynchronize(g_scratch.be ? g_scratch.be->stream : be->stream);
-            (void)hipFree(g_scratch.p);
-        }
-        g_scratch = GemmScratch{};
-        if ((rc = hip_error(hipMalloc(&g_scratch.p, need), "quantized_gemm: scratch"))) return rc;
-        g_scratch.be = be;
-        g_scratch.size = need;
-    }
-    float *part = ks > 1 ? static_cast<float *>(g_scratch.p) : nullptr;
-    _Float16 *xh = reinterpret_cast<_Float16 *>(static_cast<uint8_t *>(g_scratch.p) + part_bytes);
+    // workspace: split-K partials, then X in f16 (permuted) and its sub-block sums
+    void *ws;
+    if ((rc = get_scratch(be, need, &ws))) return rc;
+    float *part = ks > 1 ? static_cast<float *>(ws) : nullptr;
+    _Float16 *xh = reinterpret_cast<_Float16 *>(static_cast<uint8_t *>(ws) + part_bytes);
     _Float16 *xs_hi = q4 ? xh + n_x : nullptr, *xs_lo = q4 ? xs_hi + n_sub : nullptr;
     hipLaunchKernelGGL(gemm_xprep_kernel, dim3((unsigned)((n_sub + 255) / 256)), dim3(256), 0, be->stream,
                        (const uint16_t *)px, xh, xs_hi, xs_lo, m, n_cols);

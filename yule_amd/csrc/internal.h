@@ -33,6 +33,12 @@ struct yule_hip_backend {
     std::mutex mu;  // guards `buffers`; ComputeBackend is Send + Sync
     std::unordered_map<uint64_t, yule::Buffer> buffers;
     hipEvent_t timer[2] = {nullptr, nullptr};
+    // device workspace shared by the ops that need one (GEMM staging and
+    // split-K partials, split-KV attention partials); grown on demand,
+    // freed with the backend
+    std::mutex scratch_mu;
+    void *scratch = nullptr;
+    size_t scratch_size = 0;
 };
 
 namespace yule {
@@ -44,6 +50,11 @@ int hip_error(hipError_t e, const char *what);
 // Look up a handle and check that [offset, offset+need) lies inside it.
 int get_buffer(yule_hip_backend *be, uint64_t h, size_t need, void **ptr, const char *what,
                size_t offset = 0);
+
+// At least `need` bytes of the backend's workspace.  Growing it waits for
+// the stream (earlier launches may still read the old one); the pointer is
+// valid until the next call that grows it.
+int get_scratch(yule_hip_backend *be, size_t need, void **ptr);
 
 // Launch failures surface through hipGetLastError after a kernel launch.
 int check_launch(const char *what);
@@ -112,6 +123,16 @@ int launch_rope_kv(hipStream_t stream, float *q, const float *k, const float *v,
 int launch_attn_step(hipStream_t stream, const float *q, const float *k, const float *v, float *kc, float *vc,
                      const float *cos_t, const float *sin_t, const uint32_t *ctl, float *out, uint32_t n_heads,
                      uint32_t n_kv, uint32_t hd, uint32_t max_seq);
+// Split-KV (flash-decoding) attention: phase 1 over (KV head, chunk) and a
+// combine; with ctl it is the decode step (RoPE + KV write, sequence length
+// ctl[0] + 1 <= seq_cap), without it plain GQA over seq_cap rotated rows.
+// `scratch` holds split_scratch_bytes(n_heads, hd, seq_cap) bytes.
+bool split_attn_supported(uint32_t n_heads, uint32_t n_kv, uint32_t hd);
+uint32_t attn_split_min_seq();
+size_t split_scratch_bytes(uint32_t n_heads, uint32_t hd, uint32_t seq_cap);
+int launch_attn_split(hipStream_t stream, const float *q, const float *k, const float *v, float *kc, float *vc,
+                      const float *cos_t, const float *sin_t, const uint32_t *ctl, float *out, void *scratch,
+                      uint32_t n_heads, uint32_t n_kv, uint32_t hd, uint32_t seq_cap);
 int launch_argmax_advance(hipStream_t stream, const float *logits, uint32_t n, uint32_t *ctl, uint32_t *out_tokens);
 
 }  // namespace yule

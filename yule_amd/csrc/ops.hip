@@ -3,6 +3,7 @@
 // argmax the HIP runner uses.  Semantics follow CpuBackend
 // (yule-gpu/src/cpu.rs:163-539); f32 results agree to rounding, since
 // reductions run as trees instead of the reference's sequential loops.
+#include <cstdlib>
 #include <string>
 
 #include "blocks.h"
@@ -342,8 +343,11 @@ int yule_hip_gqa_decode_attn(yule_hip_backend *be, yule_buffer q, yule_buffer k_
         return set_error(YULE_ERR_INVALID, "gqa_decode_attn: n_heads must be a multiple of n_kv_heads");
     if (!head_dim || head_dim > kMaxHeadDim)
         return set_error(YULE_ERR_INVALID, "gqa_decode_attn: head_dim must be in 1..256");
-    if (!seq_len || seq_len > kMaxSeqLds)
-        return set_error(YULE_ERR_INVALID, "gqa_decode_attn: seq_len must be in 1..16384");
+    const bool split = seq_len >= attn_split_min_seq() || seq_len > kMaxSeqLds;
+    if (!seq_len || seq_len > 262144u)
+        return set_error(YULE_ERR_INVALID, "gqa_decode_attn: seq_len must be in 1..262144");
+    if (split && !split_attn_supported(n_heads, n_kv_heads, head_dim) && seq_len > kMaxSeqLds)
+        return set_error(YULE_ERR_UNSUPPORTED, "gqa_decode_attn: above 16384 positions needs <= 8 query heads per KV head");
     float *pq, *pk, *pv, *po;
     int rc;
     const size_t kv = (size_t)seq_len * n_kv_heads * head_dim;
@@ -353,6 +357,12 @@ int yule_hip_gqa_decode_attn(yule_hip_backend *be, yule_buffer q, yule_buffer k_
         (rc = f32buf(be, out, (size_t)n_heads * head_dim, &po, "gqa_decode_attn (out)")))
         return rc;
     if (head_dim % 4) return set_error(YULE_ERR_INVALID, "gqa_decode_attn: head_dim must be a multiple of 4");
+    if (split && split_attn_supported(n_heads, n_kv_heads, head_dim)) {
+        void *ws;
+        if ((rc = get_scratch(be, split_scratch_bytes(n_heads, head_dim, seq_len), &ws))) return rc;
+        return launch_attn_split(be->stream, pq, nullptr, nullptr, pk, pv, nullptr, nullptr, nullptr, po, ws, n_heads,
+                                 n_kv_heads, head_dim, seq_len);
+    }
     return launch_gqa_attn(be->stream, pq, pk, pv, po, n_heads, n_kv_heads, head_dim, seq_len);
 }
 
@@ -510,6 +520,255 @@ __global__ __launch_bounds__(256) void attn_step_kernel(const float *__restrict_
         for (uint32_t i = 0; i < ng; i++) acc += part[i * hd + tid];
         out[(size_t)h * hd + tid] = acc;
     }
+}
+
+// ------------------------------------------------------------ split-KV attention
+// Flash-decoding for long contexts (the reference's flash_decode_split.comp /
+// flash_decode_reduce.comp, vulkan/mod.rs:179-263): phase 1 runs one
+// workgroup per (KV head, chunk of positions) and serves all G query heads
+// of the group from one pass over the chunk's K and V rows, writing per head
+// the chunk maximum m_c, the sum l_c = sum_t exp(s_t - m_c) and the
+// unnormalised output o_c = sum_t exp(s_t - m_c) V_t; phase 2 combines the
+// chunks: out = sum_c exp(m_c - M) o_c / sum_c exp(m_c - M) l_c.
+// The chunk length is a function of the sequence length alone (split_chunk),
+// evaluated on the device in decode steps, so a captured graph sized for
+// max_seq serves every position; workgroups past the last chunk exit.
+constexpr uint32_t kSplitMaxGroup = 8;      // query heads per KV head
+constexpr uint32_t kSplitMinChunk = 64;
+constexpr uint32_t kSplitMaxChunks = 4096;  // chunks per head the combine handles (262144 positions)
+
+// 256 positions per chunk once that still gives two workgroups per CU, else
+// 128, else 64
+__host__ __device__ inline uint32_t split_chunk(uint32_t seq, uint32_t n_kv) {
+    const uint32_t target = 512;
+    if (n_kv * ((seq + 255) / 256) >= target) return 256;
+    if (n_kv * ((seq + 127) / 128) >= target) return 128;
+    return 64;
+}
+
+template <uint32_t G>
+__global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict__ q, const float *__restrict__ k,
+                                                         const float *__restrict__ v, float *__restrict__ kc,
+                                                         float *__restrict__ vc, const float *__restrict__ cos_t,
+                                                         const float *__restrict__ sin_t,
+                                                         const uint32_t *__restrict__ ctl, float *__restrict__ part,
+                                                         float2 *__restrict__ ml, uint32_t n_kv, uint32_t hd,
+                                                         uint32_t seq_host, uint32_t max_chunks) {
+    __shared__ __align__(16) float qs[G * kMaxHeadDim];
+    __shared__ __align__(16) float kn[kMaxHeadDim], vn[kMaxHeadDim];
+    __shared__ float pl[G * 256];
+    __shared__ __align__(16) float acc_lds[G * 1024];
+    __shared__ float red[4 * G];
+    const uint32_t kvh = blockIdx.x, chunk = blockIdx.y, tid = threadIdx.x;
+    const bool step = ctl != nullptr;
+    const uint32_t seq = step ? ctl[0] + 1 : seq_host;
+    const uint32_t pos = step ? seq - 1 : 0xFFFFFFFFu;
+    const uint32_t C = split_chunk(seq, n_kv), c0 = chunk * C;
+    if (c0 >= seq) return;   // uniform over the workgroup
+    const uint32_t len = min(C, seq - c0), kvs = n_kv * hd, half = hd / 2, h0 = kvh * G;
+    const bool own = step && pos - c0 < len;   // this chunk holds the new row
+    if (!step) {
+        for (uint32_t i = tid; i < G * hd; i += 256) qs[i] = q[(size_t)h0 * hd + i];
+    } else {
+        for (uint32_t i = tid; i < G * half; i += 256) {
+            const uint32_t g = i / half, j = i % half;
+            const float c = cos_t[(size_t)pos * half + j], sn = sin_t[(size_t)pos * half + j];
+            const float *qh = q + (size_t)(h0 + g) * hd;
+            const float x0 = qh[2 * j], x1 = qh[2 * j + 1];
+            qs[g * hd + 2 * j] = x0 * c - x1 * sn;
+            qs[g * hd + 2 * j + 1] = x0 * sn + x1 * c;
+        }
+        if (own) {
+            const float *kh = k + (size_t)kvh * hd, *vh = v + (size_t)kvh * hd;
+            for (uint32_t j = tid; j < half; j += 256) {
+                const float c = cos_t[(size_t)pos * half + j], sn = sin_t[(size_t)pos * half + j];
+                const float x0 = kh[2 * j], x1 = kh[2 * j + 1];
+                kn[2 * j] = x0 * c - x1 * sn;
+                kn[2 * j + 1] = x0 * sn + x1 * c;
+            }
+            for (uint32_t j = tid; j < hd; j += 256) vn[j] = vh[j];
+        }
+    }
+    __syncthreads();
+    if (own) {   // the only workgroup that touches row pos of this KV head
+        float *krow = kc + (size_t)pos * kvs + kvh * hd, *vrow = vc + (size_t)pos * kvs + kvh * hd;
+        for (uint32_t j = tid; j < hd; j += 256) { krow[j] = kn[j]; vrow[j] = vn[j]; }
+    }
+    // scores: LP = 256 / C adjacent lanes per position, each over a residue
+    // class of the row's float4s, combined by lane shuffles
+    const uint32_t LP = 256 / C, t = tid / LP, sub = tid % LP, nd4 = hd / 4;
+    const bool valid = t < len;
+    const uint32_t p = c0 + t;
+    float acc[G];
+#pragma unroll
+    for (uint32_t g = 0; g < G; g++) acc[g] = 0.f;
+    if (valid) {
+        const float4 *kr = reinterpret_cast<const float4 *>(p == pos ? kn : kc + (size_t)p * kvs + kvh * hd);
+        for (uint32_t c4 = sub; c4 < nd4; c4 += LP) {
+            const float4 kv = kr[c4];
+#pragma unroll
+            for (uint32_t g = 0; g < G; g++) {
+                const float4 qv = reinterpret_cast<const float4 *>(qs + g * hd)[c4];
+                acc[g] += qv.x * kv.x;
+                acc[g] += qv.y * kv.y;
+                acc[g] += qv.z * kv.z;
+                acc[g] += qv.w * kv.w;
+            }
+        }
+    }
+    const float scale = 1.0f / sqrtf((float)hd);
+    const uint32_t lane = tid & 63, w = tid >> 6;
+    float sc[G], m[G], l[G];
+#pragma unroll
+    for (uint32_t g = 0; g < G; g++) {
+        for (uint32_t off = 1; off < LP; off <<= 1) acc[g] += __shfl_xor(acc[g], off, 64);
+        sc[g] = valid ? acc[g] * scale : -INFINITY;
+        m[g] = wave_max(sc[g]);
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (uint32_t g = 0; g < G; g++) red[w * G + g] = m[g];
+    }
+    __syncthreads();
+#pragma unroll
+    for (uint32_t g = 0; g < G; g++) {
+        m[g] = fmaxf(fmaxf(red[g], red[G + g]), fmaxf(red[2 * G + g], red[3 * G + g]));
+        const float e = valid ? expf(sc[g] - m[g]) : 0.f;
+        if (valid && sub == 0) pl[g * 256 + t] = e;
+        l[g] = wave_sum(sub == 0 ? e : 0.f);
+    }
+    __syncthreads();   // every lane has read red[] (maxima); pl[] is complete
+    if (lane == 0) {
+#pragma unroll
+        for (uint32_t g = 0; g < G; g++) red[w * G + g] = l[g];
+    }
+    __syncthreads();
+#pragma unroll
+    for (uint32_t g = 0; g < G; g++) l[g] = (red[g] + red[G + g]) + (red[2 * G + g] + red[3 * G + g]);
+    // unnormalised output: lanes own a float4 of dims and a residue class of
+    // the chunk's positions; every V row loaded serves all G heads
+    const uint32_t ng = 256 / nd4, d4 = tid % nd4, gi = tid / nd4;
+    float4 o[G];
+#pragma unroll
+    for (uint32_t g = 0; g < G; g++) o[g] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (gi < ng) {
+        uint32_t tt = gi;
+        for (; tt + ng < len; tt += 2 * ng) {
+            const uint32_t pa = c0 + tt, pb = pa + ng;
+            const float4 va = reinterpret_cast<const float4 *>(pa == pos ? vn : vc + (size_t)pa * kvs + kvh * hd)[d4];
+            const float4 vb = reinterpret_cast<const float4 *>(pb == pos ? vn : vc + (size_t)pb * kvs + kvh * hd)[d4];
+#pragma unroll
+            for (uint32_t g = 0; g < G; g++) {
+                const float wa = pl[g * 256 + tt], wb = pl[g * 256 + tt + ng];
+                o[g].x += wa * va.x; o[g].y += wa * va.y; o[g].z += wa * va.z; o[g].w += wa * va.w;
+                o[g].x += wb * vb.x; o[g].y += wb * vb.y; o[g].z += wb * vb.z; o[g].w += wb * vb.w;
+            }
+        }
+        if (tt < len) {
+            const uint32_t pa = c0 + tt;
+            const float4 va = reinterpret_cast<const float4 *>(pa == pos ? vn : vc + (size_t)pa * kvs + kvh * hd)[d4];
+#pragma unroll
+            for (uint32_t g = 0; g < G; g++) {
+                const float wa = pl[g * 256 + tt];
+                o[g].x += wa * va.x; o[g].y += wa * va.y; o[g].z += wa * va.z; o[g].w += wa * va.w;
+            }
+        }
+#pragma unroll
+        for (uint32_t g = 0; g < G; g++) reinterpret_cast<float4 *>(acc_lds + (gi * G + g) * hd)[d4] = o[g];
+    }
+    __syncthreads();
+    for (uint32_t i = tid; i < G * hd; i += 256) {
+        const uint32_t g = i / hd, d = i % hd;
+        float a = 0.f;
+        for (uint32_t j = 0; j < ng; j++) a += acc_lds[(j * G + g) * hd + d];
+        part[((size_t)(h0 + g) * max_chunks + chunk) * hd + d] = a;
+    }
+    if (tid < G) ml[(size_t)(h0 + tid) * max_chunks + chunk] = make_float2(m[tid], l[tid]);
+}
+
+// Phase 2: one workgroup per query head.
+__global__ __launch_bounds__(256) void attn_combine_kernel(const float *__restrict__ part,
+                                                           const float2 *__restrict__ ml,
+                                                           const uint32_t *__restrict__ ctl, float *__restrict__ out,
+                                                           uint32_t n_kv, uint32_t hd, uint32_t seq_host,
+                                                           uint32_t max_chunks) {
+    __shared__ float wt[kSplitMaxChunks];
+    __shared__ float red[16];
+    const uint32_t h = blockIdx.x, tid = threadIdx.x;
+    const uint32_t seq = ctl ? ctl[0] + 1 : seq_host;
+    const uint32_t C = split_chunk(seq, n_kv), n_ch = (seq + C - 1) / C;
+    const float2 *mh = ml + (size_t)h * max_chunks;
+    float mx = -INFINITY;
+    for (uint32_t c = tid; c < n_ch; c += 256) mx = fmaxf(mx, mh[c].x);
+    mx = block_max(mx, red);
+    float lsum = 0.f;
+    for (uint32_t c = tid; c < n_ch; c += 256) {
+        const float2 v = mh[c];
+        const float e = expf(v.x - mx);
+        wt[c] = e;
+        lsum += e * v.y;
+    }
+    lsum = block_sum(lsum, red);   // its barriers also publish wt[]
+    const float inv = 1.0f / lsum;
+    const float *ph = part + (size_t)h * max_chunks * hd;
+    for (uint32_t d = tid; d < hd; d += 256) {
+        float a0 = 0.f, a1 = 0.f;
+        uint32_t c = 0;
+        for (; c + 1 < n_ch; c += 2) {
+            a0 += wt[c] * ph[(size_t)c * hd + d];
+            a1 += wt[c + 1] * ph[(size_t)(c + 1) * hd + d];
+        }
+        if (c < n_ch) a0 += wt[c] * ph[(size_t)c * hd + d];
+        out[(size_t)h * hd + d] = (a0 + a1) * inv;
+    }
+}
+
+bool split_attn_supported(uint32_t n_heads, uint32_t n_kv, uint32_t hd) {
+    return n_kv && n_heads % n_kv == 0 && n_heads / n_kv <= kSplitMaxGroup && hd % 4 == 0 && hd <= kMaxHeadDim;
+}
+
+// Sequence length from which attention runs split-KV (environment
+// YULE_ATTN_SPLIT_MIN, default 512); shorter sequences run one workgroup
+// per query head (attn_step_kernel).
+uint32_t attn_split_min_seq() {
+    const char *e = getenv("YULE_ATTN_SPLIT_MIN");
+    const long v = e ? strtol(e, nullptr, 10) : 0;
+    return v > 0 ? (uint32_t)v : 512u;
+}
+
+// grid chunks for a launch whose sequence length is at most `seq_cap`
+uint32_t split_max_chunks(uint32_t seq_cap) { return (seq_cap + kSplitMinChunk - 1) / kSplitMinChunk; }
+
+size_t split_scratch_bytes(uint32_t n_heads, uint32_t hd, uint32_t seq_cap) {
+    const size_t mc = split_max_chunks(seq_cap);
+    return (size_t)n_heads * mc * hd * sizeof(float) + (size_t)n_heads * mc * sizeof(float2) + 256;
+}
+
+int launch_attn_split(hipStream_t s, const float *q, const float *k, const float *v, float *kc, float *vc,
+                      const float *cos_t, const float *sin_t, const uint32_t *ctl, float *out, void *scratch,
+                      uint32_t n_heads, uint32_t n_kv, uint32_t hd, uint32_t seq_cap) {
+    const uint32_t mc = split_max_chunks(seq_cap);
+    if (mc > kSplitMaxChunks) return set_error(YULE_ERR_INVALID, "split attention: sequence too long");
+    float *part = static_cast<float *>(scratch);
+    float2 *ml = reinterpret_cast<float2 *>(part + (size_t)n_heads * mc * hd);
+    const uint32_t seq_host = ctl ? 0u : seq_cap;
+    const dim3 grid(n_kv, ctl ? mc : (seq_cap + split_chunk(seq_cap, n_kv) - 1) / split_chunk(seq_cap, n_kv));
+#define YULE_SPLIT_CASE(G)                                                                                       \
+    case G:                                                                                                      \
+        hipLaunchKernelGGL(attn_split_kernel<G>, grid, dim3(256), 0, s, q, k, v, kc, vc, cos_t, sin_t, ctl, part, \
+                           ml, n_kv, hd, seq_host, mc);                                                          \
+        break;
+    switch (n_heads / n_kv) {
+        YULE_SPLIT_CASE(1) YULE_SPLIT_CASE(2) YULE_SPLIT_CASE(3) YULE_SPLIT_CASE(4)
+        YULE_SPLIT_CASE(5) YULE_SPLIT_CASE(6) YULE_SPLIT_CASE(7) YULE_SPLIT_CASE(8)
+    default: return set_error(YULE_ERR_UNSUPPORTED, "split attention: more than 8 query heads per KV head");
+    }
+#undef YULE_SPLIT_CASE
+    int rc = check_launch("attn_split");
+    if (rc) return rc;
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(n_heads), dim3(256), 0, s, part, ml, ctl, out, n_kv, hd, seq_host,
+                       mc);
+    return check_launch("attn_combine");
 }
 
 int launch_attn_step(hipStream_t s, const float *q, const float *k, const float *v, float *kc, float *vc,

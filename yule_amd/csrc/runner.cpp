@@ -10,6 +10,7 @@
 // from a device control block (ctl = {pos, token, prompt_len}), so one HIP
 // graph captured once replays every step, prefill and decode alike; the
 // argmax kernel writes the next token and advances the position.
+#include <algorithm>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -40,8 +41,14 @@ struct yule_hip_runner {
     uint32_t *ctl_host = nullptr;  // pinned staging for ctl updates
     unsigned long long *amax = nullptr;  // lm_head argmax slot (packed key | row)
     bool fused = false;            // every matrix runs on the streaming matvec
-    hipGraph_t graph = nullptr;
-    hipGraphExec_t exec = nullptr;
+    // attention of steps whose sequence length (pos + 1) reaches split_min
+    // runs split-KV (attn_split_kernel + combine, partials in attn_ws);
+    // shorter ones run one workgroup per query head.  One captured graph
+    // per variant: [0] short, [1] split.
+    uint32_t split_min = 0;
+    void *attn_ws = nullptr;
+    hipGraph_t graph[2] = {nullptr, nullptr};
+    hipGraphExec_t exec[2] = {nullptr, nullptr};
     uint32_t pos = 0;  // host mirror of ctl[0]
 };
 
@@ -109,7 +116,7 @@ int upload_matrix(yule_hip_runner *r, const void *src, uint32_t dtype, uint32_t 
 // (SwiGLU moves into the down launch's staging when gate/up cannot pair)
 // and at the end [rms_norm + lm_head + argmax] [advance]; otherwise the
 // same operations as separate kernels.
-int enqueue_step(yule_hip_runner *r) {
+int enqueue_step(yule_hip_runner *r, bool split) {
     hipStream_t s = r->be->stream;
     const uint32_t qd = r->n_heads * r->hd, kvd = r->n_kv * r->hd;
     int rc;
@@ -140,9 +147,13 @@ int enqueue_step(yule_hip_runner *r) {
                 (rc = launch_qmv_fused(s, L.tv, &sv, 1, xin, r->dim, norm)))
                 return rc;
         }
-        if ((rc = launch_attn_step(s, r->q, r->k, r->v, L.kc, L.vc, r->cos_t, r->sin_t, r->ctl, r->attn, r->n_heads,
-                                   r->n_kv, r->hd, r->max_seq)))
-            return rc;
+        if (split)
+            rc = launch_attn_split(s, r->q, r->k, r->v, L.kc, L.vc, r->cos_t, r->sin_t, r->ctl, r->attn, r->attn_ws,
+                                   r->n_heads, r->n_kv, r->hd, r->max_seq);
+        else
+            rc = launch_attn_step(s, r->q, r->k, r->v, L.kc, L.vc, r->cos_t, r->sin_t, r->ctl, r->attn, r->n_heads,
+                                  r->n_kv, r->hd, std::min(r->max_seq, r->split_min));
+        if (rc) return rc;
         if (fuse) {
             QmvXf add;
             add.epi = kEpiAdd;
@@ -204,24 +215,29 @@ int enqueue_step(yule_hip_runner *r) {
     return launch_argmax_advance(s, r->logits, r->vocab, r->ctl, r->tokens);
 }
 
-int ensure_graph(yule_hip_runner *r) {
-    if (r->exec) return YULE_OK;
+int ensure_graph(yule_hip_runner *r, bool split) {
+    if (r->exec[split]) return YULE_OK;
     hipStream_t s = r->be->stream;
     int rc = hip_error(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "runner: begin capture");
     if (rc) return rc;
-    const int erc = enqueue_step(r);
-    rc = hip_error(hipStreamEndCapture(s, &r->graph), "runner: end capture");
+    const int erc = enqueue_step(r, split);
+    rc = hip_error(hipStreamEndCapture(s, &r->graph[split]), "runner: end capture");
     if (erc) return erc;
     if (rc) return rc;
-    return hip_error(hipGraphInstantiate(&r->exec, r->graph, nullptr, nullptr, 0), "runner: graph instantiate");
+    return hip_error(hipGraphInstantiate(&r->exec[split], r->graph[split], nullptr, nullptr, 0),
+                     "runner: graph instantiate");
 }
 
-// Replay the captured step, or (YULE_RUNNER_NO_GRAPH set, for tracing
-// profilers that do not follow graph launches) enqueue its kernels directly.
-int run_step(yule_hip_runner *r) {
+// Replay the captured step for position `pos`, or (YULE_RUNNER_NO_GRAPH set,
+// for tracing profilers that do not follow graph launches) enqueue its
+// kernels directly.
+int run_step(yule_hip_runner *r, uint32_t pos) {
     static const bool direct = getenv("YULE_RUNNER_NO_GRAPH") != nullptr;
-    if (direct) return enqueue_step(r);
-    return hip_error(hipGraphLaunch(r->exec, r->be->stream), "runner: graph launch");
+    const bool split = pos + 1 >= r->split_min;
+    if (direct) return enqueue_step(r, split);
+    int rc = ensure_graph(r, split);
+    if (rc) return rc;
+    return hip_error(hipGraphLaunch(r->exec[split], r->be->stream), "runner: graph launch");
 }
 
 int set_ctl(yule_hip_runner *r, uint32_t pos, uint32_t token, uint32_t prompt_len) {
@@ -249,11 +265,16 @@ int yule_hip_runner_create(yule_hip_backend *be, const yule_model_desc *d, yule_
     const uint32_t hd = d->dim / d->n_heads;
     if (hd % 4 || hd > 256)
         return set_error(YULE_ERR_INVALID, "runner_create: head_dim must be a multiple of 4 and <= 256");
-    if (d->max_seq > 16384) return set_error(YULE_ERR_INVALID, "runner_create: max_seq above 16384");
+    const bool can_split = split_attn_supported(d->n_heads, d->n_kv_heads, hd);
+    if (d->max_seq > (can_split ? 262144u : 16384u))
+        return set_error(YULE_ERR_INVALID, can_split ? "runner_create: max_seq above 262144"
+                                                     : "runner_create: max_seq above 16384 (more than 8 query heads "
+                                                       "per KV head)");
     auto *r = new yule_hip_runner();
     r->be = be;
     r->n_layers = d->n_layers; r->dim = d->dim; r->n_heads = d->n_heads; r->n_kv = d->n_kv_heads; r->hd = hd;
     r->ff = d->ff_dim; r->vocab = d->vocab; r->max_seq = d->max_seq; r->eps = d->norm_eps; r->rope_base = d->rope_base;
+    r->split_min = can_split ? std::min(attn_split_min_seq(), 16384u) : 0xFFFFFFFFu;
     const uint32_t qd = r->n_heads * hd, kvd = r->n_kv * hd;
     int rc = YULE_OK;
     auto fail = [&](int code) { yule_hip_runner_destroy(r); return code; };
@@ -306,6 +327,9 @@ int yule_hip_runner_create(yule_hip_backend *be, const yule_model_desc *d, yule_
         (rc = dev_alloc(r, (size_t)r->max_seq * 4, reinterpret_cast<void **>(&r->tokens))))
         return fail(rc);
     if ((rc = dev_alloc(r, sizeof(unsigned long long), reinterpret_cast<void **>(&r->amax)))) return fail(rc);
+    if (r->max_seq >= r->split_min &&
+        (rc = dev_alloc(r, split_scratch_bytes(r->n_heads, hd, r->max_seq), &r->attn_ws)))
+        return fail(rc);
     r->fused = getenv("YULE_RUNNER_UNFUSED") == nullptr && qmv_fusable(r->out_t, r->dim);
     for (const auto &L : r->layers)
         r->fused = r->fused && qmv_fusable(L.tq, r->dim) && qmv_fusable(L.tk, r->dim) && qmv_fusable(L.tv, r->dim) &&
@@ -321,8 +345,10 @@ int yule_hip_runner_create(yule_hip_backend *be, const yule_model_desc *d, yule_
 int yule_hip_runner_destroy(yule_hip_runner *r) {
     if (!r) return YULE_OK;
     if (r->be) hipStreamSynchronize(r->be->stream);
-    if (r->exec) hipGraphExecDestroy(r->exec);
-    if (r->graph) hipGraphDestroy(r->graph);
+    for (int i = 0; i < 2; i++) {
+        if (r->exec[i]) hipGraphExecDestroy(r->exec[i]);
+        if (r->graph[i]) hipGraphDestroy(r->graph[i]);
+    }
     for (void *p : r->allocs) hipFree(p);
     if (r->ctl_host) hipHostFree(r->ctl_host);
     delete r;
@@ -345,9 +371,8 @@ int yule_hip_runner_decode_step(yule_hip_runner *r, uint32_t token, float *logit
     if (r->pos >= r->max_seq) return set_error(YULE_ERR_INVALID, "context length exceeded");
     if (token >= r->vocab) return set_error(YULE_ERR_INVALID, "token id out of range");
     int rc;
-    if ((rc = ensure_graph(r))) return rc;
     if ((rc = set_ctl(r, r->pos, token, 0))) return rc;
-    if ((rc = run_step(r))) return rc;
+    if ((rc = run_step(r, r->pos))) return rc;
     r->pos++;
     if (logits &&
         (rc = hip_error(hipMemcpyAsync(logits, r->logits, (size_t)r->vocab * 4, hipMemcpyDeviceToHost, r->be->stream),
@@ -377,18 +402,20 @@ int yule_hip_runner_generate_greedy(yule_hip_runner *r, const uint32_t *prompt, 
         if (prompt[i] >= r->vocab) return set_error(YULE_ERR_INVALID, "runner_generate: token id out of range");
     hipStream_t s = r->be->stream;
     int rc;
-    if ((rc = ensure_graph(r))) return rc;
+    // both graph variants the run needs are captured before the timed loop
+    if ((rc = ensure_graph(r, false))) return rc;
+    if (n_prompt + n_decode >= r->split_min && (rc = ensure_graph(r, true))) return rc;
     if ((rc = hip_error(hipMemcpyAsync(r->prompt, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice, s),
                         "runner: prompt upload")))
         return rc;
     if ((rc = set_ctl(r, 0, 0, n_prompt))) return rc;
     for (uint32_t i = 0; i < n_prompt; i++)
-        if ((rc = run_step(r))) return rc;
+        if ((rc = run_step(r, i))) return rc;
     hipEvent_t e0 = nullptr, e1 = nullptr;
     if ((rc = hip_error(hipEventCreate(&e0), "hipEventCreate")) || (rc = hip_error(hipEventCreate(&e1), "hipEventCreate")))
         goto done;
     if ((rc = hip_error(hipEventRecord(e0, s), "hipEventRecord"))) goto done;
-    for (uint32_t i = 0; i < n_decode && !rc; i++) rc = run_step(r);
+    for (uint32_t i = 0; i < n_decode && !rc; i++) rc = run_step(r, n_prompt + i);
     if (rc || (rc = hip_error(hipEventRecord(e1, s), "hipEventRecord"))) goto done;
     if ((rc = hip_error(hipEventSynchronize(e1), "hipEventSynchronize"))) goto done;
     if (ms_per_decode_step) {

@@ -36,6 +36,24 @@ int check_launch(const char *what) {
     return e == hipSuccess ? YULE_OK : hip_error(e, what);
 }
 
+int get_scratch(yule_hip_backend *be, size_t need, void **ptr) {
+    std::lock_guard<std::mutex> lk(be->scratch_mu);
+    if (be->scratch_size < need) {
+        int rc;
+        if (be->scratch) {
+            if ((rc = hip_error(hipStreamSynchronize(be->stream), "scratch: synchronize"))) return rc;
+            (void)hipFree(be->scratch);
+            be->scratch = nullptr;
+            be->scratch_size = 0;
+        }
+        const size_t sz = (need + ((size_t)1 << 20) - 1) & ~(((size_t)1 << 20) - 1);
+        if ((rc = hip_error(hipMalloc(&be->scratch, sz), "scratch: allocate"))) return rc;
+        be->scratch_size = sz;
+    }
+    *ptr = be->scratch;
+    return YULE_OK;
+}
+
 int get_buffer(yule_hip_backend *be, uint64_t h, size_t need, void **ptr, const char *what, size_t offset) {
     std::lock_guard<std::mutex> lk(be->mu);
     auto it = be->buffers.find(h);
@@ -123,6 +141,7 @@ int yule_hip_destroy(yule_hip_backend *be) {
     hipStreamSynchronize(be->stream);
     for (auto &kv : be->buffers) hipFree(kv.second.ptr);
     be->buffers.clear();
+    if (be->scratch) hipFree(be->scratch);
     for (hipEvent_t e : be->timer)
         if (e) hipEventDestroy(e);
     hipStreamDestroy(be->stream);
