@@ -34,14 +34,15 @@ namespace yule {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-// Tiling: a 256-thread workgroup computes a BM (m) x 128 (r) tile; each of
-// its four waves a BM/2 x 64 sub-tile of MFMA 16x16x32 tiles.  K advances in
+// Tiling: a workgroup of 2*BN threads computes a BM (m) x BN (r) tile, BN
+// 128 or 256; its waves, two along m and BN/64 along r, each a BM/2 x 64
+// sub-tile of MFMA 16x16x32 tiles.  K advances in
 // stages of 64 (a quarter super-block): X and weight bytes of stage s+2 are
 // loaded into registers while stage s runs on the MFMAs out of one LDS buffer
 // and stage s+1 is dequantized into the other, one barrier per stage.  LDS
 // rows are padded to 72 halves (36 dwords: 16 consecutive rows of a
 // ds_read_b128 land on distinct banks).
-constexpr int GBN = 128, GSK = 64, GLD = GSK + 8;
+constexpr int GSK = 64, GLD = GSK + 8;
 
 __device__ __forceinline__ _Float16 bf16_to_f16(uint16_t b) {
     return (_Float16)__builtin_bit_cast(float, (uint32_t)b << 16);
@@ -116,31 +117,48 @@ struct GemmRegs {
     uint32_t mql, mqh, msc, md;
 };
 
-// Split-K: workgroup z of gridDim.z takes super-blocks [kb_lo, kb_hi) and,
-// when gridDim.z > 1, writes its partial tile to y + z*M*N (summed in a
+// Split-K: split z of `splits` takes super-blocks [kb_lo, kb_hi) and,
+// when splits > 1, writes its partial tile to y + z*M*N (summed in a
 // fixed order by gemm_reduce_kernel, so results do not depend on timing).
 // Q4_K runs two waves per SIMD (the register budget holds with a few spilled
 // bytes); Q6_K's larger dequant state keeps it at one.
-template <uint32_t DT, int BM>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DT == YULE_DTYPE_Q4_K ? 2 : 1))) void gemm_kernel(
+template <uint32_t DT, int BM, int BN>
+__global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YULE_DTYPE_Q4_K ? 2 : 1))) void gemm_kernel(
     const uint8_t *__restrict__ w, const _Float16 *__restrict__ xh, float *__restrict__ y,
-    const _Float16 *__restrict__ xs_hi, const _Float16 *__restrict__ xs_lo, uint32_t M, uint32_t N, uint32_t K) {
+    const _Float16 *__restrict__ xs_hi, const _Float16 *__restrict__ xs_lo, uint32_t M, uint32_t N, uint32_t K,
+    uint32_t xcd_remap) {
     constexpr bool Q4 = DT == YULE_DTYPE_Q4_K;
     constexpr uint32_t BB = Q4 ? 144 : 210;
     constexpr int TM = BM / 32;                 // 16-row MFMA tiles per wave along m
-    constexpr int XCH = BM * GSK / 8 / 256;     // 16-byte X chunks per thread per stage
+    constexpr uint32_t NTH = 2 * BN;            // threads: two per weight row of the tile
+    constexpr uint32_t WNN = BN / 64;           // waves along n (two along m)
+    constexpr int XCH = BM * GSK / 8 / NTH;     // 16-byte X chunks per thread per stage
     __shared__ __align__(16) _Float16 sx[2][BM * GLD];
-    __shared__ __align__(16) _Float16 sw[2][GBN * GLD];
-    __shared__ float sd[2][GBN];
+    __shared__ __align__(16) _Float16 sw[2][BN * GLD];
+    __shared__ float sd[2][BN];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t wm = wave >> 1, wn = wave & 1u;
-    const uint32_t m0 = blockIdx.y * BM, r0 = blockIdx.x * GBN;
+    const uint32_t wm = wave / WNN, wn = wave % WNN;
+    // Tile of this workgroup.  The grid is one-dimensional over
+    // (split, m tile, n tile), n fastest; workgroups are dispatched to the
+    // eight XCDs round-robin by id, so ids are remapped to give each XCD a
+    // contiguous range of tiles: the workgroups resident on one XCD then
+    // share one m tile, whose X rows stay in that XCD's L2 instead of being
+    // re-read from the last-level cache by every n tile.
+    const uint32_t nt = (N + BN - 1) / BN, mt = (M + BM - 1) / BM, tiles = nt * mt;
+    const uint32_t splits = gridDim.x / tiles;
+    uint32_t t = blockIdx.x;
+    if (xcd_remap) {
+        const uint32_t q = gridDim.x / 8u, rmd = gridDim.x % 8u, xcd = t % 8u;
+        t = xcd * q + (xcd < rmd ? xcd : rmd) + t / 8u;
+    }
+    const uint32_t zs = t / tiles, tm = (t % tiles) / nt, tn = t % nt;
+    const uint32_t m0 = tm * BM, r0 = tn * BN;
     const uint32_t bpr = K / 256;
-    const uint32_t kb_lo = (uint32_t)((uint64_t)bpr * blockIdx.z / gridDim.z);
-    const uint32_t kb_hi = (uint32_t)((uint64_t)bpr * (blockIdx.z + 1) / gridDim.z);
+    const uint32_t kb_lo = (uint32_t)((uint64_t)bpr * zs / splits);
+    const uint32_t kb_hi = (uint32_t)((uint64_t)bpr * (zs + 1) / splits);
     const uint32_t S = 4 * (kb_hi - kb_lo);     // stages of this split (>= 4)
     const size_t row_bytes = (size_t)bpr * BB;
-    if (gridDim.z > 1) y += (size_t)blockIdx.z * M * N;
+    if (splits > 1) y += (size_t)zs * M * N;
 
     floatx4 acc[TM][4], tmp[TM][4];
 #pragma unroll
@@ -157,7 +175,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DT == YULE_
         const uint32_t kb = kb_lo + (s >> 2), st = s & 3u, k0 = kb * 256u + st * GSK;
 #pragma unroll
         for (int i = 0; i < XCH; i++) {
-            const uint32_t idx = tid + 256u * i, row = idx >> 3, c = idx & 7u;
+            const uint32_t idx = tid + NTH * i, row = idx >> 3, c = idx & 7u;
             const uint32_t m = m0 + row < M ? m0 + row : M - 1u;
             R.x[i] = *reinterpret_cast<const uint4 *>(xh + (size_t)m * K + k0 + 8u * c);
         }
@@ -178,7 +196,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DT == YULE_
         const uint32_t kb = s >> 2, st = s & 3u;   // kb relative to the split (LDS slot parity only)
 #pragma unroll
         for (int i = 0; i < XCH; i++) {
-            const uint32_t idx = tid + 256u * i, row = idx >> 3, c = idx & 7u;
+            const uint32_t idx = tid + NTH * i, row = idx >> 3, c = idx & 7u;
             *reinterpret_cast<uint4 *>(sx[b] + row * GLD + 8u * c) = m0 + row < M ? R.x[i] : make_uint4(0, 0, 0, 0);
         }
         _Float16 *dst = sw[b] + wr * GLD;
@@ -382,9 +400,19 @@ namespace {
 // Split count: none once the tiles alone fill every CU; below that, as many
 // splits as fit in one round of resident workgroups (two per CU), so that
 // small-M launches keep all CUs busy without a partial second round.
-uint32_t gemm_splits(uint32_t m, uint32_t n, uint32_t k) {
+// Tile width along the weight rows: 256 (eight waves) halves the X bytes
+// each weight tile is multiplied against and measured 5-30% faster once M
+// fills the CUs with wide tiles (M >= 1024; Q6_K, whose dequant is dearer,
+// from M >= 512); 128 (four waves) below that.  YULE_GEMM_BN overrides.
+uint32_t gemm_bn(uint32_t m, uint32_t dtype) {
+    static const int env = env_int("YULE_GEMM_BN", 0);
+    if (env == 128 || env == 256) return (uint32_t)env;
+    return m >= 1024 || (dtype == YULE_DTYPE_Q6_K && m >= 512) ? 256u : 128u;
+}
+
+uint32_t gemm_splits(uint32_t m, uint32_t n, uint32_t k, uint32_t bn) {
     const uint32_t bm = m <= 64 ? 64 : 128;
-    const uint32_t tiles = ((n + GBN - 1) / GBN) * ((m + bm - 1) / bm);
+    const uint32_t tiles = ((n + bn - 1) / bn) * ((m + bm - 1) / bm);
     const uint32_t cus = (uint32_t)device_cus();
     if (tiles >= cus) return 1;
     uint32_t ks = 2 * cus / tiles;
@@ -392,16 +420,25 @@ uint32_t gemm_splits(uint32_t m, uint32_t n, uint32_t k) {
     return ks < 1 ? 1 : ks > bpr ? bpr : ks;
 }
 
+template <uint32_t DT, int BN>
+void launch_gemm_bn(hipStream_t s, const uint8_t *w, const _Float16 *xh, float *y, const _Float16 *xs_hi,
+                    const _Float16 *xs_lo, uint32_t m, uint32_t n, uint32_t k, uint32_t ks) {
+    static const uint32_t remap = (uint32_t)env_int("YULE_GEMM_XCD_REMAP", 1);
+    const uint32_t nt = (n + BN - 1) / BN;
+    if (m <= 64) {
+        hipLaunchKernelGGL((gemm_kernel<DT, 64, BN>), dim3(nt * ((m + 63) / 64) * ks), dim3(2 * BN), 0, s, w, xh, y,
+                           xs_hi, xs_lo, m, n, k, remap);
+    } else {
+        hipLaunchKernelGGL((gemm_kernel<DT, 128, BN>), dim3(nt * ((m + 127) / 128) * ks), dim3(2 * BN), 0, s, w, xh,
+                           y, xs_hi, xs_lo, m, n, k, remap);
+    }
+}
+
 template <uint32_t DT>
 void launch_gemm(hipStream_t s, const uint8_t *w, const _Float16 *xh, float *y, const _Float16 *xs_hi,
-                 const _Float16 *xs_lo, uint32_t m, uint32_t n, uint32_t k, uint32_t ks) {
-    if (m <= 64) {
-        hipLaunchKernelGGL((gemm_kernel<DT, 64>), dim3((n + GBN - 1) / GBN, (m + 63) / 64, ks), dim3(256), 0, s, w,
-                           xh, y, xs_hi, xs_lo, m, n, k);
-    } else {
-        hipLaunchKernelGGL((gemm_kernel<DT, 128>), dim3((n + GBN - 1) / GBN, (m + 127) / 128, ks), dim3(256), 0, s, w,
-                           xh, y, xs_hi, xs_lo, m, n, k);
-    }
+                 const _Float16 *xs_lo, uint32_t m, uint32_t n, uint32_t k, uint32_t ks, uint32_t bn) {
+    if (bn == 256) launch_gemm_bn<DT, 256>(s, w, xh, y, xs_hi, xs_lo, m, n, k, ks);
+    else launch_gemm_bn<DT, 128>(s, w, xh, y, xs_hi, xs_lo, m, n, k, ks);
 }
 }  // namespace
 
@@ -424,7 +461,7 @@ extern "C" int yule_hip_quantized_gemm(yule_hip_backend *be, yule_buffer weights
     if (!m || !n_rows) return YULE_OK;
     if (!n_cols) return launch_fill(be->stream, (float *)py, 0.f, (uint64_t)m * n_rows);
     const bool q4 = dtype == YULE_DTYPE_Q4_K;
-    const uint32_t ks = gemm_splits(m, n_rows, n_cols);
+    const uint32_t bn = gemm_bn(m, dtype), ks = gemm_splits(m, n_rows, n_cols, bn);
     const size_t n_x = (size_t)m * n_cols, n_sub = (size_t)m * (n_cols / 32), n_y = (size_t)m * n_rows;
     const size_t part_bytes = ks > 1 ? ((ks * n_y * sizeof(float) + 255) & ~(size_t)255) : 0;
     const size_t need = part_bytes + (n_x + (q4 ? 2 * n_sub : 0)) * sizeof(_Float16) + 256;
@@ -439,10 +476,11 @@ extern "C" int yule_hip_quantized_gemm(yule_hip_backend *be, yule_buffer weights
     if ((rc = check_launch("quantized_gemm: x pre-pass"))) return rc;
     float *out = ks > 1 ? part : (float *)py;
     if (q4)
-        launch_gemm<YULE_DTYPE_Q4_K>(be->stream, (const uint8_t *)pw, xh, out, xs_hi, xs_lo, m, n_rows, n_cols, ks);
+        launch_gemm<YULE_DTYPE_Q4_K>(be->stream, (const uint8_t *)pw, xh, out, xs_hi, xs_lo, m, n_rows, n_cols, ks,
+                                     bn);
     else
         launch_gemm<YULE_DTYPE_Q6_K>(be->stream, (const uint8_t *)pw, xh, out, nullptr, nullptr, m, n_rows, n_cols,
-                                     ks);
+                                     ks, bn);
     if ((rc = check_launch("quantized_gemm"))) return rc;
     if (ks > 1) {
         hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)((n_y + 255) / 256)), dim3(256), 0, be->stream, part,
