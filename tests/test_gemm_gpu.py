@@ -75,6 +75,30 @@ def test_gemm_config_shapes(hip, N, K):
         hip.free(h)
 
 
+@pytest.mark.parametrize("dt,M,N,K", [(DType.Q4_K, 1024, 300, 1024), (DType.Q4_K, 1100, 513, 512),
+                                      (DType.Q6_K, 512, 260, 768), (DType.Q6_K, 1030, 129, 256)],
+                         ids=lambda v: getattr(v, "name", str(v)))
+def test_gemm_wide_tiles(hip, dt, M, N, K):
+    """M large enough for the 128 x 256 tiles (eight waves), ragged N and M:
+    sampled rows vs the oracle, every row vs the GPU matvec of that row."""
+    say(f"[gemm] wide tiles {dt.name} M={M} N={N} K={K}")
+    w = synth.gen_quant(dt, 90 + M, N, K)
+    xb = bf16_bits(synth.gauss(91 + K, (M, K)))
+    y = run_gemm(hip, dt, w, xb, M, N, K)
+    xf = bf16_to_f32(xb).reshape(M, K)
+    for m in (0, 1, 127, 128, 255, M // 2, M - 1):
+        ref = oracle.qmv_f64(int(dt), w, xf[m], N, K)
+        assert np.max(np.abs(y[m] - ref)) <= tolerance_bar(ref), f"row {m}"
+    hw, hx, hy = hip.upload(w), hip.allocate(4 * K), hip.allocate(4 * N)
+    for m in range(M):
+        hip.copy_to_device(xf[m], hx)
+        hip.quantized_matmul(hw, hx, hy, N, K, dt)
+        mv = hip.download(hy, N)
+        assert np.max(np.abs(y[m] - mv)) <= 2 * tolerance_bar(mv), f"row {m} vs matvec"
+    for h in (hw, hx, hy):
+        hip.free(h)
+
+
 def test_gemm_errors(hip):
     w = synth.gen_quant(DType.Q4_K, 1, 16, 256)
     hw, hx, hy = hip.upload(w), hip.allocate(2 * 256 * 4), hip.allocate(4 * 16 * 4)
