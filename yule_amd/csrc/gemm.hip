@@ -25,6 +25,7 @@
 //    masks deliver weights, so neither side is shuffled in the main loop.
 //
 #include <mutex>
+#include <type_traits>
 #include <string>
 
 #include "qmv_common.h"
@@ -210,18 +211,20 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
             const uint32_t A = low ? hd.y : hd.w;
             const uint32_t mA = low ? 0x3F3Fu : 0x0F0Fu, mB = low ? 0u : 0x3030u;
             const uint32_t scs = ((A >> sh) & mA) | ((hd.y >> (sh + 2)) & mB);
+            // high nibbles stay in place (16 q * 2^-24, still a denormal
+            // pair) against sc * 2^6, so the product is again sc * q * 2^-14
             const _Float16 f0 = (_Float16)(float)((scs & 0xFFu) * 1024u);
-            const _Float16 f1 = (_Float16)(float)((scs >> 8) * 1024u);
+            const _Float16 f1 = (_Float16)(float)((scs >> 8) * 64u);
             const h2v S0 = {f0, f0}, S1 = {f1, f1};
             const uint32_t q[4] = {R.q.x, R.q.y, R.q.z, R.q.w};
             uint32_t lo[8], hi[8];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const uint32_t v = q[i], v4 = v >> 4;
+                const uint32_t v = q[i], v8 = v >> 8;
                 lo[2 * i] = pk_scale(v & 0x000F000Fu, S0);
-                lo[2 * i + 1] = pk_scale((v >> 8) & 0x000F000Fu, S0);
-                hi[2 * i] = pk_scale(v4 & 0x000F000Fu, S1);
-                hi[2 * i + 1] = pk_scale((v4 >> 8) & 0x000F000Fu, S1);
+                lo[2 * i + 1] = pk_scale(v8 & 0x000F000Fu, S0);
+                hi[2 * i] = pk_scale(v & 0x00F000F0u, S1);
+                hi[2 * i + 1] = pk_scale(v8 & 0x00F000F0u, S1);
             }
             o[0] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
             o[1] = make_uint4(lo[4], lo[5], lo[6], lo[7]);
@@ -268,7 +271,10 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
         }
     };
 
-    auto compute = [&](int b) {
+    // first: this stage opens a super-block, so its first k-step starts
+    // each tile's partial from zero (no separate clearing of tmp)
+    auto compute = [&](int b, auto first_t) {
+        constexpr bool first = decltype(first_t)::value;
 #pragma unroll
         for (int ks = 0; ks < GSK / 32; ks++) {
             half8 a[TM], bw[4];
@@ -284,7 +290,8 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
             for (int i = 0; i < TM; i++)
 #pragma unroll
                 for (int j = 0; j < 4; j++)
-                    tmp[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], bw[j], tmp[i][j], 0, 0, 0);
+                    tmp[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        a[i], bw[j], first && ks == 0 ? floatx4{0, 0, 0, 0} : tmp[i][j], 0, 0, 0);
         }
     };
     auto block_done = [&](uint32_t kb) {   // final += d[r] * super-block partial
@@ -294,7 +301,7 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
 #pragma unroll
             for (int i = 0; i < TM; i++) {
                 acc[i][j] += dr * tmp[i][j];
-                tmp[i][j] = floatx4{0, 0, 0, 0};
+                if constexpr (!Q4) tmp[i][j] = floatx4{0, 0, 0, 0};
             }
         }
     };
@@ -305,18 +312,51 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
     dequant_stage(0, R0, 0);
     load_stage(2 < S ? 2 : S - 1, R0);
     __syncthreads();
-    for (uint32_t s = 0; s < S; s += 2) {   // S = 4 * bpr is even
-        compute(0);
-        dequant_stage(s + 1, R1, 1);
-        load_stage(s + 3 < S ? s + 3 : S - 1, R1);
-        __syncthreads();
-        compute(1);
-        if (((s + 1) & 3u) == 3u) block_done((s + 1) >> 2);
-        if (s + 2 < S) {
+    // Q4_K: one super-block (four stages) per pass; stage t computes out of
+    // LDS buffer t & 1 while stage t + 1 is dequantized into the other and
+    // the bytes of stage t + 3 load into the register set stage t + 1 freed.
+    // The pass's first stage starts every tile's partial from zero.  Q6_K,
+    // whose dequant state is larger, keeps a two-stage pass (the longer one
+    // spills) and clears the partials in block_done.
+    // The last pass's final dequant and load are unconditional (stage S does
+    // not exist: its dequant writes LDS buffer 0 and scale slot (S/4) & 1,
+    // which nothing reads any more, and the load re-reads stage S - 1): a
+    // branch there would make the compiler wait for every load in flight at
+    // the loop head instead of only for the stage about to be dequantized.
+    const std::integral_constant<bool, true> opens{};
+    const std::integral_constant<bool, false> cont{};
+    if constexpr (Q4) {
+        for (uint32_t s = 0; s < S; s += 4) {
+            compute(0, opens);
+            dequant_stage(s + 1, R1, 1);
+            load_stage(s + 3 < S ? s + 3 : S - 1, R1);
+            __syncthreads();
+            compute(1, cont);
             dequant_stage(s + 2, R0, 0);
             load_stage(s + 4 < S ? s + 4 : S - 1, R0);
+            __syncthreads();
+            compute(0, cont);
+            dequant_stage(s + 3, R1, 1);
+            load_stage(s + 5 < S ? s + 5 : S - 1, R1);
+            __syncthreads();
+            compute(1, cont);
+            block_done(s >> 2);
+            dequant_stage(s + 4, R0, 0);
+            load_stage(s + 6 < S ? s + 6 : S - 1, R0);
+            __syncthreads();
         }
-        __syncthreads();
+    } else {
+        for (uint32_t s = 0; s < S; s += 2) {
+            compute(0, cont);
+            dequant_stage(s + 1, R1, 1);
+            load_stage(s + 3 < S ? s + 3 : S - 1, R1);
+            __syncthreads();
+            compute(1, cont);
+            if (((s + 1) & 3u) == 3u) block_done((s + 1) >> 2);
+            dequant_stage(s + 2, R0, 0);
+            load_stage(s + 4 < S ? s + 4 : S - 1, R0);
+            __syncthreads();
+        }
     }
 
     if constexpr (Q4) {
