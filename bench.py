@@ -129,6 +129,30 @@ def matrix_rate(hip, layer, name, launches):
     return us, gbs
 
 
+def read_probe(hip, layer, name, launches, n_wg=2048):
+    """What one launch that only streams the same weight bytes achieves
+    (yule_hip_read_probe, grid-stride 16-byte loads, 2048 workgroups),
+    over the same rotating copies as the matrix it stands beside.  The XOR
+    checksum of the first launch is checked against the host bytes."""
+    _, r, c = next(s for s in layer.shapes if s[0] == name)
+    nbytes = matrix_bytes(layer.dt, r, c)
+    part = hip.allocate(4 * n_wg)
+    hip.read_probe(layer.w[name][0], nbytes, part, n_wg)
+    got = int(np.bitwise_xor.reduce(hip.download(part, n_wg, np.uint32)))
+    want = int(np.bitwise_xor.reduce(np.ascontiguousarray(layer.host[name]).view(np.uint32).ravel()))
+    if got != want:
+        raise RuntimeError(f"read probe checksum {got:#x} != host {want:#x}")
+    for i in range(64):
+        hip.read_probe(layer.w[name][i % layer.copies], nbytes, part, n_wg)
+    hip.timer_start()
+    for i in range(launches):
+        hip.read_probe(layer.w[name][i % layer.copies], nbytes, part, n_wg)
+    us = hip.timer_stop() * 1e3 / launches
+    hip.free(part)
+    return {"us": round(us, 3), "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1), "bytes": nbytes,
+            "launch": "yule_hip_read_probe, 2048 x 256 threads, back-to-back stream launches"}
+
+
 def cpu_baseline(layer, budget_s=12.0, max_passes=2000):
     """Yule's CPU decode matvec path (oracle restatement of model_runner.rs:
     152-244 + simd/avx2.rs) over the same Q4_K layer bytes, host-resident."""
@@ -344,6 +368,10 @@ def main():
                 "kernel": "qmv_stream_kernel<Q4K,64,2,256> 14336x4096", "avg_launch_us": round(us, 3),
                 "algo_bytes_per_launch": dom_bytes}
     log(f"dominant kernel Q4_K 14336x4096: {us:.2f} us/launch, {gbs:.1f} GB/s")
+    roofline["read_probe"] = read_probe(hip, q4k, "ffn_gate", n_dom)
+    roofline["frac_of_read_probe"] = round(gbs / roofline["read_probe"]["GB/s"], 4)
+    log(f"read probe over the same weight copies: {roofline['read_probe']['us']:.2f} us/launch, "
+        f"{roofline['read_probe']['GB/s']:.1f} GB/s")
 
     extra = {"layer_as_7_calls_GB/s": round(value7, 1), "per_matrix_q4k": {}}
     for name, r, c in LLAMA3_LAYER:

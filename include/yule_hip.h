@@ -307,6 +307,15 @@ typedef struct {
 int yule_hip_time_qmv_ops(yule_hip_backend *be, const yule_qmv_op *ops, uint32_t n_ops, uint32_t iters,
                           int use_graph, float *ms_total);
 
+/* Roofline probe: one launch that streams `bytes` (a multiple of 16) of
+ * `src` with n_partials 256-thread workgroups (grid-stride 16-byte loads)
+ * and writes, per workgroup, the XOR of every 32-bit word it read to
+ * partials[i] (the XOR of all partials is the XOR of the whole range).  It
+ * measures what a single launch that only reads the same bytes achieves,
+ * beside the quantized kernels' own rates.  No reference counterpart. */
+int yule_hip_read_probe(yule_hip_backend *be, yule_buffer src, uint64_t bytes, yule_buffer partials,
+                        uint32_t n_partials);
+
 /* Event timer on the backend stream: timer_start records a start event;
  * timer_stop records a stop event after everything enqueued since, waits
  * for it and writes the elapsed milliseconds. */

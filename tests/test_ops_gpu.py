@@ -217,3 +217,24 @@ def test_argmax_kats(hip):
     assert int(hip.download(out, 1, np.uint32)[0]) == oracle.argmax(v)
     hip.free(h)
     hip.free(out)
+
+
+@pytest.mark.parametrize("n_bytes,n_wg", [(16, 1), (16, 64), (4096, 3), (1_000_016, 2048), (33_030_144, 2048)])
+def test_read_probe_reads_every_word_once(hip, n_bytes, n_wg):
+    """The roofline probe: the XOR of its per-workgroup partials equals the
+    XOR of every 32-bit word of the range (each word read exactly once)."""
+    say(f"[ops] read_probe {n_bytes} B over {n_wg} workgroups")
+    rng = np.random.default_rng(n_bytes)
+    data = rng.integers(0, 2**32, n_bytes // 4, dtype=np.uint32)
+    src, part = hip.upload(data), hip.allocate(4 * n_wg)
+    hip.read_probe(src, n_bytes, part, n_wg)
+    got = np.bitwise_xor.reduce(hip.download(part, n_wg, np.uint32))
+    assert int(got) == int(np.bitwise_xor.reduce(data))
+    with pytest.raises(YuleGpuError):
+        hip.read_probe(src, n_bytes + 16, part, n_wg)          # past the buffer
+    with pytest.raises(YuleGpuError):
+        hip.read_probe(src, n_bytes - 4 if n_bytes > 16 else 8, part, n_wg)   # not a multiple of 16
+    with pytest.raises(YuleGpuError):
+        hip.read_probe(src, n_bytes, part, n_wg + 1)           # partials too small
+    hip.free(src)
+    hip.free(part)

@@ -72,6 +72,7 @@ _SIGS: dict[str, tuple] = {
     "yule_hip_gguf_get_str": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(C.c_char_p)]),
     "yule_hip_gguf_get_array_len": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(C.c_uint64)]),
     "yule_hip_runner_create_from_gguf": (C.c_int, [C.c_void_p, C.c_char_p, C.c_uint32, C.POINTER(C.c_void_p)]),
+    "yule_hip_read_probe": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint32]),
     "yule_hip_timer_start": (C.c_int, [C.c_void_p]),
     "yule_hip_timer_stop": (C.c_int, [C.c_void_p, C.POINTER(C.c_float)]),
     "yule_hip_time_qmv_ops": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_int,
@@ -269,6 +270,11 @@ class HipBackend:
     def gqa_decode_attn(self, q, k_cache, v_cache, out, n_heads, n_kv_heads, head_dim, seq_len) -> None:
         self._check(self._lib.yule_hip_gqa_decode_attn(self._be, _h(q), _h(k_cache), _h(v_cache), _h(out), n_heads,
                                                        n_kv_heads, head_dim, seq_len))
+
+    def read_probe(self, src, n_bytes: int, partials, n_partials: int) -> None:
+        """One streaming-read launch over n_bytes of src (roofline probe);
+        partials[i] = XOR of the words workgroup i read."""
+        self._check(self._lib.yule_hip_read_probe(self._be, _h(src), n_bytes, _h(partials), n_partials))
 
     def argmax(self, inp, n: int, out) -> None:
         self._check(self._lib.yule_hip_argmax(self._be, _h(inp), n, _h(out)))

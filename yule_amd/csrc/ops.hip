@@ -210,6 +210,27 @@ int launch_argmax(hipStream_t s, const float *in, uint32_t n, uint32_t *out) {
 
 using namespace yule;
 
+// ------------------------------------------------------------ read probe
+// Streams `n16` 16-byte words from `src` (grid-stride, one load in flight
+// per lane, the fastest single-launch read pattern measured on gfx950) and
+// writes one XOR of every word each workgroup read to part[blockIdx.x], so
+// that the reads are observable and the host can check them.
+__global__ __launch_bounds__(256) void read_probe_kernel(const uint4 *__restrict__ src, uint64_t n16,
+                                                         uint32_t *__restrict__ part) {
+    __shared__ uint32_t red[4];
+    const uint64_t T = (uint64_t)gridDim.x * 256;
+    uint32_t acc = 0;
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += T) {
+        const uint4 v = src[i];
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) acc ^= __shfl_xor(acc, off, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) part[blockIdx.x] = red[0] ^ red[1] ^ red[2] ^ red[3];
+}
+
 #define BE_OR_FAIL(be) \
     if (!(be)) return set_error(YULE_ERR_INVALID, "null backend")
 
@@ -364,6 +385,21 @@ int yule_hip_gqa_decode_attn(yule_hip_backend *be, yule_buffer q, yule_buffer k_
                                  n_kv_heads, head_dim, seq_len);
     }
     return launch_gqa_attn(be->stream, pq, pk, pv, po, n_heads, n_kv_heads, head_dim, seq_len);
+}
+
+int yule_hip_read_probe(yule_hip_backend *be, yule_buffer src, uint64_t bytes, yule_buffer partials,
+                        uint32_t n_partials) {
+    BE_OR_FAIL(be);
+    if (bytes % 16 || n_partials == 0 || n_partials > 65536)
+        return set_error(YULE_ERR_INVALID, "read_probe: bytes must be a multiple of 16, n_partials in 1..65536");
+    void *ps, *pp;
+    int rc;
+    if ((rc = get_buffer(be, src, bytes, &ps, "read_probe (src)")) ||
+        (rc = get_buffer(be, partials, (size_t)n_partials * 4, &pp, "read_probe (partials)")))
+        return rc;
+    hipLaunchKernelGGL(read_probe_kernel, dim3(n_partials), dim3(256), 0, be->stream, (const uint4 *)ps, bytes / 16,
+                       (uint32_t *)pp);
+    return check_launch("read_probe");
 }
 
 int yule_hip_argmax(yule_hip_backend *be, yule_buffer in, uint32_t n, yule_buffer out) {
