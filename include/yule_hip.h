@@ -122,13 +122,14 @@ int yule_hip_attn_value(yule_hip_backend *be, yule_buffer weights, yule_buffer v
 
 /* ComputeBackend::quantized_matmul (lib.rs:116-131) — the hot path.
  * y[r] = sum_b vec_dot(W[r, b], x[b*bs .. (b+1)*bs]) for r < n_rows.
- * weights: raw GGUF blocks, row-major, n_cols/bs blocks per row;
- * input: f32[n_cols]; output: f32[n_rows], fully overwritten.
+ * weights: raw GGUF blocks, row-major, ceil(n_cols/bs) blocks per row;
+ * input: f32[n_cols]; output: f32[n_rows], fully overwritten.  When n_cols
+ * is not a block multiple the last block's columns >= n_cols are skipped,
+ * as in the reference's GPU kernels (cuda/mod.rs:311-313, qmv_*.cu).
  * dtype: Q4_0, Q8_0, Q4_K or Q6_K (the reference's GPU set), plus Q5_K
  * (the CPU path's vec_dot_q5_k, dequant.rs:1088-1140) and Q8_K (the
  * reference has its dequant only, dequant.rs:376-384; here it runs through
- * the same matvec); n_cols must be a multiple of the block size (GGUF rows
- * always are).  Other dtypes -> YULE_ERR_UNSUPPORTED, as the Vulkan
+ * the same matvec).  Other dtypes -> YULE_ERR_UNSUPPORTED, as the Vulkan
  * backend's Err (yule-gpu/src/vulkan/mod.rs:333-343). */
 int yule_hip_quantized_matmul(yule_hip_backend *be, yule_buffer weights, yule_buffer input,
                               yule_buffer output, uint32_t n_rows, uint32_t n_cols, uint32_t dtype);

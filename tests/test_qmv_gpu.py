@@ -10,6 +10,7 @@ import pytest
 import oracle
 from refgen import kats, tolerance_bar, xorshift_blocks
 from yule_amd import DType, synth
+from yule_amd.formats import block_size
 from yule_amd.backend import YuleGpuError
 
 pytestmark = pytest.mark.gpu
@@ -174,7 +175,7 @@ def test_qmv_edge_cases_and_errors(hip):
         hip.quantized_matmul(hw, hx, hy, 4, 256, 3)   # Q4_1: not on the GPU path
     assert e.value.code == 2
     with pytest.raises(YuleGpuError):
-        hip.quantized_matmul(hw, hx, hy, 4, 100, dt)  # not a block multiple
+        hip.quantized_matmul(hw, hx, hy, 4, 257, dt)  # needs ceil(257/256) = 2 blocks per row
     with pytest.raises(YuleGpuError):
         hip.quantized_matmul(hw, hx, hy, 5, 256, dt)  # weights too small
     with pytest.raises(YuleGpuError):
@@ -182,6 +183,34 @@ def test_qmv_edge_cases_and_errors(hip):
     with pytest.raises(YuleGpuError):
         hip.quantized_matmul(hw, hx, 999999, 4, 256, dt)  # unknown handle
     for h in (hw, hx, hy):
+        hip.free(h)
+
+
+@pytest.mark.parametrize("dt", FMTS, ids=lambda d: d.name)
+@pytest.mark.parametrize("n_rows,n_cols", [(5, 1), (33, 100), (300, 1000), (7, 4097), (64, 14300)])
+def test_qmv_ragged_columns(hip, dt, n_rows, n_cols):
+    """n_cols not a block multiple: ceil(n_cols/bs) blocks per row with the
+    columns >= n_cols skipped (the reference's GPU kernels, cuda/mod.rs:
+    311-313 and kernels/cuda/qmv_*.cu); the input holds exactly n_cols
+    floats.  Reference: f64 over the bit-exact dequantized rows, first
+    n_cols columns."""
+    bs = block_size(dt)
+    n_pad = -(-n_cols // bs) * bs
+    say(f"[qmv] ragged {dt.name} {n_rows}x{n_cols} ({n_pad // bs} blocks per row)")
+    w = synth.gen_quant(dt, 400 + n_cols, n_rows, n_pad)
+    x = synth.gauss(401, n_cols)
+    W = oracle.dequant(int(dt), w).reshape(n_rows, n_pad)[:, :n_cols].astype(np.float64)
+    want = W @ x.astype(np.float64)
+    hw, hx, hy = hip.upload(w), hip.upload(x), hip.allocate(4 * n_rows)
+    hip.quantized_matmul(hw, hx, hy, n_rows, n_cols, dt)
+    got = hip.download(hy, n_rows)
+    assert np.max(np.abs(got - want)) <= tolerance_bar(want)
+    outs = [hip.allocate(4 * n_rows) for _ in range(2)]
+    hw2 = hip.upload(w)
+    hip.quantized_matmul_multi([hw, hw2], hx, outs, [n_rows, n_rows], n_cols, dt)
+    for o in outs:
+        assert np.array_equal(hip.download(o, n_rows), got)
+    for h in [hw, hw2, hx, hy] + outs:
         hip.free(h)
 
 

@@ -104,6 +104,8 @@ int launch_embed_rows(hipStream_t stream, uint32_t dtype, const uint8_t *table, 
                       uint32_t n_rows, float *dst, uint32_t dim);
 // out[i] = value for i < n
 int launch_fill(hipStream_t stream, float *out, float value, uint64_t n);
+// out[i] = i < n ? x[i] : 0 for i < n_out (a row staged zero-padded)
+int launch_pad(hipStream_t stream, const float *x, uint32_t n, float *out, uint32_t n_out);
 // op 0 silu, 1 mul, 2 add, 3 silu(a)*b
 int launch_eltwise(hipStream_t stream, int op, const float *a, const float *b, float *out, uint32_t n);
 int launch_rms_norm(hipStream_t stream, const float *x, const float *w, float *out, uint32_t n, float eps);

@@ -56,6 +56,16 @@ int launch_fill(hipStream_t s, float *out, float v, uint64_t n) {
     return check_launch("fill");
 }
 
+__global__ void pad_kernel(const float *__restrict__ x, uint32_t n, float *__restrict__ out, uint32_t n_out) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n_out) out[i] = i < n ? x[i] : 0.f;
+}
+
+int launch_pad(hipStream_t s, const float *x, uint32_t n, float *out, uint32_t n_out) {
+    hipLaunchKernelGGL(pad_kernel, dim3((n_out + 255) / 256), dim3(256), 0, s, x, n, out, n_out);
+    return check_launch("pad");
+}
+
 // op 0: silu (cpu.rs:339-357), 1: element_mul, 2: add, 3: silu_mul
 // (model_runner.rs:967-972: g * (1/(1+exp(-g))) * u)
 __global__ void eltwise_kernel(int op, const float *__restrict__ a, const float *__restrict__ b,

@@ -265,13 +265,12 @@ static int check_qmv_args(yule_hip_backend *be, yule_buffer weights, yule_buffer
     if (!quant_geometry(dtype, &bs, &bb))
         return set_error(YULE_ERR_UNSUPPORTED,
                          std::string(what) + ": dtype " + std::to_string(dtype) + " not supported on this backend");
-    if (n_cols % bs)
-        return set_error(YULE_ERR_INVALID, std::string(what) + ": n_cols " + std::to_string(n_cols) +
-                                               " is not a multiple of the block size " + std::to_string(bs));
     if (input == output) return set_error(YULE_ERR_INVALID, std::string(what) + ": input and output alias");
     void *pw, *px, *py;
     int rc;
-    const size_t wbytes = (size_t)n_rows * (n_cols / bs) * bb;
+    // ceil(n_cols / bs) blocks per row, as the reference's GPU backends
+    // launch them (cuda/mod.rs:311-313; vulkan/mod.rs:324-351)
+    const size_t wbytes = (size_t)n_rows * ((n_cols + bs - 1) / bs) * bb;
     if ((rc = get_buffer(be, weights, wbytes, &pw, what))) return rc;
     if ((rc = get_buffer(be, input, (size_t)n_cols * 4, &px, what))) return rc;
     if ((rc = get_buffer(be, output, (size_t)n_rows * 4, &py, what))) return rc;
@@ -301,6 +300,28 @@ static int prepare_multi(yule_hip_backend *be, uint32_t n_mats, const yule_buffe
     return YULE_OK;
 }
 
+// A row length that is not a multiple of the block size: the reference's
+// GPU kernels run ceil(n_cols / bs) blocks per row and skip the columns
+// >= n_cols (kernels/cuda/qmv_*.cu, shaders/qmv_*.comp column checks).
+// Here x is staged in the backend workspace zero-padded to the block
+// multiple, so the last block's extra columns contribute exactly 0 and the
+// kernels run unchanged.  (The CPU path floors instead, cpu.rs:544-590; the
+// GPU backends' semantics are the ones a GPU drop-in keeps.)
+static int pad_input(yule_hip_backend *be, uint32_t dtype, const float *x, uint32_t n_cols, const float **xp,
+                     uint32_t *n_cols_p) {
+    uint32_t bs, bb;
+    quant_geometry(dtype, &bs, &bb);
+    const uint32_t np = (n_cols + bs - 1) / bs * bs;
+    *xp = x;
+    *n_cols_p = np;
+    if (np == n_cols) return YULE_OK;
+    void *ws;
+    int rc = get_scratch(be, (size_t)np * sizeof(float), &ws);
+    if (rc) return rc;
+    *xp = static_cast<const float *>(ws);
+    return launch_pad(be->stream, x, n_cols, static_cast<float *>(ws), np);
+}
+
 int yule_hip_quantized_matmul(yule_hip_backend *be, yule_buffer weights, yule_buffer input, yule_buffer output,
                               uint32_t n_rows, uint32_t n_cols, uint32_t dtype) {
     YULE_CHECK_BE(be);
@@ -309,7 +330,10 @@ int yule_hip_quantized_matmul(yule_hip_backend *be, yule_buffer weights, yule_bu
     if (rc) return rc;
     if (n_rows == 0) return YULE_OK;
     if (empty) return launch_fill(be->stream, y, 0.0f, n_rows);  // zero blocks per row -> y = 0
-    return launch_qmv(be->stream, dtype, w, x, y, n_rows, n_cols);
+    const float *xp;
+    uint32_t np;
+    if ((rc = pad_input(be, dtype, x, n_cols, &xp, &np))) return rc;
+    return launch_qmv(be->stream, dtype, w, xp, y, n_rows, np);
 }
 
 int yule_hip_quantized_matmul_multi(yule_hip_backend *be, uint32_t n_mats, const yule_buffer *weights,
@@ -330,7 +354,10 @@ int yule_hip_quantized_matmul_multi(yule_hip_backend *be, uint32_t n_mats, const
             if ((rc = launch_fill(be->stream, segs[i].y, 0.0f, segs[i].n_rows))) return rc;
         return YULE_OK;
     }
-    return launch_qmv_multi(be->stream, dtype, segs, n, x, n_cols);
+    const float *xp;
+    uint32_t np;
+    if ((rc = pad_input(be, dtype, x, n_cols, &xp, &np))) return rc;
+    return launch_qmv_multi(be->stream, dtype, segs, n, xp, np);
 }
 
 int yule_hip_dequantize(yule_hip_backend *be, yule_buffer src, size_t src_offset, yule_buffer dst,
@@ -358,6 +385,10 @@ int yule_hip_time_qmv_ops(yule_hip_backend *be, const yule_qmv_op *ops, uint32_t
                                ops[i].n_cols, ops[i].dtype, "time_qmv_ops", L[i].segs, &L[i].x);
         if (rc) return rc;
         if (ops[i].n_cols == 0) return set_error(YULE_ERR_INVALID, "time_qmv_ops: empty matrix");
+        uint32_t bs, bb;
+        quant_geometry(ops[i].dtype, &bs, &bb);
+        if (ops[i].n_cols % bs)
+            return set_error(YULE_ERR_INVALID, "time_qmv_ops: n_cols must be a multiple of the block size");
         for (uint32_t j = 0; j < ops[i].n_mats; j++)
             if (!ops[i].n_rows[j]) return set_error(YULE_ERR_INVALID, "time_qmv_ops: empty matrix");
         L[i].dtype = ops[i].dtype; L[i].n_cols = ops[i].n_cols; L[i].n = ops[i].n_mats;
