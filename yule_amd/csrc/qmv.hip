@@ -54,20 +54,13 @@ __device__ __forceinline__ uint32_t shr64(uint32_t hi, uint32_t lo, uint32_t s) 
     return (uint32_t)((((uint64_t)hi << 32) | lo) >> s);
 }
 
-// Weight loads; YULE_QMV_NT=1 adds the nontemporal hint (measured slower
-// for this kernel on gfx950, so off by default).
-#ifndef YULE_QMV_NT
-#define YULE_QMV_NT 0
-#endif
+// Weight loads (plain: the nontemporal hint measured slower here on gfx950).
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 ldw16(const uint8_t *p) {
-    const u32x4 v = YULE_QMV_NT ? __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p))
-                                : *reinterpret_cast<const u32x4 *>(p);
+    const u32x4 v = *reinterpret_cast<const u32x4 *>(p);
     return make_uint4(v.x, v.y, v.z, v.w);
 }
-__device__ __forceinline__ uint32_t ldw4(const uint32_t *p) {
-    return YULE_QMV_NT ? __builtin_nontemporal_load(p) : *p;
-}
+__device__ __forceinline__ uint32_t ldw4(const uint32_t *p) { return *p; }
 
 // Activation accessors: float4 at element i (i % 4 == 0) of x, either from
 // global memory or from the LDS copy, which pads 4 floats after every 32 so
@@ -675,14 +668,7 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const Segs sg, const flo
                 if (t == 0 && row < n_rows) sg.y[0][row] = g * (1.0f / (1.0f + expf(-g))) * u;
                 it++;
             } else {
-#ifdef YULE_QMV_FAKE_DOT
-                const uint32_t *rw = reinterpret_cast<const uint32_t *>(&buf[j]);
-                uint32_t hsh = 0;
-                for (uint32_t q = 0; q < sizeof(buf[j]) / 4; q++) hsh ^= rw[q];
-                finish(__builtin_bit_cast(float, hsh & 0x3F7FFFFFu) + xs[0], r, it, r + stride >= n_rows);
-#else
                 finish(F::dot(buf[j], sub, xs, aux), r, it, r + stride >= n_rows);
-#endif
                 it++;
             }
         }
@@ -738,7 +724,7 @@ static void launch_stream_nt(hipStream_t s, const Segs &sg, const float *x, uint
 
 template <class F, int W>
 static void launch_stream(hipStream_t s, const Segs &sg, const float *x, uint32_t bpr, const QmvXf &xf) {
-    static const int nt_narrow = env_int("YULE_QMV_NT", 256), nt_wide = env_int("YULE_QMV_NT_WIDE", 1024);
+    static const int nt_narrow = env_int("YULE_QMV_THREADS", 256), nt_wide = env_int("YULE_QMV_THREADS_WIDE", 1024);
     const int nt = W >= 512 ? 1024 : W >= 128 ? nt_wide : nt_narrow;
     if (nt >= 1024) return launch_stream_nt<F, W, 1024>(s, sg, x, bpr, xf);
     if constexpr (W >= 512) return;   // unreachable: 512-lane teams only run in 1024-thread workgroups
