@@ -153,11 +153,8 @@ def read_probe(hip, layer, name, launches, n_wg=2048):
             "launch": "yule_hip_read_probe, 2048 x 256 threads, back-to-back stream launches"}
 
 
-def cpu_baseline(layer, budget_s=12.0, max_passes=2000):
-    """Yule's CPU decode matvec path (oracle restatement of model_runner.rs:
-    152-244 + simd/avx2.rs) over the same Q4_K layer bytes, host-resident."""
+def _time_qmv_layer(layer, threads, budget_s, max_passes):
     import oracle
-    threads = min(16, os.cpu_count() or 1)
     mats = [(layer.host[n], layer.host[f"x{c}"], r, c) for n, r, c in layer.shapes]
     for w, x, r, c in mats:                       # warm-up pass
         oracle.qmv(int(layer.dt), w, x, r, c, threads)
@@ -167,12 +164,40 @@ def cpu_baseline(layer, budget_s=12.0, max_passes=2000):
             oracle.qmv(int(layer.dt), w, x, r, c, threads)
         passes += 1
     dt = time.perf_counter() - t0
-    gbs = passes * layer.step_bytes / dt / 1e9
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+    return passes * layer.step_bytes / dt / 1e9, passes, dt
+
+
+def cpu_baseline(layer, budget_s=12.0, max_passes=2000):
+    """Yule's CPU decode matvec path over the same Q4_K layer bytes,
+    host-resident: the oracle's restatement of model_runner.rs:152-244 (the
+    per-call std::thread row split).  When oracle/_ref holds the reference's
+    own Q4_K assembly kernel (yule-core/src/kernels/q4k_gemv_avx2.S, which
+    the reference's AVX2 build uses for every Q4_K block, simd/avx2.rs:
+    84-96), the block dots run through it and the baseline is
+    kind "reference"; the pure restatement (the Rust-fallback AVX2 body) is
+    reported beside it.  Otherwise the restatement alone, kind "port"."""
+    import oracle
+    threads = min(16, os.cpu_count() or 1)
+    asm = oracle.q4k_asm() if layer.dt == DType.Q4_K else None
+    if asm is None:
+        gbs, passes, dt = _time_qmv_layer(layer, threads, budget_s, max_passes)
+        return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+                "sample": f"{passes} passes of the Q4_K Llama-3-8B layer (7 projections, "
+                          f"{layer.step_bytes / 1e6:.1f} MB each pass) through the oracle's restatement of Yule's "
+                          f"AVX2 qmv with a per-call std::thread row split, {threads} threads, {dt:.1f} s",
+                "host_cpu": _cpu_model()}
+    port, _, _ = _time_qmv_layer(layer, threads, budget_s / 2, max_passes)
+    oracle.set_q4k_dot(asm)
+    try:
+        gbs, passes, dt = _time_qmv_layer(layer, threads, budget_s / 2, max_passes)
+    finally:
+        oracle.set_q4k_dot(None)
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "reference",
             "sample": f"{passes} passes of the Q4_K Llama-3-8B layer (7 projections, "
-                      f"{layer.step_bytes / 1e6:.1f} MB each pass) through the oracle's restatement of Yule's "
-                      f"AVX2 qmv with a per-call std::thread row split, {threads} threads, {dt:.1f} s",
-            "host_cpu": _cpu_model()}
+                      f"{layer.step_bytes / 1e6:.1f} MB each pass): the reference's q4k_gemv_avx2.S (assembled from "
+                      f"its sources into oracle/_ref) for every block, inside the restatement of model_runner.rs "
+                      f"qmv's per-call std::thread row split, {threads} threads, {dt:.1f} s",
+            "port_value": round(port, 3), "host_cpu": _cpu_model()}
 
 
 def decode_e2e(hip, cpu: bool):

@@ -67,6 +67,7 @@ def lib() -> C.CDLL:
         L.yo_qmv_f64.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32]
         L.yo_qmv.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_int]
         L.yo_have_avx2.restype = C.c_int
+        L.yo_set_q4k_dot.argtypes = [C.c_void_p]
         L.yo_argmax.argtypes = [C.c_void_p, C.c_uint32]
         L.yo_argmax.restype = C.c_uint32
         L.yo_rope_table.argtypes = [C.c_uint32, C.c_uint32, C.c_float, C.c_void_p, C.c_void_p]
@@ -164,6 +165,13 @@ def q4k_asm():
     L.yule_q4k_gemv_avx2.argtypes = [C.c_void_p, C.c_void_p]
     L.yule_q4k_gemv_avx2.restype = C.c_float
     return L.yule_q4k_gemv_avx2
+
+
+def set_q4k_dot(fn) -> None:
+    """Run the AVX2 path's Q4_K block dot through `fn` (q4k_asm(): the
+    reference's assembly kernel, as its own AVX2 build does), or through the
+    Rust-fallback restatement again with None."""
+    lib().yo_set_q4k_dot(C.cast(fn, C.c_void_p) if fn is not None else None)
 
 
 class Runner:

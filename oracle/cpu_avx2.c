@@ -134,6 +134,14 @@ __attribute__((target("avx2,fma"))) static float dot_q5_k(const uint8_t *blk, co
 /* avx2.rs:305-337 — the AVX2 Q6_K body is the scalar loop */
 static float dot_q6_k(const uint8_t *blk, const float *act) { return yo_vec_dot_q6_k(blk, act); }
 
+/* The reference's AVX2 build runs Q4_K through its hand-written assembly
+ * kernel when that is compiled in (simd/avx2.rs:84-96,
+ * kernels/q4k_gemv_avx2.S); yo_set_q4k_dot installs that function (loaded
+ * from oracle/_ref by the caller) in place of the Rust-fallback restatement
+ * above, NULL restores the restatement. */
+static yo_q4k_dot_fn g_q4k_dot = NULL;
+void yo_set_q4k_dot(yo_q4k_dot_fn fn) { g_q4k_dot = fn; }
+
 /* simd::vec_dot, simd/mod.rs:38-47 */
 int yo_vec_dot_block(int dtype, const uint8_t *blk, const float *act, float *res) {
     if (g_level == 0) g_level = yo_have_avx2() ? 2 : 1;
@@ -141,7 +149,7 @@ int yo_vec_dot_block(int dtype, const uint8_t *blk, const float *act, float *res
         switch (dtype) {
         case YO_Q8_0: *res = dot_q8_0(blk, act); return 0;
         case YO_Q4_0: *res = dot_q4_0(blk, act); return 0;
-        case YO_Q4_K: *res = dot_q4_k(blk, act); return 0;
+        case YO_Q4_K: *res = g_q4k_dot ? g_q4k_dot(blk, act) : dot_q4_k(blk, act); return 0;
         case YO_Q6_K: *res = dot_q6_k(blk, act); return 0;
         case YO_Q5_K: *res = dot_q5_k(blk, act); return 0;
         default: break;

@@ -73,6 +73,11 @@ int yo_have_avx2(void);
 int yo_vec_dot_block(int dtype, const uint8_t *blk, const float *act, float *res);
 /* qmv of model_runner.rs:152-244: rows split over n_threads std::threads
  * spawned per call when n_rows >= 128 (n_threads <= 0: all online CPUs). */
+/* Q4_K block dot of the AVX2 path: the reference's assembly kernel when
+ * installed (simd/avx2.rs:84-96), else the Rust-fallback restatement. */
+typedef float (*yo_q4k_dot_fn)(const uint8_t *blk, const float *act);
+void yo_set_q4k_dot(yo_q4k_dot_fn fn);
+
 int yo_qmv(int dtype, const uint8_t *w, const float *x, float *y,
            uint32_t n_rows, uint32_t n_cols, int n_threads);
 

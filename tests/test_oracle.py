@@ -14,7 +14,8 @@ import numpy as np
 import pytest
 
 import oracle
-from refgen import (GOLDEN, kats, pack_q4k, pack_q4k_scales, pack_q6k, q6k_sub_of, xorshift_blocks)
+from refgen import (GOLDEN, kats, pack_q4k, pack_q4k_scales, pack_q6k, q6k_sub_of, tolerance_bar, xorshift_blocks)
+from yule_amd import DType, synth
 
 K = kats()
 RNG = np.random.default_rng(1234)
@@ -311,3 +312,26 @@ def test_rope_table_kats():
     assert abs(c[5 * 2] - math.cos(5.0)) < 1e-6 and abs(s[5 * 2] - math.sin(5.0)) < 1e-6
     # pair 1: freq = 1/10000^(2/4) = 0.01
     assert abs(c[5 * 2 + 1] - math.cos(0.05)) < 1e-6
+
+
+def test_qmv_through_reference_asm_matches_restatement():
+    """oracle.set_q4k_dot(q4k_asm()): the AVX2 qmv with the reference's own
+    assembly block dot (the reference's AVX2 build) agrees with the
+    Rust-fallback restatement and with the f64 dot, threaded and not."""
+    asm = oracle.q4k_asm()
+    if asm is None:
+        pytest.skip("oracle/_ref not built (needs the reference tree)")
+    w = synth.gen_quant(DType.Q4_K, 61, 300, 4096)
+    x = synth.gauss(62, 4096)
+    ref = oracle.qmv_f64(int(DType.Q4_K), w, x, 300, 4096)
+    port = oracle.qmv(int(DType.Q4_K), w, x, 300, 4096, 4)
+    oracle.set_q4k_dot(asm)
+    try:
+        a1 = oracle.qmv(int(DType.Q4_K), w, x, 300, 4096, 1)
+        a4 = oracle.qmv(int(DType.Q4_K), w, x, 300, 4096, 4)
+    finally:
+        oracle.set_q4k_dot(None)
+    assert np.array_equal(a1, a4)
+    assert np.max(np.abs(a1 - ref)) <= tolerance_bar(ref)
+    assert np.max(np.abs(a1 - port)) <= tolerance_bar(ref)
+    assert np.array_equal(oracle.qmv(int(DType.Q4_K), w, x, 300, 4096, 4), port)   # restored
