@@ -223,16 +223,25 @@ def decode_e2e(hip, cpu: bool):
     if cpu:
         import oracle
         threads = min(16, os.cpu_count() or 1)
-        r = oracle.Runner(model, n_threads=threads)
-        r.forward(int(prompt[0]))
-        n, t0 = 0, time.perf_counter()
-        while n < 4 or (n < 48 and time.perf_counter() - t0 < 12.0):
-            r.forward(int(prompt[(n + 1) % 128]))
-            n += 1
-        cms = 1e3 * (time.perf_counter() - t0) / n
-        res["cpu_decode"] = {"tok_s": round(1000.0 / cms, 2), "threads": threads, "kind": "port",
+        asm = oracle.q4k_asm()          # the reference's Q4_K assembly kernel, as its AVX2 build runs it
+        if asm is not None:
+            oracle.set_q4k_dot(asm)
+        try:
+            r = oracle.Runner(model, n_threads=threads)
+            r.forward(int(prompt[0]))
+            n, t0 = 0, time.perf_counter()
+            while n < 4 or (n < 48 and time.perf_counter() - t0 < 12.0):
+                r.forward(int(prompt[(n + 1) % 128]))
+                n += 1
+            cms = 1e3 * (time.perf_counter() - t0) / n
+        finally:
+            oracle.set_q4k_dot(None)
+        what = ("the reference's q4k_gemv_avx2.S for every Q4_K block" if asm is not None
+                else "the Rust-fallback restatement of the AVX2 Q4_K body")
+        res["cpu_decode"] = {"tok_s": round(1000.0 / cms, 2), "threads": threads,
+                             "kind": "reference" if asm is not None else "port",
                              "sample": f"{n} forward steps at positions 1..{n} of the same model through the "
-                                       f"oracle's restatement of Yule's CPU TransformerRunner"}
+                                       f"oracle's restatement of Yule's CPU TransformerRunner with {what}"}
         res["decode_speedup_vs_cpu"] = round(cms / ms, 1)
     return res
 
