@@ -41,9 +41,9 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 // stages of 64 (a quarter super-block): X and weight bytes of stage s+2 are
 // loaded into registers while stage s runs on the MFMAs out of one LDS buffer
 // and stage s+1 is dequantized into the other, one barrier per stage.  LDS
-// rows are padded to 72 halves (36 dwords: 16 consecutive rows of a
-// ds_read_b128 land on distinct banks).
-constexpr int GSK = 64, GLD = GSK + 8;
+// rows are padded (72 or 80 halves) so that the 16 rows one ds_read_b128
+// reads spread over the banks.
+constexpr int GSK = 64;
 
 __device__ __forceinline__ _Float16 bf16_to_f16(uint16_t b) {
     return (_Float16)__builtin_bit_cast(float, (uint32_t)b << 16);
@@ -134,6 +134,10 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
     constexpr uint32_t NTH = 2 * BN;            // threads: two per weight row of the tile
     constexpr uint32_t WNN = BN / 64;           // waves along n (two along m)
     constexpr int XCH = BM * GSK / 8 / NTH;     // 16-byte X chunks per thread per stage
+    // LDS row pitch in halves: 72 keeps two 128-wide workgroups per CU; the
+    // 256-wide tile (one per CU) measured 6-7% faster at 80 than at 72, 88,
+    // 96 or 104
+    constexpr int GLD = BN == 256 ? 80 : GSK + 8;
     __shared__ __align__(16) _Float16 sx[2][BM * GLD];
     __shared__ __align__(16) _Float16 sw[2][BN * GLD];
     __shared__ float sd[2][BN];
