@@ -202,7 +202,16 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
 #pragma unroll
         for (int i = 0; i < XCH; i++) {
             const uint32_t idx = tid + NTH * i, row = idx >> 3, c = idx & 7u;
-            *reinterpret_cast<uint4 *>(sx[b] + row * GLD + 8u * c) = m0 + row < M ? R.x[i] : make_uint4(0, 0, 0, 0);
+            if constexpr (Q4) {
+                // rows past M are stored as zeros with a mask: the select
+                // below compiles to branches and register copies around every
+                // stage (10% at M = 512); Q6_K keeps it, its masks spill
+                const uint32_t mk = 0u - (uint32_t)(m0 + row < M);
+                *reinterpret_cast<uint4 *>(sx[b] + row * GLD + 8u * c) =
+                    make_uint4(R.x[i].x & mk, R.x[i].y & mk, R.x[i].z & mk, R.x[i].w & mk);
+            } else {
+                *reinterpret_cast<uint4 *>(sx[b] + row * GLD + 8u * c) = m0 + row < M ? R.x[i] : make_uint4(0, 0, 0, 0);
+            }
         }
         _Float16 *dst = sw[b] + wr * GLD;
         uint4 o[4];
@@ -234,7 +243,9 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
             o[1] = make_uint4(lo[4], lo[5], lo[6], lo[7]);
             o[2] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
             o[3] = make_uint4(hi[4], hi[5], hi[6], hi[7]);
-            if (!wrow_ok) o[0] = o[1] = o[2] = o[3] = make_uint4(0, 0, 0, 0);
+            const uint32_t wk = 0u - (uint32_t)wrow_ok;
+#pragma unroll
+            for (int c = 0; c < 4; c++) o[c] = make_uint4(o[c].x & wk, o[c].y & wk, o[c].z & wk, o[c].w & wk);
             // this thread's 16 bytes: k = 16 part + 0..15 (low), 32 + 16 part + 0..15 (high)
             *reinterpret_cast<uint4 *>(dst + 16u * part) = o[0];
             *reinterpret_cast<uint4 *>(dst + 16u * part + 8u) = o[1];
