@@ -221,3 +221,57 @@ def test_find_missing_tensor(tmp_path):
             g.tensor_data("b")
         assert e.value.code == ERR_INVALID
         assert np.array_equal(g.tensor_data("a"), np.zeros(16, np.uint8))
+
+
+def test_fuzz_corrupted_files_never_crash(tmp_path):
+    """Random byte flips, truncations and length-field overwrites of a valid
+    model file: the parser either accepts the file (then every tensor lies
+    inside it) or raises a parse error; it never reads out of bounds."""
+    from yule_amd.model import LlamaConfig
+    cfg = LlamaConfig(n_layers=1, dim=256, n_heads=4, n_kv_heads=2, ff_dim=256, vocab=64, max_seq=16)
+    p = tmp_path / "base.gguf"
+    SyntheticModel.generate(cfg, seed=1, scheme="Q4_K_M").to_gguf(p)
+    base = bytearray(p.read_bytes())
+    with GgufFile(p) as g:
+        header_end = g.data_offset
+    rng = np.random.default_rng(7)
+    q = tmp_path / "fuzz.gguf"
+    outcomes = {"ok": 0, "err": 0}
+    for it in range(300):
+        d = bytearray(base)
+        kind = it % 3
+        if kind == 0:      # flip bytes in the header region
+            for _ in range(int(rng.integers(1, 8))):
+                d[int(rng.integers(0, header_end))] ^= int(rng.integers(1, 256))
+        elif kind == 1:    # truncate anywhere
+            d = d[: int(rng.integers(0, len(d)))]
+        else:              # overwrite an aligned u64 in the header with an extreme value
+            pos = int(rng.integers(0, max(1, header_end - 8)))
+            extremes = [0, 1, 2**31, 2**32 - 1, 2**63, 2**64 - 1]
+            d[pos:pos + 8] = struct.pack("<Q", extremes[int(rng.integers(0, len(extremes)))])
+        q.write_bytes(bytes(d))
+        try:
+            with GgufFile(q) as g:
+                for t in g.tensors:
+                    assert g.data_offset + t.offset + t.size_bytes <= len(d)
+                outcomes["ok"] += 1
+        except YuleGpuError as e:
+            assert e.code in (ERR_PARSE, ERR_IO)
+            outcomes["err"] += 1
+    assert outcomes["err"] > 100
+
+
+@pytest.mark.parametrize("raw,ok", [(b"llama", True), ("héllo 世\U0001F600".encode(), True),
+                                     (b"\xff", False), (b"\xc0\xaf", False), (b"\xed\xa0\x80", False),
+                                     (b"\xf4\x90\x80\x80", False), (b"\xe2\x82", False)])
+def test_strings_must_be_utf8(tmp_path, raw, ok):
+    """Keys, string values and tensor names are UTF-8 (gguf.rs:226-243):
+    overlong forms, surrogates, code points past U+10FFFF and truncated
+    sequences are parse errors."""
+    d = struct.pack("<IIQQ", GGUF_MAGIC, 3, 0, 1) + struct.pack("<Q", 1) + b"k" + struct.pack("<I", 8) + \
+        struct.pack("<Q", len(raw)) + raw
+    if ok:
+        with parse(tmp_path, d) as g:
+            assert g.get_str("k") == raw.decode()
+    else:
+        assert "UTF-8" in str(parse_err(tmp_path, d))

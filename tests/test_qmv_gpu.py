@@ -243,3 +243,55 @@ def test_qmv_multi_equals_separate_calls(hip, dt):
         hip.quantized_matmul_multi(hws[:2], hx, [o1, hx], rows[:2], n_cols, dt)   # output aliases input
     for h in hws + [hx, o1, o2]:
         hip.free(h)
+
+
+def test_workspace_users_from_two_threads(hip):
+    """Entry points that stage through the backend workspace (ragged
+    quantized_matmul, split-KV attention) called concurrently from two host
+    threads on one backend: every result equals the single-threaded one."""
+    import threading
+    say("[qmv] workspace users from two threads")
+    jobs = []
+    for t in range(2):
+        n_rows, n_cols = 300 + 7 * t, 1000 + 13 * t
+        dt = DType.Q4_K if t == 0 else DType.Q8_0
+        bs = block_size(dt)
+        w = synth.gen_quant(dt, 500 + t, n_rows, -(-n_cols // bs) * bs)
+        x = synth.gauss(501 + t, n_cols)
+        jobs.append((dt, hip.upload(w), hip.upload(x), hip.allocate(4 * n_rows), n_rows, n_cols))
+    want = []
+    for dt, hw, hx, hy, r, c in jobs:
+        hip.quantized_matmul(hw, hx, hy, r, c, dt)
+        want.append(hip.download(hy, r))
+    nh, nkv, hd, seq = 32, 4, 64, 3000
+    q, kc, vc = synth.gauss(8, nh * hd), synth.gauss(9, (seq, nkv * hd)), synth.gauss(10, (seq, nkv * hd))
+    hq, hk, hv = hip.upload(q), hip.upload(kc), hip.upload(vc)
+    ho = [hip.allocate(4 * nh * hd) for _ in range(2)]
+    hip.gqa_decode_attn(hq, hk, hv, ho[0], nh, nkv, hd, seq)
+    attn_want = hip.download(ho[0], nh * hd)
+    errors = []
+
+    def worker(t):
+        try:
+            dt, hw, hx, hy, r, c = jobs[t]
+            for _ in range(50):
+                hip.quantized_matmul(hw, hx, hy, r, c, dt)
+                hip.gqa_decode_attn(hq, hk, hv, ho[t], nh, nkv, hd, seq)
+        except Exception as e:   # noqa: BLE001
+            errors.append(e)
+    ths = [threading.Thread(target=worker, args=(t,)) for t in range(2)]
+    for th in ths:
+        th.start()
+    for th in ths:
+        th.join()
+    assert not errors
+    hip.synchronize()
+    for (dt, hw, hx, hy, r, c), wv in zip(jobs, want):
+        assert np.array_equal(hip.download(hy, r), wv)
+    for h in ho:
+        assert np.array_equal(hip.download(h, nh * hd), attn_want)
+    for dt, hw, hx, hy, r, c in jobs:
+        for h in (hw, hx, hy):
+            hip.free(h)
+    for h in [hq, hk, hv] + ho:
+        hip.free(h)

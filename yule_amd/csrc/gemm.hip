@@ -521,8 +521,9 @@ extern "C" int yule_hip_quantized_gemm(yule_hip_backend *be, yule_buffer weights
     const size_t part_bytes = ks > 1 ? ((ks * n_y * sizeof(float) + 255) & ~(size_t)255) : 0;
     const size_t need = part_bytes + (n_x + (q4 ? 2 * n_sub : 0)) * sizeof(_Float16) + 256;
     // workspace: split-K partials, then X in f16 (permuted) and its sub-block sums
-    void *ws;
-    if ((rc = get_scratch(be, need, &ws))) return rc;
+    ScratchLease lease;   // held until every launch below is enqueued
+    if ((rc = get_scratch(be, need, &lease))) return rc;
+    void *ws = lease.ptr;
     float *part = ks > 1 ? static_cast<float *>(ws) : nullptr;
     _Float16 *xh = reinterpret_cast<_Float16 *>(static_cast<uint8_t *>(ws) + part_bytes);
     _Float16 *xs_hi = q4 ? xh + n_x : nullptr, *xs_lo = q4 ? xs_hi + n_sub : nullptr;

@@ -77,6 +77,32 @@ bool type_geometry(uint32_t id, uint64_t *bs, uint64_t *bb, bool *quantized) {
     return true;
 }
 
+// Well-formed UTF-8 as Rust's String::from_utf8 accepts it (gguf.rs:226-243
+// rejects anything else): no overlong forms, no surrogates, nothing above
+// U+10FFFF.
+bool valid_utf8(const uint8_t *p, size_t n) {
+    size_t i = 0;
+    while (i < n) {
+        const uint8_t c = p[i];
+        if (c < 0x80) { i++; continue; }
+        size_t len;
+        uint8_t lo = 0x80, hi = 0xBF;   // bounds of the first continuation byte
+        if (c >= 0xC2 && c <= 0xDF) len = 2;
+        else if (c == 0xE0) { len = 3; lo = 0xA0; }
+        else if ((c >= 0xE1 && c <= 0xEC) || c == 0xEE || c == 0xEF) len = 3;
+        else if (c == 0xED) { len = 3; hi = 0x9F; }
+        else if (c == 0xF0) { len = 4; lo = 0x90; }
+        else if (c >= 0xF1 && c <= 0xF3) len = 4;
+        else if (c == 0xF4) { len = 4; hi = 0x8F; }
+        else return false;
+        if (n - i < len || p[i + 1] < lo || p[i + 1] > hi) return false;
+        for (size_t k = 2; k < len; k++)
+            if (p[i + k] < 0x80 || p[i + k] > 0xBF) return false;
+        i += len;
+    }
+    return true;
+}
+
 struct Cursor {
     const uint8_t *p;
     size_t n, pos = 0;
@@ -105,6 +131,10 @@ struct Cursor {
             return false;
         }
         if (!need((size_t)len)) return false;
+        if (!valid_utf8(p + pos, (size_t)len)) {
+            err = "invalid UTF-8 in string at offset " + std::to_string(pos);
+            return false;
+        }
         s->assign(reinterpret_cast<const char *>(p + pos), (size_t)len);
         pos += (size_t)len;
         return true;

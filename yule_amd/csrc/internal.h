@@ -51,10 +51,16 @@ int hip_error(hipError_t e, const char *what);
 int get_buffer(yule_hip_backend *be, uint64_t h, size_t need, void **ptr, const char *what,
                size_t offset = 0);
 
-// At least `need` bytes of the backend's workspace.  Growing it waits for
-// the stream (earlier launches may still read the old one); the pointer is
-// valid until the next call that grows it.
-int get_scratch(yule_hip_backend *be, size_t need, void **ptr);
+// The backend's workspace for one call.  The lease holds the workspace lock
+// until it is destroyed, so a call enqueues every launch that uses the
+// workspace before another thread's call can get it: launches on the one
+// backend stream then never interleave over it.  Growing it waits for the
+// stream (earlier launches may still read the old one).
+struct ScratchLease {
+    std::unique_lock<std::mutex> lock;
+    void *ptr = nullptr;
+};
+int get_scratch(yule_hip_backend *be, size_t need, ScratchLease *lease);
 
 // Launch failures surface through hipGetLastError after a kernel launch.
 int check_launch(const char *what);

@@ -389,10 +389,10 @@ int yule_hip_gqa_decode_attn(yule_hip_backend *be, yule_buffer q, yule_buffer k_
         return rc;
     if (head_dim % 4) return set_error(YULE_ERR_INVALID, "gqa_decode_attn: head_dim must be a multiple of 4");
     if (split && split_attn_supported(n_heads, n_kv_heads, head_dim)) {
-        void *ws;
+        ScratchLease ws;   // held until both launches are enqueued
         if ((rc = get_scratch(be, split_scratch_bytes(n_heads, head_dim, seq_len), &ws))) return rc;
-        return launch_attn_split(be->stream, pq, nullptr, nullptr, pk, pv, nullptr, nullptr, nullptr, po, ws, n_heads,
-                                 n_kv_heads, head_dim, seq_len);
+        return launch_attn_split(be->stream, pq, nullptr, nullptr, pk, pv, nullptr, nullptr, nullptr, po, ws.ptr,
+                                 n_heads, n_kv_heads, head_dim, seq_len);
     }
     return launch_gqa_attn(be->stream, pq, pk, pv, po, n_heads, n_kv_heads, head_dim, seq_len);
 }

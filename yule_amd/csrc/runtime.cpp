@@ -36,8 +36,8 @@ int check_launch(const char *what) {
     return e == hipSuccess ? YULE_OK : hip_error(e, what);
 }
 
-int get_scratch(yule_hip_backend *be, size_t need, void **ptr) {
-    std::lock_guard<std::mutex> lk(be->scratch_mu);
+int get_scratch(yule_hip_backend *be, size_t need, ScratchLease *lease) {
+    std::unique_lock<std::mutex> lk(be->scratch_mu);
     if (be->scratch_size < need) {
         int rc;
         if (be->scratch) {
@@ -50,7 +50,8 @@ int get_scratch(yule_hip_backend *be, size_t need, void **ptr) {
         if ((rc = hip_error(hipMalloc(&be->scratch, sz), "scratch: allocate"))) return rc;
         be->scratch_size = sz;
     }
-    *ptr = be->scratch;
+    lease->ptr = be->scratch;
+    lease->lock = std::move(lk);
     return YULE_OK;
 }
 
@@ -308,18 +309,17 @@ static int prepare_multi(yule_hip_backend *be, uint32_t n_mats, const yule_buffe
 // kernels run unchanged.  (The CPU path floors instead, cpu.rs:544-590; the
 // GPU backends' semantics are the ones a GPU drop-in keeps.)
 static int pad_input(yule_hip_backend *be, uint32_t dtype, const float *x, uint32_t n_cols, const float **xp,
-                     uint32_t *n_cols_p) {
+                     uint32_t *n_cols_p, ScratchLease *ws) {
     uint32_t bs, bb;
     quant_geometry(dtype, &bs, &bb);
     const uint32_t np = (n_cols + bs - 1) / bs * bs;
     *xp = x;
     *n_cols_p = np;
     if (np == n_cols) return YULE_OK;
-    void *ws;
-    int rc = get_scratch(be, (size_t)np * sizeof(float), &ws);
+    int rc = get_scratch(be, (size_t)np * sizeof(float), ws);
     if (rc) return rc;
-    *xp = static_cast<const float *>(ws);
-    return launch_pad(be->stream, x, n_cols, static_cast<float *>(ws), np);
+    *xp = static_cast<const float *>(ws->ptr);
+    return launch_pad(be->stream, x, n_cols, static_cast<float *>(ws->ptr), np);
 }
 
 int yule_hip_quantized_matmul(yule_hip_backend *be, yule_buffer weights, yule_buffer input, yule_buffer output,
@@ -332,7 +332,8 @@ int yule_hip_quantized_matmul(yule_hip_backend *be, yule_buffer weights, yule_bu
     if (empty) return launch_fill(be->stream, y, 0.0f, n_rows);  // zero blocks per row -> y = 0
     const float *xp;
     uint32_t np;
-    if ((rc = pad_input(be, dtype, x, n_cols, &xp, &np))) return rc;
+    ScratchLease ws;   // held until the matvec is enqueued
+    if ((rc = pad_input(be, dtype, x, n_cols, &xp, &np, &ws))) return rc;
     return launch_qmv(be->stream, dtype, w, xp, y, n_rows, np);
 }
 
@@ -356,7 +357,8 @@ int yule_hip_quantized_matmul_multi(yule_hip_backend *be, uint32_t n_mats, const
     }
     const float *xp;
     uint32_t np;
-    if ((rc = pad_input(be, dtype, x, n_cols, &xp, &np))) return rc;
+    ScratchLease ws;   // held until the matvec is enqueued
+    if ((rc = pad_input(be, dtype, x, n_cols, &xp, &np, &ws))) return rc;
     return launch_qmv_multi(be->stream, dtype, segs, n, xp, np);
 }
 
