@@ -81,12 +81,14 @@ struct QmvSeg {
 // activation vector while it is staged, and an epilogue.
 constexpr uint32_t kXfNone = 0, kXfRmsNorm = 1, kXfSwiGlu = 2;
 constexpr uint32_t kEpiStore = 0, kEpiAdd = 1, kEpiArgmax = 2;
+// argmax epilogue slots (one per workgroup of the launch; zero-filled once)
+constexpr uint32_t kArgmaxSlots = 2048;
 struct QmvXf {
     uint32_t mode = kXfNone;         // kXfRmsNorm: x*inv_rms*a; kXfSwiGlu: x*sigmoid(x)*a
     const float *a = nullptr;        // norm weight or up vector, n_cols floats
     float eps = 0.f;
-    uint32_t epi = kEpiStore;        // kEpiAdd: y += result; kEpiArgmax: store + atomicMax(*amax)
-    unsigned long long *amax = nullptr;
+    uint32_t epi = kEpiStore;        // kEpiAdd: y += result; kEpiArgmax: store, and each workgroup's
+    unsigned long long *amax = nullptr;  // best (key << 32 | row) into amax[blockIdx.x] (kArgmaxSlots)
     bool pair = false;               // gate/up pair: segment 0 output = silu(gate)*up
 };
 
@@ -120,10 +122,10 @@ int launch_gqa_attn(hipStream_t stream, const float *q, const float *kc, const f
                     uint32_t n_kv, uint32_t hd, uint32_t seq);
 int launch_argmax(hipStream_t stream, const float *in, uint32_t n, uint32_t *out);
 // decode-runner steps driven by the device control block ctl = {pos, token, prompt_len}
-// (also zeroes *amax when non-null: the lm_head argmax slot of the step)
 int launch_embed_step(hipStream_t stream, uint32_t dtype, const uint8_t *table, const uint32_t *ctl,
-                      const uint32_t *prompt, uint32_t vocab, float *dst, uint32_t dim, unsigned long long *amax);
-int launch_advance(hipStream_t stream, const unsigned long long *amax, uint32_t *ctl, uint32_t *out_tokens);
+                      const uint32_t *prompt, uint32_t vocab, float *dst, uint32_t dim);
+// reduce the lm_head's kArgmaxSlots workgroup slots, then advance the control block
+int launch_advance(hipStream_t stream, const unsigned long long *slots, uint32_t *ctl, uint32_t *out_tokens);
 int launch_rope_kv(hipStream_t stream, float *q, const float *k, const float *v, float *kc, float *vc,
                    const float *cos_t, const float *sin_t, const uint32_t *ctl, uint32_t nq, uint32_t nk,
                    uint32_t hd);

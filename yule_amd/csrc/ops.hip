@@ -436,10 +436,8 @@ __device__ __forceinline__ uint32_t step_token(const uint32_t *ctl, const uint32
 
 __global__ void embed_step_kernel(uint32_t dtype, uint32_t bs, uint32_t bb, const uint8_t *__restrict__ table,
                                   const uint32_t *__restrict__ ctl, const uint32_t *__restrict__ prompt,
-                                  uint32_t vocab, float *__restrict__ dst, uint32_t dim,
-                                  unsigned long long *__restrict__ amax) {
+                                  uint32_t vocab, float *__restrict__ dst, uint32_t dim) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i == 0 && amax) *amax = 0ull;   // this step's lm_head argmax starts empty
     if (i >= dim) return;
     uint32_t t = step_token(ctl, prompt);
     t = t < vocab ? t : vocab - 1;   // host-checked tokens are in range; clamp keeps reads inside the table
@@ -448,11 +446,11 @@ __global__ void embed_step_kernel(uint32_t dtype, uint32_t bs, uint32_t bb, cons
 }
 
 int launch_embed_step(hipStream_t s, uint32_t dtype, const uint8_t *table, const uint32_t *ctl, const uint32_t *prompt,
-                      uint32_t vocab, float *dst, uint32_t dim, unsigned long long *amax) {
+                      uint32_t vocab, float *dst, uint32_t dim) {
     uint32_t bs, bb;
     if (!quant_geometry(dtype, &bs, &bb)) return set_error(YULE_ERR_UNSUPPORTED, "embedding: unsupported dtype");
     hipLaunchKernelGGL(embed_step_kernel, dim3((dim + 255) / 256), dim3(256), 0, s, dtype, bs, bb, table, ctl, prompt,
-                       vocab, dst, dim, amax);
+                       vocab, dst, dim);
     return check_launch("embedding");
 }
 
@@ -904,18 +902,34 @@ __global__ __launch_bounds__(1024) void argmax_advance_kernel(const float *__res
     }
 }
 
-// Advance the control block from the packed argmax key the lm_head matvec
-// left in *amax (low 32 bits: the winning row).
-__global__ void advance_kernel(const unsigned long long *__restrict__ amax, uint32_t *__restrict__ ctl,
-                               uint32_t *__restrict__ out_tokens) {
-    const uint32_t tok = (uint32_t)(*amax & 0xFFFFFFFFull), pos = ctl[0];
-    ctl[1] = tok;
-    out_tokens[pos] = tok;
-    ctl[0] = pos + 1;
+// Advance the control block from the lm_head matvec's argmax: the maximum of
+// the packed keys (key << 32 | row) its workgroups left in their slots (slots
+// no workgroup of the launch owns stay 0 and never win); the low 32 bits are
+// the winning row, the last one among equal maxima.
+__global__ __launch_bounds__(1024) void advance_kernel(const unsigned long long *__restrict__ slots,
+                                                       uint32_t *__restrict__ ctl, uint32_t *__restrict__ out_tokens) {
+    static_assert(kArgmaxSlots == 2 * 1024, "two slots per thread");
+    __shared__ unsigned long long wbest[16];
+    const unsigned long long s0 = slots[threadIdx.x], s1 = slots[threadIdx.x + 1024];
+    unsigned long long b = s0 > s1 ? s0 : s1;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const unsigned long long o = __shfl_xor(b, off, 64);
+        b = o > b ? o : b;
+    }
+    if ((threadIdx.x & 63) == 0) wbest[threadIdx.x >> 6] = b;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 16; w++) b = wbest[w] > b ? wbest[w] : b;
+        const uint32_t tok = (uint32_t)(b & 0xFFFFFFFFull), pos = ctl[0];
+        ctl[1] = tok;
+        out_tokens[pos] = tok;
+        ctl[0] = pos + 1;
+    }
 }
 
-int launch_advance(hipStream_t s, const unsigned long long *amax, uint32_t *ctl, uint32_t *out_tokens) {
-    hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, s, amax, ctl, out_tokens);
+int launch_advance(hipStream_t s, const unsigned long long *slots, uint32_t *ctl, uint32_t *out_tokens) {
+    hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1024), 0, s, slots, ctl, out_tokens);
     return check_launch("advance");
 }
 

@@ -673,7 +673,7 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const Segs sg, const flo
             }
         }
     }
-    if (xf.epi == kEpiArgmax) {   // uniform: one atomic per workgroup
+    if (xf.epi == kEpiArgmax) {   // uniform: the workgroup's best row into its own slot
         __shared__ unsigned long long wbest[NWV];
 #pragma unroll
         for (int off = 32; off >= 1; off >>= 1) {
@@ -685,7 +685,7 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const Segs sg, const flo
         if (tid == 0) {
             unsigned long long b = wbest[0];
             for (uint32_t i = 1; i < NWV; i++) b = wbest[i] > b ? wbest[i] : b;
-            atomicMax(xf.amax, b);
+            xf.amax[blockIdx.x] = b;   // one slot per workgroup: no contended atomic
         }
     }
 }
@@ -718,7 +718,8 @@ static void launch_stream_nt(hipStream_t s, const Segs &sg, const float *x, uint
     const uint32_t rows = xf.pair ? sg.start[1] : sg.total;
     const uint32_t iters = (rows + RI - 1) / RI;
     const uint32_t cap = (uint32_t)(device_cus() * wg);
-    const uint32_t blocks = iters < cap ? iters : cap;
+    uint32_t blocks = iters < cap ? iters : cap;
+    if (xf.epi == kEpiArgmax && blocks > kArgmaxSlots) blocks = kArgmaxSlots;   // one slot per workgroup
     launch_stream_d<F, W, 2, NT>(s, sg, x, bpr, blocks, xf);
 }
 

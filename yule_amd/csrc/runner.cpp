@@ -39,7 +39,7 @@ struct yule_hip_runner {
     float *hidden, *normed, *q, *k, *v, *attn, *proj, *gate, *up, *ffn, *logits;
     uint32_t *ctl = nullptr, *prompt = nullptr, *tokens = nullptr;
     uint32_t *ctl_host = nullptr;  // pinned staging for ctl updates
-    unsigned long long *amax = nullptr;  // lm_head argmax slot (packed key | row)
+    unsigned long long *amax = nullptr;  // lm_head argmax slots, one per workgroup (packed key | row)
     bool fused = false;            // every matrix runs on the streaming matvec
     // attention of steps whose sequence length (pos + 1) reaches split_min
     // runs split-KV (attn_split_kernel + combine, partials in attn_ws);
@@ -121,8 +121,7 @@ int enqueue_step(yule_hip_runner *r, bool split) {
     const uint32_t qd = r->n_heads * r->hd, kvd = r->n_kv * r->hd;
     int rc;
     const bool fuse = r->fused;
-    if ((rc = launch_embed_step(s, r->embd_t, r->embd, r->ctl, r->prompt, r->vocab, r->hidden, r->dim,
-                                fuse ? r->amax : nullptr)))
+    if ((rc = launch_embed_step(s, r->embd_t, r->embd, r->ctl, r->prompt, r->vocab, r->hidden, r->dim)))
         return rc;
     for (const auto &L : r->layers) {
         // attention block (model_runner.rs:619-784)
@@ -326,7 +325,8 @@ int yule_hip_runner_create(yule_hip_backend *be, const yule_model_desc *d, yule_
         (rc = dev_alloc(r, (size_t)r->max_seq * 4, reinterpret_cast<void **>(&r->prompt))) ||
         (rc = dev_alloc(r, (size_t)r->max_seq * 4, reinterpret_cast<void **>(&r->tokens))))
         return fail(rc);
-    if ((rc = dev_alloc(r, sizeof(unsigned long long), reinterpret_cast<void **>(&r->amax)))) return fail(rc);
+    if ((rc = dev_alloc(r, kArgmaxSlots * sizeof(unsigned long long), reinterpret_cast<void **>(&r->amax))))
+        return fail(rc);
     if (r->max_seq >= r->split_min &&
         (rc = dev_alloc(r, split_scratch_bytes(r->n_heads, hd, r->max_seq), &r->attn_ws)))
         return fail(rc);
