@@ -132,7 +132,9 @@ def test_attn_score_value_kats(hip):
 
 
 @pytest.mark.parametrize("hd,nh,nkv,seq", [(2, 2, 1, 2), (64, 32, 4, 384), (128, 32, 8, 1000), (64, 8, 8, 1),
-                                          (256, 8, 2, 200), (64, 32, 4, 600), (80, 8, 2, 77), (32, 4, 4, 33)])
+                                          (256, 8, 2, 200), (64, 32, 4, 600), (80, 8, 2, 77), (32, 4, 4, 33),
+                                          (16, 8, 2, 100), (8, 4, 1, 50), (4, 4, 2, 300), (48, 8, 2, 200),
+                                          (4, 32, 2, 1500), (16, 32, 2, 3000), (96, 32, 2, 1100)])
 def test_gqa_decode_attn(hip, hd, nh, nkv, seq):
     say(f"[ops] gqa_decode_attn hd={hd} heads={nh}/{nkv} seq={seq}")
     if hd == 2:

@@ -12,14 +12,62 @@
 namespace yule {
 
 // ------------------------------------------------------------ reductions
+// Wave reductions by DPP row permutations (VALU latency, unlike the LDS
+// permute network a lane shuffle goes through): lane-xor 1 and 2 inside
+// quads, then the half-row and row mirrors, which pair whole quads and
+// whole half-rows once those hold equal values; the four row results are
+// combined from readlanes.  Every lane returns the wave result; call them
+// with all 64 lanes active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppXor1 = 0xB1;         // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;         // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;  // lane i of 8 <- lane 7 - i
+constexpr int kDppMirror = 0x140;      // lane i of 16 <- lane 15 - i
+__device__ __forceinline__ float lane_of(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
+    v += dpp_mov<kDppXor1>(v);
+    v += dpp_mov<kDppXor2>(v);
+    v += dpp_mov<kDppHalfMirror>(v);
+    v += dpp_mov<kDppMirror>(v);
+    return (lane_of(v, 0) + lane_of(v, 16)) + (lane_of(v, 32) + lane_of(v, 48));
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    v = fmaxf(v, dpp_mov<kDppXor1>(v));
+    v = fmaxf(v, dpp_mov<kDppXor2>(v));
+    v = fmaxf(v, dpp_mov<kDppHalfMirror>(v));
+    v = fmaxf(v, dpp_mov<kDppMirror>(v));
+    return fmaxf(fmaxf(lane_of(v, 0), lane_of(v, 16)), fmaxf(lane_of(v, 32), lane_of(v, 48)));
+}
+// sum over the lanes i, i + n, i + 2n, ... of the wave (n a power of two up
+// to 64), every lane receiving its class's sum: row rotations for strides
+// inside a 16-lane row, then the row and half-wave swaps (each pairs every
+// lane with one other, so adding both swapped copies sums the pair)
+__device__ __forceinline__ float strided_sum(float v, uint32_t n) {
+    if (n <= 1) v += dpp_mov<0x121>(v);   // row_ror:1
+    if (n <= 2) v += dpp_mov<0x122>(v);   // row_ror:2
+    if (n <= 4) v += dpp_mov<0x124>(v);   // row_ror:4
+    if (n <= 8) v += dpp_mov<0x128>(v);   // row_ror:8
+    if (n <= 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    if (n <= 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    return v;
+}
+// sum over aligned groups of n lanes (n = 1, 2, 4 or 8), every lane of a
+// group receiving the group's sum
+__device__ __forceinline__ float group_sum(float v, uint32_t n) {
+    if (n >= 2) v += dpp_mov<kDppXor1>(v);
+    if (n >= 4) v += dpp_mov<kDppXor2>(v);
+    if (n >= 8) v += dpp_mov<kDppHalfMirror>(v);
     return v;
 }
 // block-wide reductions for blockDim.x a multiple of 64 and <= 1024
@@ -460,93 +508,215 @@ int launch_embed_step(hipStream_t s, uint32_t dtype, const uint8_t *table, const
 // 0..pos (model_runner.rs:679-758).  One workgroup per query head; the
 // first head of each KV group writes that group's cache row, and every
 // workgroup uses its own rotated copy of the new k / v for position pos, so
-// no workgroup reads a cache row another one is writing.  Scores: one lane
-// per position (full head-dim dot from float4 loads of the K row); softmax
+// no workgroup reads a cache row another one is writing.  Scores: a few
+// lanes per position (float4 loads of the K row, shuffle-reduced); softmax
 // over LDS; output: lanes over the head dimension, positions split across
-// 256/hd lane groups and combined through LDS.
+// 4·NT/hd lane groups and combined through LDS.
 // Without a control block (ctl == nullptr) it is plain GQA attention of the
 // already-rotated q over cache rows 0..seq_host-1 (the ABI entry point).
-__global__ __launch_bounds__(256) void attn_step_kernel(const float *__restrict__ q, const float *__restrict__ k,
-                                                        const float *__restrict__ v, float *__restrict__ kc,
-                                                        float *__restrict__ vc, const float *__restrict__ cos_t,
-                                                        const float *__restrict__ sin_t,
-                                                        const uint32_t *__restrict__ ctl, float *__restrict__ out,
-                                                        uint32_t group, uint32_t n_kv, uint32_t hd,
-                                                        uint32_t seq_host) {
-    extern __shared__ float scores[];                 // [pos + 1]
+// cache row width bound of attn_step_kernel: its prefetched rows (below
+// 8192) then sit at byte offsets below 2^32
+constexpr uint64_t kAttnMaxKvDim = 1u << 17;
+
+template <int NT>
+__global__ __launch_bounds__(NT) void attn_step_kernel(const float *__restrict__ q, const float *__restrict__ k,
+                                                       const float *__restrict__ v, float *__restrict__ kc,
+                                                       float *__restrict__ vc, const float *__restrict__ cos_t,
+                                                       const float *__restrict__ sin_t,
+                                                       const uint32_t *__restrict__ ctl, float *__restrict__ out,
+                                                       uint32_t group, uint32_t n_kv, uint32_t hd,
+                                                       uint32_t seq_host) {
+    constexpr int PRE = 8;                              // V rows per lane loaded before the softmax
+    constexpr int KPRE = 8;                             // float4 of a K row per lane
+    constexpr uint32_t NW = NT / 64;
+    static_assert(kMaxHeadDim <= NT, "one lane per head dimension");
+    extern __shared__ float scores[];                   // [pos + 1]
     __shared__ __align__(16) float qs[kMaxHeadDim], kn[kMaxHeadDim], vn[kMaxHeadDim];
-    __shared__ __align__(16) float part[1024];          // ng * hd partial outputs (ng * hd = 1024)
-    __shared__ float red[16];
+    __shared__ __align__(16) float part[4 * NT];        // partial outputs: at most ng * hd = 4 * NT
+    __shared__ float red[16], wstat[2 * NW];
     const uint32_t h = blockIdx.x, kvh = h / group, kvs = n_kv * hd, half = hd / 2, tid = threadIdx.x;
+    const uint32_t lane = tid & 63, w = tid >> 6;
     const bool step = ctl != nullptr;
     const uint32_t seq = step ? ctl[0] + 1 : seq_host;
     const uint32_t pos = step ? seq - 1 : 0xFFFFFFFFu;   // row served from the local copy
+    const float *kbase = kc + (size_t)kvh * hd, *vbase = vc + (size_t)kvh * hd;
+    // output layout: each lane owns 4 consecutive dims (float4 of V) and the
+    // positions g, g + ng, ...; the first PRE of them are loaded now, so
+    // their latency overlaps the K loads and the softmax (the row at pos is
+    // loaded and not used: it comes from the local copy).  Cache rows are
+    // buffer loads whose range ends at row seq (lanes past it read zeros),
+    // and a wave skips a prefetch whose positions all lie past seq (a
+    // uniform branch): every issued load costs L1 address cycles, in range
+    // or not.  The RoPE inputs are loaded last; the rotation then waits for
+    // every prefetch too, which all fly at once.
+    const uint32_t nd4 = hd / 4, ng = NT / nd4, d4 = tid % nd4, g = tid / nd4;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(w);
+    // rows 0..seq-1 of this KV head (prefetched rows are below PRE * ng <=
+    // 8192; the host keeps their offsets below 2^32 bytes)
+    const uint64_t row_bytes = (uint64_t)kvs * sizeof(float);
+    const uint64_t rec = (uint64_t)seq * row_bytes;
+    const int nrec = (int)(rec < 0xFFFFFF00ull ? rec : 0xFFFFFF00ull);   // offset 0xFFFFFFF0 stays outside
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(kbase), (short)0, nrec, 0x00020000);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(vbase), (short)0, nrec, 0x00020000);
+    auto row_load = [&](const __amdgpu_buffer_rsrc_t &rs_, uint32_t off) {
+        const auto r = __builtin_amdgcn_raw_buffer_load_b128(rs_, off, 0, 0);
+        return make_float4(__uint_as_float(r[0]), __uint_as_float(r[1]), __uint_as_float(r[2]), __uint_as_float(r[3]));
+    };
+    const uint32_t rb = (uint32_t)row_bytes, vstep = ng * rb, g0 = wv * 64 / nd4;   // g0: the wave's first group
+    uint32_t voff = g * rb + d4 * 16u;
+    asm("" : "+v"(voff));   // keeps the sums below from being re-associated into multiply-adds
+    float4 vpre[PRE];
+#pragma unroll
+    for (int u = 0; u < PRE; u++) {
+        vpre[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (g0 + u * ng < seq) vpre[u] = row_load(vrs, voff + u * vstep);
+    }
+    // scores: kl lanes per position (the smallest power of two giving each
+    // lane at most KPRE float4 of the K row), NT / kl positions per pass; the
+    // first pass's K rows are loaded now, before q is rotated
+    uint32_t kl = 1;
+    while (kl * KPRE < nd4) kl *= 2;
+    const uint32_t kpass = NT / kl, kt = tid / kl, kp = tid % kl;
+    float4 kpre[KPRE];
+    uint32_t koff = kt * rb;
+    asm("" : "+v"(koff));
+#pragma unroll
+    for (int u = 0; u < KPRE; u++) kpre[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (wv * 64 / kl < seq) {
+#pragma unroll
+        for (int u = 0; u < KPRE; u++) {
+            const uint32_t c4 = kp + u * kl;   // columns past the row read zeros
+            kpre[u] = row_load(krs, c4 < nd4 ? koff + c4 * 16u : 0xFFFFFFF0u);
+        }
+    }
     const float *qh = q + (size_t)h * hd;
-    if (!step) {
-        for (uint32_t i = tid; i < hd; i += 256) qs[i] = qh[i];
+    const float *kh = step ? k + (size_t)kvh * hd : qh, *vh = step ? v + (size_t)kvh * hd : qh;
+    const float *ct = step ? cos_t + (size_t)pos * half : qh, *st = step ? sin_t + (size_t)pos * half : qh;
+    const uint32_t ri = tid < half ? tid : half - 1, vi = tid < hd ? tid : hd - 1;
+    const float rc = ct[ri], rs = st[ri], qx0 = qh[2 * ri], qx1 = qh[2 * ri + 1];
+    const float kx0 = kh[2 * ri], kx1 = kh[2 * ri + 1], vx = vh[vi];
+    if (step && tid < half) {
+        qs[2 * tid] = qx0 * rc - qx1 * rs;
+        qs[2 * tid + 1] = qx0 * rs + qx1 * rc;
+        kn[2 * tid] = kx0 * rc - kx1 * rs;
+        kn[2 * tid + 1] = kx0 * rs + kx1 * rc;
     }
-    const float *kh = step ? k + (size_t)kvh * hd : nullptr, *vh = step ? v + (size_t)kvh * hd : nullptr;
-    for (uint32_t i = tid; step && i < half; i += 256) {
-        const float c = cos_t[(size_t)pos * half + i], sn = sin_t[(size_t)pos * half + i];
-        float x0 = qh[2 * i], x1 = qh[2 * i + 1];
-        qs[2 * i] = x0 * c - x1 * sn;
-        qs[2 * i + 1] = x0 * sn + x1 * c;
-        x0 = kh[2 * i]; x1 = kh[2 * i + 1];
-        kn[2 * i] = x0 * c - x1 * sn;
-        kn[2 * i + 1] = x0 * sn + x1 * c;
-    }
-    for (uint32_t i = tid; step && i < hd; i += 256) vn[i] = vh[i];
+    if (tid < hd) (step ? vn : qs)[tid] = vx;
     __syncthreads();
     if (step && h % group == 0) {
         float *krow = kc + (size_t)pos * kvs + kvh * hd, *vrow = vc + (size_t)pos * kvs + kvh * hd;
-        for (uint32_t i = tid; i < hd; i += 256) { krow[i] = kn[i]; vrow[i] = vn[i]; }
+        for (uint32_t i = tid; i < hd; i += NT) { krow[i] = kn[i]; vrow[i] = vn[i]; }
     }
     const float scale = 1.0f / sqrtf((float)hd);
-    float m = -INFINITY;
-    for (uint32_t t = tid; t < seq; t += 256) {
-        const float4 *kr = reinterpret_cast<const float4 *>(t == pos ? kn : kc + (size_t)t * kvs + kvh * hd);
-        float acc = 0.f;
-        for (uint32_t c4 = 0; c4 < hd / 4; c4++) {
-            const float4 kv = kr[c4];
-            acc += qs[4 * c4] * kv.x;
-            acc += qs[4 * c4 + 1] * kv.y;
-            acc += qs[4 * c4 + 2] * kv.z;
-            acc += qs[4 * c4 + 3] * kv.w;
+    const float4 *qs4 = reinterpret_cast<const float4 *>(qs), *kn4 = reinterpret_cast<const float4 *>(kn);
+    const float4 *vn4 = reinterpret_cast<const float4 *>(vn);
+    // the registers holding row pos take the local copy (the cache row may
+    // not be written yet); the loops below are then free of branches
+    if (step) {
+        if (kt == pos) {
+#pragma unroll
+            for (int u = 0; u < KPRE; u++) {
+                const uint32_t c4 = kp + u * kl;
+                kpre[u] = c4 < nd4 ? kn4[c4] : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
         }
-        const float sc = acc * scale;
-        scores[t] = sc;
-        m = fmaxf(m, sc);
+#pragma unroll
+        for (int u = 0; u < PRE; u++)
+            if (g + u * ng == pos) vpre[u] = vn4[d4];
     }
-    m = block_max(m, red);
-    float sum = 0.f;
-    for (uint32_t t = tid; t < seq; t += 256) {
-        const float e = expf(scores[t] - m);
-        scores[t] = e;
-        sum += e;
+    // softmax weights: p_t = scores[t] * f[wave of t] * inv.  One pass:
+    // scores hold exp(s_t - m_w) with m_w the max of wave w's positions, and
+    // f[w] = exp(m_w - M) (lane w of every wave holds f[w]).  Several passes:
+    // block-wide max and sum, f = 1.
+    float fl = 1.f, inv;
+    if (seq <= kpass) {
+        // q . K_t over this lane's float4s kp + u * kl of the row (zeros past
+        // it), summed over the kl lanes
+        float acc = 0.f;
+#pragma unroll
+        for (int u = 0; u < KPRE; u++) {
+            const uint32_t c4 = kp + u * kl;
+            const float4 qv = qs4[c4 < nd4 ? c4 : nd4 - 1], kr = kpre[u];
+            acc += qv.x * kr.x;
+            acc += qv.y * kr.y;
+            acc += qv.z * kr.z;
+            acc += qv.w * kr.w;
+        }
+        const bool valid = kt < seq;
+        const float sc = group_sum(acc, kl) * scale;
+        const float mw = wave_max(valid ? sc : -INFINITY);
+        const float e = valid ? expf(sc - mw) : 0.f;
+        const float lw = wave_sum(kp == 0 ? e : 0.f);
+        if (valid && kp == 0) scores[kt] = e;
+        if (lane == 0) { wstat[2 * w] = mw; wstat[2 * w + 1] = lw; }
+        __syncthreads();
+        const float ml = lane < NW ? wstat[2 * lane] : -INFINITY;
+        const float mx = wave_max(ml);
+        fl = lane < NW ? expf(ml - mx) : 0.f;
+        inv = 1.0f / wave_sum(lane < NW ? fl * wstat[2 * lane + 1] : 0.f);
+    } else {
+        float m = -INFINITY;
+        for (uint32_t base = 0; base < seq; base += kpass) {
+            const uint32_t t = base + kt;
+            const float4 *kr = reinterpret_cast<const float4 *>(kbase + (size_t)(t < seq ? t : seq - 1) * kvs);
+            float acc = 0.f;
+#pragma unroll
+            for (int u = 0; u < KPRE; u++) {
+                const uint32_t c4 = kp + u * kl;
+                if (c4 < nd4) {
+                    const float4 kv = t == pos ? kn4[c4] : kr[c4], qv = qs4[c4];
+                    acc += qv.x * kv.x;
+                    acc += qv.y * kv.y;
+                    acc += qv.z * kv.z;
+                    acc += qv.w * kv.w;
+                }
+            }
+            const float sc = group_sum(acc, kl) * scale;
+            if (t < seq) {
+                if (kp == 0) scores[t] = sc;
+                m = fmaxf(m, sc);
+            }
+        }
+        m = block_max(m, red);
+        float sum = 0.f;
+        for (uint32_t t = tid; t < seq; t += NT) {
+            const float e = expf(scores[t] - m);
+            scores[t] = e;
+            sum += e;
+        }
+        inv = 1.0f / block_sum(sum, red);   // its barriers also publish scores[]
     }
-    sum = block_sum(sum, red);   // its barriers also publish scores[]
-    const float inv = 1.0f / sum;
-    // output: each lane owns 4 consecutive dims (float4 of V) and a
-    // residue class of positions; four independent accumulators keep four
-    // V loads in flight per lane
-    const uint32_t nd4 = hd / 4, ng = 256 / nd4, d4 = tid % nd4, g = tid / nd4;
+    // the prefetched positions (lanes of groups g >= ng, which exist only when
+    // hd / 4 does not divide NT, accumulate what is never written out)
     float4 o[4];
 #pragma unroll
     for (int u = 0; u < 4; u++) o[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int u = 0; u < PRE; u++) {
+        const uint32_t t = g + u * ng, wt = t * kl / 64;
+        const float f = __shfl(fl, wt < NW ? wt : NW - 1, 64);   // 1 beyond the first pass
+        const float sv = scores[t < seq ? t : seq - 1];
+        const float p = t < seq ? sv * f * inv : 0.f;
+        const float4 vv = vpre[u];
+        float4 &a = o[u & 3];
+        a.x += p * vv.x; a.y += p * vv.y; a.z += p * vv.z; a.w += p * vv.w;
+    }
+    // positions past the preloaded ones (several passes only): four
+    // independent accumulators keep four V loads in flight per lane
     if (g < ng) {
-        uint32_t t = g;
+        uint32_t t = g + PRE * ng;
         for (; t + 3 * ng < seq; t += 4 * ng) {
 #pragma unroll
             for (int u = 0; u < 4; u++) {
                 const uint32_t tt = t + u * ng;
-                const float *vr = tt == pos ? vn : vc + (size_t)tt * kvs + kvh * hd;
+                const float *vr = tt == pos ? vn : vbase + (size_t)tt * kvs;
                 const float4 vv = reinterpret_cast<const float4 *>(vr)[d4];
                 const float p = scores[tt] * inv;
                 o[u].x += p * vv.x; o[u].y += p * vv.y; o[u].z += p * vv.z; o[u].w += p * vv.w;
             }
         }
         for (; t < seq; t += ng) {
-            const float *vr = t == pos ? vn : vc + (size_t)t * kvs + kvh * hd;
+            const float *vr = t == pos ? vn : vbase + (size_t)t * kvs;
             const float4 vv = reinterpret_cast<const float4 *>(vr)[d4];
             const float p = scores[t] * inv;
             o[0].x += p * vv.x; o[0].y += p * vv.y; o[0].z += p * vv.z; o[0].w += p * vv.w;
@@ -557,12 +727,25 @@ __global__ __launch_bounds__(256) void attn_step_kernel(const float *__restrict_
     acc4.y = (o[0].y + o[1].y) + (o[2].y + o[3].y);
     acc4.z = (o[0].z + o[1].z) + (o[2].z + o[3].z);
     acc4.w = (o[0].w + o[1].w) + (o[2].w + o[3].w);
-    if (g < ng) reinterpret_cast<float4 *>(part)[g * nd4 + d4] = acc4;
+    // combine the lane groups: when hd / 4 divides 64, the groups inside a
+    // wave first by shuffles, leaving NW partials per dim; otherwise all ng
+    const bool in_wave = 64 % nd4 == 0;
+    if (in_wave) {
+        acc4.x = strided_sum(acc4.x, nd4);
+        acc4.y = strided_sum(acc4.y, nd4);
+        acc4.z = strided_sum(acc4.z, nd4);
+        acc4.w = strided_sum(acc4.w, nd4);
+        if (lane < nd4) reinterpret_cast<float4 *>(part)[w * nd4 + d4] = acc4;
+    } else if (g < ng) {
+        reinterpret_cast<float4 *>(part)[g * nd4 + d4] = acc4;
+    }
     __syncthreads();
-    if (tid < hd) {
+    const uint32_t nparts = in_wave ? NW : ng;
+    for (uint32_t i = tid; i < hd; i += NT) {
         float acc = 0.f;
-        for (uint32_t i = 0; i < ng; i++) acc += part[i * hd + tid];
-        out[(size_t)h * hd + tid] = acc;
+#pragma unroll 16
+        for (uint32_t j = 0; j < nparts; j++) acc += part[j * hd + i];
+        out[(size_t)h * hd + i] = acc;
     }
 }
 
@@ -815,19 +998,43 @@ int launch_attn_split(hipStream_t s, const float *q, const float *k, const float
     return check_launch("attn_combine");
 }
 
+// workgroup size of the one-workgroup-per-head attention kernel
+// (environment YULE_ATTN_THREADS: 256 or 1024, default 1024)
+static int attn_threads() {
+    static const int nt = [] {
+        const char *e = getenv("YULE_ATTN_THREADS");
+        return e && strtol(e, nullptr, 10) == 256 ? 256 : 1024;
+    }();
+    return nt;
+}
+
 int launch_attn_step(hipStream_t s, const float *q, const float *k, const float *v, float *kc, float *vc,
                      const float *cos_t, const float *sin_t, const uint32_t *ctl, float *out, uint32_t n_heads,
                      uint32_t n_kv, uint32_t hd, uint32_t max_seq) {
-    hipLaunchKernelGGL(attn_step_kernel, dim3(n_heads), dim3(256), (size_t)max_seq * sizeof(float), s, q, k, v, kc, vc,
-                       cos_t, sin_t, ctl, out, n_heads / n_kv, n_kv, hd, 0u);
+    if ((uint64_t)n_kv * hd > kAttnMaxKvDim)
+        return set_error(YULE_ERR_UNSUPPORTED, "attention: n_kv_heads * head_dim above 131072");
+    const size_t lds = (size_t)max_seq * sizeof(float);
+    if (attn_threads() == 1024)
+        hipLaunchKernelGGL(attn_step_kernel<1024>, dim3(n_heads), dim3(1024), lds, s, q, k, v, kc, vc, cos_t, sin_t,
+                           ctl, out, n_heads / n_kv, n_kv, hd, 0u);
+    else
+        hipLaunchKernelGGL(attn_step_kernel<256>, dim3(n_heads), dim3(256), lds, s, q, k, v, kc, vc, cos_t, sin_t,
+                           ctl, out, n_heads / n_kv, n_kv, hd, 0u);
     return check_launch("attn_step");
 }
 
 int launch_gqa_attn(hipStream_t s, const float *q, const float *kc, const float *vc, float *out, uint32_t n_heads,
                     uint32_t n_kv, uint32_t hd, uint32_t seq) {
-    hipLaunchKernelGGL(attn_step_kernel, dim3(n_heads), dim3(256), (size_t)seq * sizeof(float), s, q, nullptr, nullptr,
-                       const_cast<float *>(kc), const_cast<float *>(vc), nullptr, nullptr, nullptr, out,
-                       n_heads / n_kv, n_kv, hd, seq);
+    if ((uint64_t)n_kv * hd > kAttnMaxKvDim)
+        return set_error(YULE_ERR_UNSUPPORTED, "gqa_decode_attn: n_kv_heads * head_dim above 131072");
+    const size_t lds = (size_t)seq * sizeof(float);
+    float *kcw = const_cast<float *>(kc), *vcw = const_cast<float *>(vc);
+    if (attn_threads() == 1024)
+        hipLaunchKernelGGL(attn_step_kernel<1024>, dim3(n_heads), dim3(1024), lds, s, q, nullptr, nullptr, kcw, vcw,
+                           nullptr, nullptr, nullptr, out, n_heads / n_kv, n_kv, hd, seq);
+    else
+        hipLaunchKernelGGL(attn_step_kernel<256>, dim3(n_heads), dim3(256), lds, s, q, nullptr, nullptr, kcw, vcw,
+                           nullptr, nullptr, nullptr, out, n_heads / n_kv, n_kv, hd, seq);
     return check_launch("gqa_decode_attn");
 }
 
