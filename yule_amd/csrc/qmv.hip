@@ -500,7 +500,7 @@ struct RawPair {
 // PAIR: segments 0 and 1 are the gate and up matrices (equal row counts);
 // a team computes row r of both and stores silu(g)*u into segment 0's
 // output (model_runner.rs:963-972), so SwiGLU costs nothing extra.
-template <class F, int W, int D, int NT, bool PAIR = false>
+template <class F, int W, int D, int NT, bool PAIR, bool TWO>
 __global__ __launch_bounds__(NT) void qmv_stream_kernel(const Segs sg, const float *__restrict__ x, uint32_t bpr,
                                                         const QmvXf xf) {
     static_assert(!PAIR || W <= 64, "paired rows need single-wave teams");
@@ -561,26 +561,35 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const Segs sg, const flo
         }
     };
 
-    // Prologue order: this thread's share of x is loaded into registers
-    // first, then the first rows' weight loads are issued, then x goes to
-    // LDS.  Loads complete in issue order, so waiting for x does not wait
-    // for the weights, and HBM latency overlaps the whole staging.
-    constexpr uint32_t kXPer = 8;   // float4 of x per thread held in flight (K <= 8192 in one pass)
+    // Prologue order: this thread's share of x, and of the fused input
+    // transform's second operand (RMSNorm weight or SwiGLU up), is loaded
+    // into registers first, then the first rows' weight loads are issued,
+    // then x goes to LDS.  Loads complete in issue order, so waiting for x
+    // does not wait for the weights, and HBM latency overlaps the whole
+    // staging.
+    // float4 of x per thread held in flight (K <= 32 * NT in one pass; paired
+    // kernels hold fewer, keeping their register count)
+    constexpr uint32_t kXPer = PAIR ? 4 : 8;
     Buf buf[D];
+    // TWO: a fused input transform is on (its operand is loaded with x); a
+    // template parameter, so the plain kernels carry none of its code
     {
         const uint32_t n = bpr * F::BS, n4 = n / 4;
         const float4 *x4 = reinterpret_cast<const float4 *>(x), *a4 = reinterpret_cast<const float4 *>(xf.a);
-        float4 xv[kXPer];
+        float4 xv[kXPer], av[kXPer];
 #pragma unroll
         for (uint32_t q = 0; q < kXPer; q++) {
             const uint32_t i = tid + NT * q;
-            if (i < n4) xv[q] = x4[i];
+            if (i < n4) {
+                xv[q] = x4[i];
+                if constexpr (TWO) av[q] = a4[i];
+            }
         }
 #pragma unroll
         for (int j = 0; j < D - 1; j++)
             if (r0 + j * stride < n_rows) buf[j] = fetch(r0 + j * stride);
         float inv = 1.0f;
-        if (xf.mode == kXfRmsNorm) {
+        if (TWO && xf.mode == kXfRmsNorm) {
             // rms_norm (model_runner.rs:246-275) computed by every workgroup
             float ss = 0.f;
 #pragma unroll
@@ -601,24 +610,22 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const Segs sg, const flo
             for (uint32_t i = 0; i < NWV; i++) ss += part[i];
             inv = 1.0f / sqrtf(ss / (float)n + xf.eps);
         }
-        auto put = [&](uint32_t i, float4 v) {
-            if (xf.mode == kXfRmsNorm) {
-                const float4 wv = a4[i];
-                v.x = v.x * inv * wv.x; v.y = v.y * inv * wv.y; v.z = v.z * inv * wv.z; v.w = v.w * inv * wv.w;
-            } else if (xf.mode == kXfSwiGlu) {
+        auto put = [&](uint32_t i, float4 v, float4 a) {
+            if (TWO && xf.mode == kXfRmsNorm) {
+                v.x = v.x * inv * a.x; v.y = v.y * inv * a.y; v.z = v.z * inv * a.z; v.w = v.w * inv * a.w;
+            } else if (TWO && xf.mode == kXfSwiGlu) {
                 // gate * sigmoid(gate) * up (model_runner.rs:967-972)
-                const float4 u = a4[i];
-                v.x = v.x * (1.0f / (1.0f + expf(-v.x))) * u.x;
-                v.y = v.y * (1.0f / (1.0f + expf(-v.y))) * u.y;
-                v.z = v.z * (1.0f / (1.0f + expf(-v.z))) * u.z;
-                v.w = v.w * (1.0f / (1.0f + expf(-v.w))) * u.w;
+                v.x = v.x * (1.0f / (1.0f + expf(-v.x))) * a.x;
+                v.y = v.y * (1.0f / (1.0f + expf(-v.y))) * a.y;
+                v.z = v.z * (1.0f / (1.0f + expf(-v.z))) * a.z;
+                v.w = v.w * (1.0f / (1.0f + expf(-v.w))) * a.w;
             }
             *reinterpret_cast<float4 *>(xl + lds_pad(4 * i)) = v;
         };
 #pragma unroll
         for (uint32_t q = 0; q < kXPer; q++)
-            if (tid + NT * q < n4) put(tid + NT * q, xv[q]);
-        for (uint32_t i = tid + NT * kXPer; i < n4; i += NT) put(i, x4[i]);
+            if (tid + NT * q < n4) put(tid + NT * q, xv[q], TWO ? av[q] : xv[q]);
+        for (uint32_t i = tid + NT * kXPer; i < n4; i += NT) put(i, x4[i], TWO ? a4[i] : x4[i]);
         __syncthreads();
     }
     float xs[F::NX], aux[F::NAUX];
@@ -695,13 +702,18 @@ static void launch_stream_d(hipStream_t s, const Segs &sg, const float *x, uint3
                             const QmvXf &xf) {
     const size_t lds = (size_t)lds_pad(bpr * F::BS) * sizeof(float);
     if constexpr (W <= 64) {
-        if (xf.pair) {
-            hipLaunchKernelGGL((qmv_stream_kernel<F, W, D, NT, true>), dim3(blocks), dim3(NT), lds, s, sg, x, bpr,
-                               xf);
+        if (xf.pair) {   // always with a transform (checked by launch_qmv_fused)
+            hipLaunchKernelGGL((qmv_stream_kernel<F, W, D, NT, true, true>), dim3(blocks), dim3(NT), lds, s, sg, x,
+                               bpr, xf);
             return;
         }
     }
-    hipLaunchKernelGGL((qmv_stream_kernel<F, W, D, NT>), dim3(blocks), dim3(NT), lds, s, sg, x, bpr, xf);
+    if (xf.mode != kXfNone)
+        hipLaunchKernelGGL((qmv_stream_kernel<F, W, D, NT, false, true>), dim3(blocks), dim3(NT), lds, s, sg, x, bpr,
+                           xf);
+    else
+        hipLaunchKernelGGL((qmv_stream_kernel<F, W, D, NT, false, false>), dim3(blocks), dim3(NT), lds, s, sg, x,
+                           bpr, xf);
 }
 
 // Workgroup shape: NT threads (RI = NT / W teams) share one LDS copy of the
@@ -804,8 +816,9 @@ int launch_qmv_fused(hipStream_t s, uint32_t dtype, const QmvSeg *segs, uint32_t
     if (n_seg == 0 || n_seg > kMaxSegs) return set_error(YULE_ERR_INVALID, "quantized_matmul: bad segment count");
     if (xf.epi == kEpiArgmax && n_seg != 1)
         return set_error(YULE_ERR_INVALID, "quantized_matmul: argmax epilogue needs a single matrix");
-    if (xf.pair && (n_seg != 2 || segs[0].n_rows != segs[1].n_rows || !qmv_pairable(dtype, n_cols)))
-        return set_error(YULE_ERR_INVALID, "quantized_matmul: paired gate/up needs two equal single-wave matrices");
+    if (xf.pair && (n_seg != 2 || segs[0].n_rows != segs[1].n_rows || !qmv_pairable(dtype, n_cols) ||
+                    xf.mode == kXfNone))
+        return set_error(YULE_ERR_INVALID, "quantized_matmul: paired gate/up needs two equal single-wave matrices and an input transform");
     int rc;
     switch (dtype) {
     case YULE_DTYPE_Q4_K: rc = launch_fmt<Q4K>(s, segs, n_seg, x, n_cols, xf); break;
