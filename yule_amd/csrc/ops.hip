@@ -45,21 +45,17 @@ __device__ __forceinline__ float wave_max(float v) {
 }
 // sum over the lanes i, i + n, i + 2n, ... of the wave (n a power of two up
 // to 64), every lane receiving its class's sum: row rotations for strides
-// inside a 16-lane row, then the row and half-wave swaps (each pairs every
-// lane with one other, so adding both swapped copies sums the pair)
+// inside a 16-lane row, lane shuffles across rows.  (The gfx950 row and
+// half-wave swap builtins were tried for the cross-row steps: with both
+// operands the same value the optimizer has folded the two swapped copies
+// into one in some contexts, giving wrong sums, so they are not used.)
 __device__ __forceinline__ float strided_sum(float v, uint32_t n) {
     if (n <= 1) v += dpp_mov<0x121>(v);   // row_ror:1
     if (n <= 2) v += dpp_mov<0x122>(v);   // row_ror:2
     if (n <= 4) v += dpp_mov<0x124>(v);   // row_ror:4
     if (n <= 8) v += dpp_mov<0x128>(v);   // row_ror:8
-    if (n <= 16) {
-        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-        v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-    }
-    if (n <= 32) {
-        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-        v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-    }
+    if (n <= 16) v += __shfl_xor(v, 16, 64);
+    if (n <= 32) v += __shfl_xor(v, 32, 64);
     return v;
 }
 // sum over aligned groups of n lanes (n = 1, 2, 4 or 8), every lane of a
