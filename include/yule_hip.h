@@ -170,6 +170,7 @@ int yule_hip_silu_mul(yule_hip_backend *be, yule_buffer gate, yule_buffer up, yu
  * (environment YULE_ATTN_SPLIT_MIN) it runs split-KV (flash-decoding,
  * shaders/flash_decode_split.comp + flash_decode_reduce.comp) when a KV
  * head serves <= 8 query heads; above 16384 positions that is required.
+ * Below the split threshold n_kv_heads*head_dim must be <= 131072.
  * The split partials live in a backend-owned workspace. */
 int yule_hip_gqa_decode_attn(yule_hip_backend *be, yule_buffer q, yule_buffer k_cache,
                              yule_buffer v_cache, yule_buffer out, uint32_t n_heads,
