@@ -201,6 +201,8 @@ def test_gqa_decode_attn_limits(hip):
         hip.gqa_decode_attn(h, h, h, h, 32, 2, 64, 16385)
     with pytest.raises(YuleGpuError, match="262144"):
         hip.gqa_decode_attn(h, h, h, h, 32, 4, 64, 262145)
+    with pytest.raises(YuleGpuError, match="131072"):   # per-head kernel's cache row width
+        hip.gqa_decode_attn(h, h, h, h, 513, 513, 256, 10)
     hip.free(h)
 
 

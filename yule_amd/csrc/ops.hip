@@ -224,6 +224,9 @@ __global__ void attn_value_kernel(const float *__restrict__ w, const float *__re
 // ------------------------------------------------------------ GQA decode attention
 constexpr uint32_t kMaxSeqLds = 16384;
 constexpr uint32_t kMaxHeadDim = 256;
+// cache row width bound of attn_step_kernel: its prefetched rows (below
+// 8192) then sit at byte offsets below 2^32
+constexpr uint64_t kAttnMaxKvDim = 1u << 17;
 
 // ------------------------------------------------------------ argmax
 // argmax_ct (sampler.rs:150-163): the last maximal index wins.
@@ -423,6 +426,8 @@ int yule_hip_gqa_decode_attn(yule_hip_backend *be, yule_buffer q, yule_buffer k_
         return set_error(YULE_ERR_INVALID, "gqa_decode_attn: seq_len must be in 1..262144");
     if (split && !split_attn_supported(n_heads, n_kv_heads, head_dim) && seq_len > kMaxSeqLds)
         return set_error(YULE_ERR_UNSUPPORTED, "gqa_decode_attn: above 16384 positions needs <= 8 query heads per KV head");
+    if (!(split && split_attn_supported(n_heads, n_kv_heads, head_dim)) && (uint64_t)n_kv_heads * head_dim > kAttnMaxKvDim)
+        return set_error(YULE_ERR_UNSUPPORTED, "gqa_decode_attn: n_kv_heads * head_dim above 131072");
     float *pq, *pk, *pv, *po;
     int rc;
     const size_t kv = (size_t)seq_len * n_kv_heads * head_dim;
@@ -510,9 +515,6 @@ int launch_embed_step(hipStream_t s, uint32_t dtype, const uint8_t *table, const
 // 4·NT/hd lane groups and combined through LDS.
 // Without a control block (ctl == nullptr) it is plain GQA attention of the
 // already-rotated q over cache rows 0..seq_host-1 (the ABI entry point).
-// cache row width bound of attn_step_kernel: its prefetched rows (below
-// 8192) then sit at byte offsets below 2^32
-constexpr uint64_t kAttnMaxKvDim = 1u << 17;
 // its workgroup size (256 measured 6.0 / 9.7 us at 64 / 384 positions against
 // 6.4 / 7.5 us for 1024, TinyLlama shapes)
 constexpr int kAttnThreads = 1024;
