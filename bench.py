@@ -249,26 +249,27 @@ def decode_e2e(hip, cpu: bool):
 MFMA_F16_PEAK_TFLOPS = 2500.0   # MI355X dense f16/bf16 MFMA
 
 
-def prefill_gemm(hip):
+def prefill_gemm(hip, dt=DType.Q4_K, shapes=((14336, 4096), (4096, 14336)), ms_=(64, 512, 2048)):
     """Q4_K 14336x4096 and 4096x14336 weights times a bf16
-    activation matrix of M in {64, 512, 2048} rows, on the MFMA path."""
+    activation matrix of M in {64, 512, 2048} rows, on the MFMA path (other
+    formats: the same kernel family, reported beside it)."""
     out = {}
-    for n_rows, n_cols in ((14336, 4096), (4096, 14336)):
-        w = hip.upload(synth.gen_quant(DType.Q4_K, 81, n_rows, n_cols))
-        for M in (64, 512, 2048):
+    for n_rows, n_cols in shapes:
+        w = hip.upload(synth.gen_quant(dt, 81, n_rows, n_cols))
+        for M in ms_:
             xb = (synth.gauss(82, (M, n_cols)).view(np.uint32) >> 16).astype(np.uint16)   # bf16 (truncated)
             hx, hy = hip.upload(xb), hip.allocate(4 * M * n_rows)
             reps = max(3, min(50, int(2e4 // M)))
-            hip.quantized_gemm(w, hx, hy, M, n_rows, n_cols, DType.Q4_K)   # warm-up
+            hip.quantized_gemm(w, hx, hy, M, n_rows, n_cols, dt)   # warm-up
             hip.synchronize()
             hip.timer_start()
             for _ in range(reps):
-                hip.quantized_gemm(w, hx, hy, M, n_rows, n_cols, DType.Q4_K)
+                hip.quantized_gemm(w, hx, hy, M, n_rows, n_cols, dt)
             ms = hip.timer_stop() / reps
             tflops = 2.0 * M * n_rows * n_cols / (ms * 1e-3) / 1e12
             out[f"{n_rows}x{n_cols} M={M}"] = {"us": round(ms * 1e3, 1), "TFLOP/s": round(tflops, 1),
                                                "mfma_util": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
-            log(f"prefill GEMM Q4_K {n_rows}x{n_cols} M={M}: {ms * 1e3:.1f} us, {tflops:.1f} TFLOP/s")
+            log(f"prefill GEMM {dt.name} {n_rows}x{n_cols} M={M}: {ms * 1e3:.1f} us, {tflops:.1f} TFLOP/s")
             hip.free(hx)
             hip.free(hy)
         hip.free(w)
@@ -424,6 +425,8 @@ def main():
 
     if not args.quick:
         extra["prefill_gemm_q4k"] = prefill_gemm(hip)
+        extra["prefill_gemm_other_formats"] = {
+            dt.name: prefill_gemm(hip, dt, ((14336, 4096),), (512, 2048)) for dt in (DType.Q6_K, DType.Q8_0, DType.Q4_0)}
         for dt in (DType.Q6_K, DType.Q8_0):
             log(f"generating Llama-3-8B {dt.name} layer")
             L = Layer(hip, dt, LLAMA3_LAYER, args.copies, seed=21 + int(dt))

@@ -19,6 +19,10 @@
 //  * Q6_K, w = d*sc*(q-32): the B operand is sc*(q-32) (|.| <= 4064; exact
 //    up to 2048, above that rounded to the nearest even integer, i.e.
 //    < 2.5e-4 relative on those few weights), d applied per super-block.
+//  * Q8_0 / Q4_0, w = d*q and d*(q-8): the B operand is the integer q or
+//    q - 8 (exact in f16, made from 1024 + q with one packed subtract), d
+//    applied per 32-weight block: a 32-k MFMA step is exactly one block, so
+//    acc += d * (that step's product).
 //  * X: bf16 -> f16 is exact for every bf16 in f16's normal range.  A pre-pass
 //    converts X once per call (not once per weight tile) and stores each group
 //    of four k in the order {0,2,1,3}, the order in which the dword nibble
@@ -116,20 +120,33 @@ struct GemmRegs {
     uint4 h, q;
     uint32_t ql[9], qh[9], sc[2], d[2];
     uint32_t mql, mqh, msc, md;
+    uint32_t qb[10], mqb;   // Q8_0 / Q4_0: the thread's 32-weight block as raw dwords
 };
+
+// 32-weight-block formats: block bytes (2-byte d, then the quants)
+template <uint32_t DT>
+constexpr uint32_t block32_bytes() { return DT == YULE_DTYPE_Q8_0 ? 34u : 18u; }
+
+// two f16 in a dword from two 8-bit fields (bits 0-7, 16-23; upper bits
+// clear): 1024 + u is exact, so subtracting (1024 + bias) leaves u - bias
+__device__ __forceinline__ uint32_t u8pair_to_f16(uint32_t v, _Float16 bias) {
+    const h2v h = __builtin_bit_cast(h2v, v | 0x64006400u) - h2v{(_Float16)1024.0f + bias, (_Float16)1024.0f + bias};
+    return __builtin_bit_cast(uint32_t, h);
+}
 
 // Split-K: split z of `splits` takes super-blocks [kb_lo, kb_hi) and,
 // when splits > 1, writes its partial tile to y + z*M*N (summed in a
 // fixed order by gemm_reduce_kernel, so results do not depend on timing).
-// Q4_K runs two waves per SIMD (the register budget holds with a few spilled
-// bytes); Q6_K's larger dequant state keeps it at one.
+// Q4_K, Q8_0 and Q4_0 run two waves per SIMD (Q4_K's register budget holds
+// with a few spilled bytes); Q6_K's larger dequant state keeps it at one.
 template <uint32_t DT, int BM, int BN>
-__global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YULE_DTYPE_Q4_K ? 2 : 1))) void gemm_kernel(
+__global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YULE_DTYPE_Q6_K ? 1 : 2))) void gemm_kernel(
     const uint8_t *__restrict__ w, const _Float16 *__restrict__ xh, float *__restrict__ y,
     const _Float16 *__restrict__ xs_hi, const _Float16 *__restrict__ xs_lo, uint32_t M, uint32_t N, uint32_t K,
     uint32_t xcd_remap) {
     constexpr bool Q4 = DT == YULE_DTYPE_Q4_K;
-    constexpr uint32_t BB = Q4 ? 144 : 210;
+    constexpr bool B32 = DT == YULE_DTYPE_Q8_0 || DT == YULE_DTYPE_Q4_0;   // 32-weight blocks, d per block
+    constexpr uint32_t BB = Q4 ? 144 : DT == YULE_DTYPE_Q6_K ? 210 : block32_bytes<DT>();
     constexpr int TM = BM / 32;                 // 16-row MFMA tiles per wave along m
     constexpr uint32_t NTH = 2 * BN;            // threads: two per weight row of the tile
     constexpr uint32_t WNN = BN / 64;           // waves along n (two along m)
@@ -140,7 +157,7 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
     constexpr int GLD = BN == 256 ? 80 : GSK + 8;
     __shared__ __align__(16) _Float16 sx[2][BM * GLD];
     __shared__ __align__(16) _Float16 sw[2][BN * GLD];
-    __shared__ float sd[2][BN];
+    __shared__ float sd[2][B32 ? 2 : 1][BN];   // d per weight row: super-block slot, or the stage's two blocks
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t wm = wave / WNN, wn = wave % WNN;
     // Tile of this workgroup.  The grid is one-dimensional over
@@ -162,7 +179,7 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
     const uint32_t kb_lo = (uint32_t)((uint64_t)bpr * zs / splits);
     const uint32_t kb_hi = (uint32_t)((uint64_t)bpr * (zs + 1) / splits);
     const uint32_t S = 4 * (kb_hi - kb_lo);     // stages of this split (>= 4)
-    const size_t row_bytes = (size_t)bpr * BB;
+    const size_t row_bytes = B32 ? (size_t)(K / 32) * BB : (size_t)bpr * BB;
     if (splits > 1) y += (size_t)zs * M * N;
 
     floatx4 acc[TM][4], tmp[TM][4];
@@ -184,6 +201,15 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
             const uint32_t m = m0 + row < M ? m0 + row : M - 1u;
             R.x[i] = *reinterpret_cast<const uint4 *>(xh + (size_t)m * K + k0 + 8u * c);
         }
+        if constexpr (B32) {
+            // block 2 (kb*4 + st) + part of the row: k = 64 stage + 32 part
+            const uint8_t *blk = wrow + (size_t)(8u * kb + 2u * st + part) * BB;
+            R.mqb = (uint32_t)(reinterpret_cast<uintptr_t>(blk) & 3u);   // 0 or 2: blocks are 2-byte aligned
+            const uint32_t *w4 = reinterpret_cast<const uint32_t *>(blk - R.mqb);
+#pragma unroll
+            for (int i = 0; i < (DT == YULE_DTYPE_Q8_0 ? 10 : 6); i++) R.qb[i] = w4[i];
+            return;
+        }
         const uint8_t *blk = wrow + (size_t)kb * BB;
         if constexpr (Q4) {
             R.h = *reinterpret_cast<const uint4 *>(blk);
@@ -202,7 +228,7 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
 #pragma unroll
         for (int i = 0; i < XCH; i++) {
             const uint32_t idx = tid + NTH * i, row = idx >> 3, c = idx & 7u;
-            if constexpr (Q4) {
+            if constexpr (Q4 || B32) {
                 // rows past M are stored as zeros with a mask: the select
                 // below compiles to branches and register copies around every
                 // stage (10% at M = 512); Q6_K keeps it, its masks spill
@@ -215,7 +241,41 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
         }
         _Float16 *dst = sw[b] + wr * GLD;
         uint4 o[4];
-        if constexpr (Q4) {
+        if constexpr (B32) {
+            // d, then the quants from byte 2 of the block (mqb = 0: the block
+            // starts at raw dword 0; mqb = 2: at its upper half)
+            const bool up = R.mqb != 0;
+            const uint32_t dbits = up ? R.qb[0] >> 16 : R.qb[0] & 0xFFFFu;
+            uint32_t outw[16];
+            if constexpr (DT == YULE_DTYPE_Q8_0) {
+                // signed bytes q[4t..4t+3] -> (q0, q2), (q1, q3): the X order {0,2,1,3}
+#pragma unroll
+                for (int t = 0; t < 8; t++) {
+                    const uint32_t q = up ? R.qb[t + 1] : __builtin_amdgcn_alignbyte(R.qb[t + 1], R.qb[t], 2);
+                    outw[2 * t] = u8pair_to_f16((q & 0x00FF00FFu) ^ 0x00800080u, (_Float16)128.0f);
+                    outw[2 * t + 1] = u8pair_to_f16(((q >> 8) & 0x00FF00FFu) ^ 0x00800080u, (_Float16)128.0f);
+                }
+            } else {
+                // Q4_0 (dequant.rs:77-86): weight 2j is the low nibble of quant
+                // byte j, 2j+1 its high nibble; bytes b0..b3 hold weights
+                // 8t..8t+7 -> (lo b0, lo b1), (hi b0, hi b1), (lo b2, lo b3), (hi b2, hi b3)
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    const uint32_t q = up ? R.qb[t + 1] : __builtin_amdgcn_alignbyte(R.qb[t + 1], R.qb[t], 2);
+                    const uint32_t lo = q & 0x0F0F0F0Fu, hi = (q >> 4) & 0x0F0F0F0Fu;
+                    outw[4 * t] = u8pair_to_f16(__builtin_amdgcn_perm(0u, lo, 0x0C010C00u), (_Float16)8.0f);
+                    outw[4 * t + 1] = u8pair_to_f16(__builtin_amdgcn_perm(0u, hi, 0x0C010C00u), (_Float16)8.0f);
+                    outw[4 * t + 2] = u8pair_to_f16(__builtin_amdgcn_perm(0u, lo, 0x0C030C02u), (_Float16)8.0f);
+                    outw[4 * t + 3] = u8pair_to_f16(__builtin_amdgcn_perm(0u, hi, 0x0C030C02u), (_Float16)8.0f);
+                }
+            }
+            const uint32_t wk = 0u - (uint32_t)wrow_ok;
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+                *reinterpret_cast<uint4 *>(dst + 32u * part + 8u * c) =
+                    make_uint4(outw[4 * c] & wk, outw[4 * c + 1] & wk, outw[4 * c + 2] & wk, outw[4 * c + 3] & wk);
+            sd[b][part][wr] = wrow_ok ? f16_bits(dbits) : 0.f;
+        } else if constexpr (Q4) {
             // 6-bit scales of sub-blocks 2st (low nibbles) and 2st+1 (high),
             // get_scale_min_k4 (dequant.rs:176-190)
             const uint4 hd = R.h;
@@ -251,7 +311,7 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
             *reinterpret_cast<uint4 *>(dst + 16u * part + 8u) = o[1];
             *reinterpret_cast<uint4 *>(dst + 32u + 16u * part) = o[2];
             *reinterpret_cast<uint4 *>(dst + 32u + 16u * part + 8u) = o[3];
-            if (st == 0 && part == 0) sd[kb & 1u][wr] = wrow_ok ? f16_bits(hd.x) * 16384.0f : 0.f;
+            if (st == 0 && part == 0) sd[kb & 1u][0][wr] = wrow_ok ? f16_bits(hd.x) * 16384.0f : 0.f;
         } else {
             // Q6_K (dequant.rs:340-372): k = 32 part + l, quarter g = 2(st&1)+part of half st/2
             uint32_t ql[8], qh[8], scw[1], dw[1];
@@ -282,7 +342,7 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
                                         : make_uint4(0, 0, 0, 0);
                 *reinterpret_cast<uint4 *>(dst + 32u * part + 8u * c) = v;
             }
-            if (st == 0 && part == 0) sd[kb & 1u][wr] = wrow_ok ? f16_bits(dw[0]) : 0.f;
+            if (st == 0 && part == 0) sd[kb & 1u][0][wr] = wrow_ok ? f16_bits(dw[0]) : 0.f;
         }
     };
 
@@ -301,18 +361,33 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
             for (int j = 0; j < 4; j++)
                 bw[j] = *reinterpret_cast<const half8 *>(sw[b] + (wn * 64 + j * 16 + (lane & 15u)) * GLD + ks * 32 +
                                                          8u * (lane >> 4));
+            if constexpr (B32) {
+                // one k-step is one block: acc += d[r][block] * (its MFMA from zero)
 #pragma unroll
-            for (int i = 0; i < TM; i++)
+                for (int i = 0; i < TM; i++)
 #pragma unroll
-                for (int j = 0; j < 4; j++)
-                    tmp[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                        a[i], bw[j], first && ks == 0 ? floatx4{0, 0, 0, 0} : tmp[i][j], 0, 0, 0);
+                    for (int j = 0; j < 4; j++)
+                        tmp[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], bw[j], floatx4{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const float dr = sd[b][ks][wn * 64 + j * 16 + (lane & 15u)];
+#pragma unroll
+                    for (int i = 0; i < TM; i++) acc[i][j] += dr * tmp[i][j];
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        tmp[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            a[i], bw[j], first && ks == 0 ? floatx4{0, 0, 0, 0} : tmp[i][j], 0, 0, 0);
+            }
         }
     };
     auto block_done = [&](uint32_t kb) {   // final += d[r] * super-block partial
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const float dr = sd[kb & 1u][wn * 64 + j * 16 + (lane & 15u)];
+            const float dr = sd[kb & 1u][0][wn * 64 + j * 16 + (lane & 15u)];
 #pragma unroll
             for (int i = 0; i < TM; i++) {
                 acc[i][j] += dr * tmp[i][j];
@@ -358,6 +433,17 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
             block_done(s >> 2);
             dequant_stage(s + 4, R0, 0);
             load_stage(s + 6 < S ? s + 6 : S - 1, R0);
+            __syncthreads();
+        }
+    } else if constexpr (B32) {
+        for (uint32_t s = 0; s < S; s += 2) {
+            compute(0, cont);
+            dequant_stage(s + 1, R1, 1);
+            load_stage(s + 3 < S ? s + 3 : S - 1, R1);
+            __syncthreads();
+            compute(1, cont);
+            dequant_stage(s + 2, R0, 0);
+            load_stage(s + 4 < S ? s + 4 : S - 1, R0);
             __syncthreads();
         }
     } else {
@@ -500,9 +586,9 @@ void launch_gemm(hipStream_t s, const uint8_t *w, const _Float16 *xh, float *y, 
 extern "C" int yule_hip_quantized_gemm(yule_hip_backend *be, yule_buffer weights, yule_buffer x_bf16, yule_buffer y,
                                        uint32_t m, uint32_t n_rows, uint32_t n_cols, uint32_t dtype) {
     if (!be) return set_error(YULE_ERR_INVALID, "null backend");
-    if (dtype != YULE_DTYPE_Q4_K && dtype != YULE_DTYPE_Q6_K)
+    if (dtype != YULE_DTYPE_Q4_K && dtype != YULE_DTYPE_Q6_K && dtype != YULE_DTYPE_Q8_0 && dtype != YULE_DTYPE_Q4_0)
         return set_error(YULE_ERR_UNSUPPORTED, "quantized_gemm: dtype " + std::to_string(dtype) +
-                                                   " not supported (Q4_K and Q6_K)");
+                                                   " not supported (Q4_0, Q4_K, Q6_K, Q8_0)");
     if (n_cols % 256) return set_error(YULE_ERR_INVALID, "quantized_gemm: n_cols must be a multiple of 256");
     uint32_t bs, bb;
     quant_geometry(dtype, &bs, &bb);
@@ -531,12 +617,13 @@ extern "C" int yule_hip_quantized_gemm(yule_hip_backend *be, yule_buffer weights
                        (const uint16_t *)px, xh, xs_hi, xs_lo, m, n_cols);
     if ((rc = check_launch("quantized_gemm: x pre-pass"))) return rc;
     float *out = ks > 1 ? part : (float *)py;
-    if (q4)
-        launch_gemm<YULE_DTYPE_Q4_K>(be->stream, (const uint8_t *)pw, xh, out, xs_hi, xs_lo, m, n_rows, n_cols, ks,
-                                     bn);
-    else
-        launch_gemm<YULE_DTYPE_Q6_K>(be->stream, (const uint8_t *)pw, xh, out, nullptr, nullptr, m, n_rows, n_cols,
-                                     ks, bn);
+    const uint8_t *wq = (const uint8_t *)pw;
+    switch (dtype) {
+    case YULE_DTYPE_Q4_K: launch_gemm<YULE_DTYPE_Q4_K>(be->stream, wq, xh, out, xs_hi, xs_lo, m, n_rows, n_cols, ks, bn); break;
+    case YULE_DTYPE_Q6_K: launch_gemm<YULE_DTYPE_Q6_K>(be->stream, wq, xh, out, nullptr, nullptr, m, n_rows, n_cols, ks, bn); break;
+    case YULE_DTYPE_Q8_0: launch_gemm<YULE_DTYPE_Q8_0>(be->stream, wq, xh, out, nullptr, nullptr, m, n_rows, n_cols, ks, bn); break;
+    default: launch_gemm<YULE_DTYPE_Q4_0>(be->stream, wq, xh, out, nullptr, nullptr, m, n_rows, n_cols, ks, bn); break;
+    }
     if ((rc = check_launch("quantized_gemm"))) return rc;
     if (ks > 1) {
         hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)((n_y + 255) / 256)), dim3(256), 0, be->stream, part,
