@@ -320,21 +320,20 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
             align_raw<4>(R.sc, R.msc, scw);
             align_raw<4>(R.d, R.md, dw);
             const uint32_t g = 2u * (st & 1u) + part, nib = 4u * (st & 1u), qsh = 2u * g;
-            const int sc0 = (int)(int8_t)(scw[0] & 0xFFu), sc1 = (int)(int8_t)((scw[0] >> 8) & 0xFFu);
-            const int perm[4] = {0, 2, 1, 3};
+            const _Float16 sc0 = (_Float16)(float)(int8_t)(scw[0] & 0xFFu);
+            const _Float16 sc1 = (_Float16)(float)(int8_t)((scw[0] >> 8) & 0xFFu);
+            const h2v S0 = {sc0, sc0}, S1 = {sc1, sc1};
             uint32_t outw[16];
+            // four weights per dword: the 6-bit values q (byte lanes), paired
+            // (q0, q2), (q1, q3) in the X order {0,2,1,3}, as f16 q - 32
+            // (exact), times the sub-block scale in f16: the packed multiply
+            // rounds the integer product to nearest even, as converting it does
 #pragma unroll
-            for (int t = 0; t < 16; t++) {   // output dword t = positions 2t, 2t+1
-                uint16_t hv[2];
-#pragma unroll
-                for (int e = 0; e < 2; e++) {
-                    const uint32_t pos = 2 * t + e, l = (pos & ~3u) + perm[pos & 3u];
-                    const uint32_t qlb = (ql[l / 4] >> (8 * (l & 3))) & 0xFFu;
-                    const uint32_t qhb = (qh[l / 4] >> (8 * (l & 3))) & 0xFFu;
-                    const int q = (int)(((qlb >> nib) & 0xFu) | (((qhb >> qsh) & 3u) << 4)) - 32;
-                    hv[e] = __builtin_bit_cast(uint16_t, (_Float16)(float)((l < 16 ? sc0 : sc1) * q));
-                }
-                outw[t] = (uint32_t)hv[0] | ((uint32_t)hv[1] << 16);
+            for (int i = 0; i < 8; i++) {
+                const uint32_t q6 = ((ql[i] >> nib) & 0x0F0F0F0Fu) | (((qh[i] >> qsh) & 0x03030303u) << 4);
+                const h2v sc = i < 4 ? S0 : S1;   // weights 0-15 / 16-31 of the quarter
+                outw[2 * i] = pk_scale(u8pair_to_f16(q6 & 0x00FF00FFu, (_Float16)32.0f), sc);
+                outw[2 * i + 1] = pk_scale(u8pair_to_f16((q6 >> 8) & 0x00FF00FFu, (_Float16)32.0f), sc);
             }
 #pragma unroll
             for (int c = 0; c < 4; c++) {
