@@ -178,8 +178,15 @@ class Runner:
     """TransformerRunner restatement (oracle/runner.c) over a model dict from
     yule_amd.model (tensors by GGUF name)."""
 
+    # formats the reference's CPU vec_dot dispatch handles (simd/scalar.rs:4-22);
+    # a model with any other matrix format cannot run on Yule's CPU path
+    VEC_DOT = (2, 8, 12, 13, 14)   # Q4_0, Q8_0, Q4_K, Q5_K, Q6_K
+
     def __init__(self, model, n_threads: int = 0):
         cfg = model.cfg
+        for name, t in model.tensors.items():
+            if t.data.ndim and name != "token_embd.weight" and t.dtype not in (0, 1) and int(t.dtype) not in self.VEC_DOT:
+                raise ValueError(f"{name}: dtype {int(t.dtype)} has no vec_dot in the reference (scalar.rs:4-22)")
         self._keep = []
         layers = (Layer * cfg.n_layers)()
         for i in range(cfg.n_layers):

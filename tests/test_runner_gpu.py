@@ -49,6 +49,44 @@ def test_runner_logits_match_oracle_small(hip, tiny, fused, split_min, monkeypat
     run.close()
 
 
+@pytest.mark.parametrize("scheme", ["Q4_0", "Q8_0", "Q6_K", "Q5_K", "Q8_K"])
+def test_runner_uniform_formats_match_oracle(hip, scheme):
+    """Models whose every matrix (embedding, projections, lm_head) is one
+    format: per-step logits within the bar, then greedy tokens identical.
+    Q8_K has no vec_dot in the reference (scalar.rs:4-22), so Yule's CPU
+    runner cannot run it; its reference is the f64 forward over the
+    bit-exact dequantized weights."""
+    say(f"[runner] small {scheme} model vs oracle")
+    m = SyntheticModel.generate(TINY_TEST, seed=7, scheme=scheme)
+
+    def reference():
+        return NpForward(m) if scheme == "Q8_K" else oracle.Runner(m, n_threads=4)
+    run = HipRunner(hip, m)
+    try:
+        ref = reference()
+        for t in synth.uniform_tokens(13, 12, m.cfg.vocab):
+            got, want = run.decode_step(int(t)), ref.forward(int(t))
+            assert np.max(np.abs(got - want)) <= tolerance_bar(want)
+    finally:
+        run.close()
+    prompt = synth.uniform_tokens(14, 8, m.cfg.vocab)
+    n_dec = 24
+    run = HipRunner(hip, m)
+    try:
+        toks, _ = run.generate_greedy(prompt, n_dec)
+    finally:
+        run.close()
+    ref = reference()
+    for t in prompt:
+        logits = ref.forward(int(t))
+    want = []
+    for i in range(n_dec + 1):
+        want.append(oracle.argmax(logits))
+        if i < n_dec:
+            logits = ref.forward(want[-1])
+    assert list(toks) == want
+
+
 def test_runner_greedy_matches_oracle_small(hip, tiny):
     say("[runner] small model greedy tokens vs oracle")
     prompt = synth.uniform_tokens(12, 20, tiny.cfg.vocab)
