@@ -426,7 +426,8 @@ def main():
     if not args.quick:
         extra["prefill_gemm_q4k"] = prefill_gemm(hip)
         extra["prefill_gemm_other_formats"] = {
-            dt.name: prefill_gemm(hip, dt, ((14336, 4096),), (512, 2048)) for dt in (DType.Q6_K, DType.Q8_0, DType.Q4_0)}
+            dt.name: prefill_gemm(hip, dt, ((14336, 4096),), (512, 2048))
+            for dt in (DType.Q4_0, DType.Q5_K, DType.Q6_K, DType.Q8_0, DType.Q8_K)}
         for dt in (DType.Q6_K, DType.Q8_0):
             log(f"generating Llama-3-8B {dt.name} layer")
             L = Layer(hip, dt, LLAMA3_LAYER, args.copies, seed=21 + int(dt))

@@ -184,8 +184,9 @@ int yule_hip_argmax(yule_hip_backend *be, yule_buffer in, uint32_t n, yule_buffe
  * token by token, yule-infer/src/model_runner.rs:1075-1081):
  * Y[m][r] = sum_c X[m][c] * W[r][c] for m < M, with X bf16 [M][n_cols]
  * (row-major), W raw GGUF blocks as in quantized_matmul, Y f32 [M][n_rows].
- * Runs on the MFMA units; Q4_0, Q4_K, Q6_K and Q8_0 (other dtypes return
- * YULE_ERR_UNSUPPORTED), n_cols a multiple of 256, M any positive size. */
+ * Runs on the MFMA units; Q4_0, Q4_K, Q5_K, Q6_K, Q8_0 and Q8_K (other
+ * dtypes return YULE_ERR_UNSUPPORTED), n_cols a multiple of 256, M any
+ * positive size. */
 int yule_hip_quantized_gemm(yule_hip_backend *be, yule_buffer weights, yule_buffer x_bf16,
                             yule_buffer y, uint32_t m, uint32_t n_rows, uint32_t n_cols,
                             uint32_t dtype);

@@ -1,4 +1,4 @@
-"""Prefill dequant-GEMM (yule_hip_quantized_gemm, Q4_0 / Q4_K / Q6_K / Q8_0) on
+"""Prefill dequant-GEMM (yule_hip_quantized_gemm, Q4_0 / Q4_K / Q5_K / Q6_K / Q8_0 / Q8_K) on
 the MFMA units: each row
 of Y must equal the quantized matvec of the same row of X to the matvec bar
 (max|y - y_ref| <= 1e-3 * ||y_ref||_2 / sqrt(N), y_ref the f64 dot of the
@@ -40,7 +40,8 @@ def run_gemm(hip, dt, w, xb, M, N, K):
     return y
 
 
-@pytest.mark.parametrize("dt", [DType.Q4_K, DType.Q6_K, DType.Q8_0, DType.Q4_0], ids=lambda d: d.name)
+@pytest.mark.parametrize("dt", [DType.Q4_K, DType.Q6_K, DType.Q8_0, DType.Q4_0, DType.Q5_K, DType.Q8_K],
+                         ids=lambda d: d.name)
 @pytest.mark.parametrize("M,N,K", [(1, 128, 256), (7, 300, 512), (64, 256, 1024), (130, 129, 2048), (65, 200, 5632)])
 def test_gemm_rows_match_oracle(hip, dt, M, N, K):
     say(f"[gemm] {dt.name} M={M} N={N} K={K}")
@@ -78,7 +79,8 @@ def test_gemm_config_shapes(hip, N, K):
 
 @pytest.mark.parametrize("dt,M,N,K", [(DType.Q4_K, 1024, 300, 1024), (DType.Q4_K, 1100, 513, 512),
                                       (DType.Q6_K, 512, 260, 768), (DType.Q6_K, 1030, 129, 256),
-                                      (DType.Q8_0, 1024, 300, 1024), (DType.Q4_0, 1100, 513, 512)],
+                                      (DType.Q8_0, 1024, 300, 1024), (DType.Q4_0, 1100, 513, 512),
+                                      (DType.Q5_K, 1024, 300, 1024), (DType.Q8_K, 1030, 129, 512)],
                          ids=lambda v: getattr(v, "name", str(v)))
 def test_gemm_wide_tiles(hip, dt, M, N, K):
     """M large enough for the 128 x 256 tiles (eight waves), ragged N and M:
@@ -105,7 +107,7 @@ def test_gemm_errors(hip):
     w = synth.gen_quant(DType.Q4_K, 1, 16, 256)
     hw, hx, hy = hip.upload(w), hip.allocate(2 * 256 * 4), hip.allocate(4 * 16 * 4)
     with pytest.raises(YuleGpuError):
-        hip.quantized_gemm(hw, hx, hy, 4, 16, 256, DType.Q5_K)      # not on the MFMA path
+        hip.quantized_gemm(hw, hx, hy, 4, 16, 256, DType.F16)       # not on the MFMA path
     with pytest.raises(YuleGpuError):
         hip.quantized_gemm(hw, hx, hy, 5, 16, 256, DType.Q4_K)      # x too small
     with pytest.raises(YuleGpuError):

@@ -19,6 +19,9 @@
 //  * Q6_K, w = d*sc*(q-32): the B operand is sc*(q-32) (|.| <= 4064; exact
 //    up to 2048, above that rounded to the nearest even integer, i.e.
 //    < 2.5e-4 relative on those few weights), d applied per super-block.
+//  * Q5_K: Q4_K with the fifth bit of each quant ORed in from qh before the
+//    scale multiply (sc*q <= 63*31 = 1953, still exact); same min term.
+//  * Q8_K, w = d*q: the B operand is q (int8, exact), f32 d per super-block.
 //  * Q8_0 / Q4_0, w = d*q and d*(q-8): the B operand is the integer q or
 //    q - 8 (exact in f16, made from 1024 + q with one packed subtract), d
 //    applied per 32-weight block: a 32-k MFMA step is exactly one block, so
@@ -117,7 +120,7 @@ __global__ void gemm_xprep_kernel(const uint16_t *__restrict__ x, _Float16 *__re
 template <uint32_t DT, int XCH>
 struct GemmRegs {
     uint4 x[XCH];
-    uint4 h, q;
+    uint4 h, q, q5h;   // Q4_K / Q5_K: header, 16 quant bytes; Q5_K: the matching 16 qh bytes
     uint32_t ql[9], qh[9], sc[2], d[2];
     uint32_t mql, mqh, msc, md;
     uint32_t qb[10], mqb;   // Q8_0 / Q4_0: the thread's 32-weight block as raw dwords
@@ -144,9 +147,12 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
     const uint8_t *__restrict__ w, const _Float16 *__restrict__ xh, float *__restrict__ y,
     const _Float16 *__restrict__ xs_hi, const _Float16 *__restrict__ xs_lo, uint32_t M, uint32_t N, uint32_t K,
     uint32_t xcd_remap) {
-    constexpr bool Q4 = DT == YULE_DTYPE_Q4_K;
+    constexpr bool Q5 = DT == YULE_DTYPE_Q5_K;
+    constexpr bool Q4 = DT == YULE_DTYPE_Q4_K || Q5;   // Q5_K: Q4_K plus a fifth bit per weight from qh
     constexpr bool B32 = DT == YULE_DTYPE_Q8_0 || DT == YULE_DTYPE_Q4_0;   // 32-weight blocks, d per block
-    constexpr uint32_t BB = Q4 ? 144 : DT == YULE_DTYPE_Q6_K ? 210 : block32_bytes<DT>();
+    constexpr bool Q8K = DT == YULE_DTYPE_Q8_K;   // 256 int8 weights, f32 d per super-block
+    constexpr bool SBP = Q4 || Q8K;                // super-block passes of four stages
+    constexpr uint32_t BB = Q5 ? 176 : Q4 ? 144 : Q8K ? 292 : DT == YULE_DTYPE_Q6_K ? 210 : block32_bytes<DT>();
     constexpr int TM = BM / 32;                 // 16-row MFMA tiles per wave along m
     constexpr uint32_t NTH = 2 * BN;            // threads: two per weight row of the tile
     constexpr uint32_t WNN = BN / 64;           // waves along n (two along m)
@@ -211,7 +217,20 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
             return;
         }
         const uint8_t *blk = wrow + (size_t)kb * BB;
-        if constexpr (Q4) {
+        if constexpr (Q8K) {
+            // Q8_K (dequant.rs:376-384): f32 d at 0, int8 quants at 4 (dword aligned)
+            const uint32_t *w4 = reinterpret_cast<const uint32_t *>(blk);
+            R.d[0] = w4[0];
+#pragma unroll
+            for (int i = 0; i < 8; i++) R.qb[i] = w4[1u + 16u * st + 8u * part + i];
+            return;
+        }
+        if constexpr (Q5) {
+            // Q5_K (dequant.rs:297-338): qh at 16, quants at 48
+            R.h = *reinterpret_cast<const uint4 *>(blk);
+            R.q = *reinterpret_cast<const uint4 *>(blk + 48u + 32u * st + 16u * part);
+            R.q5h = *reinterpret_cast<const uint4 *>(blk + 16u + 16u * part);
+        } else if constexpr (Q4) {
             R.h = *reinterpret_cast<const uint4 *>(blk);
             R.q = *reinterpret_cast<const uint4 *>(blk + 16u + 32u * st + 16u * part);
         } else {
@@ -228,7 +247,7 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
 #pragma unroll
         for (int i = 0; i < XCH; i++) {
             const uint32_t idx = tid + NTH * i, row = idx >> 3, c = idx & 7u;
-            if constexpr (Q4 || B32) {
+            if constexpr (Q4 || B32 || Q8K) {
                 // rows past M are stored as zeros with a mask: the select
                 // below compiles to branches and register copies around every
                 // stage (10% at M = 512); Q6_K keeps it, its masks spill
@@ -241,7 +260,21 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
         }
         _Float16 *dst = sw[b] + wr * GLD;
         uint4 o[4];
-        if constexpr (B32) {
+        if constexpr (Q8K) {
+            uint32_t outw[16];
+#pragma unroll
+            for (int t = 0; t < 8; t++) {   // signed bytes -> (q0, q2), (q1, q3): the X order {0,2,1,3}
+                const uint32_t q = R.qb[t];
+                outw[2 * t] = u8pair_to_f16((q & 0x00FF00FFu) ^ 0x00800080u, (_Float16)128.0f);
+                outw[2 * t + 1] = u8pair_to_f16(((q >> 8) & 0x00FF00FFu) ^ 0x00800080u, (_Float16)128.0f);
+            }
+            const uint32_t wk = 0u - (uint32_t)wrow_ok;
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+                *reinterpret_cast<uint4 *>(dst + 32u * part + 8u * c) =
+                    make_uint4(outw[4 * c] & wk, outw[4 * c + 1] & wk, outw[4 * c + 2] & wk, outw[4 * c + 3] & wk);
+            if (st == 0 && part == 0) sd[kb & 1u][0][wr] = wrow_ok ? __builtin_bit_cast(float, R.d[0]) : 0.f;
+        } else if constexpr (B32) {
             // d, then the quants from byte 2 of the block (mqb = 0: the block
             // starts at raw dword 0; mqb = 2: at its upper half)
             const bool up = R.mqb != 0;
@@ -290,14 +323,26 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
             const _Float16 f1 = (_Float16)(float)((scs >> 8) * 64u);
             const h2v S0 = {f0, f0}, S1 = {f1, f1};
             const uint32_t q[4] = {R.q.x, R.q.y, R.q.z, R.q.w};
+            const uint32_t qb[4] = {R.q5h.x, R.q5h.y, R.q5h.z, R.q5h.w};
             uint32_t lo[8], hi[8];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const uint32_t v = q[i], v8 = v >> 8;
-                lo[2 * i] = pk_scale(v & 0x000F000Fu, S0);
-                lo[2 * i + 1] = pk_scale(v8 & 0x000F000Fu, S0);
-                hi[2 * i] = pk_scale(v & 0x00F000F0u, S1);
-                hi[2 * i + 1] = pk_scale(v8 & 0x00F000F0u, S1);
+                uint32_t l0 = v & 0x000F000Fu, l1 = v8 & 0x000F000Fu, h0 = v & 0x00F000F0u, h1 = v8 & 0x00F000F0u;
+                if constexpr (Q5) {
+                    // fifth bits: qh bit 2st for the low-nibble weights (into bit
+                    // 4 of each half), bit 2st+1 for the high ones (held as 16 q:
+                    // into bit 8); the pairs stay f16 denormals
+                    const uint32_t b = qb[i], b8 = b >> 8;
+                    l0 |= ((b >> (2u * st)) & 0x00010001u) << 4;
+                    l1 |= ((b8 >> (2u * st)) & 0x00010001u) << 4;
+                    h0 |= ((b >> (2u * st + 1u)) & 0x00010001u) << 8;
+                    h1 |= ((b8 >> (2u * st + 1u)) & 0x00010001u) << 8;
+                }
+                lo[2 * i] = pk_scale(l0, S0);
+                lo[2 * i + 1] = pk_scale(l1, S0);
+                hi[2 * i] = pk_scale(h0, S1);
+                hi[2 * i + 1] = pk_scale(h1, S1);
             }
             o[0] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
             o[1] = make_uint4(lo[4], lo[5], lo[6], lo[7]);
@@ -390,7 +435,7 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
 #pragma unroll
             for (int i = 0; i < TM; i++) {
                 acc[i][j] += dr * tmp[i][j];
-                if constexpr (!Q4) tmp[i][j] = floatx4{0, 0, 0, 0};
+                if constexpr (!SBP) tmp[i][j] = floatx4{0, 0, 0, 0};
             }
         }
     };
@@ -401,7 +446,7 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
     dequant_stage(0, R0, 0);
     load_stage(2 < S ? 2 : S - 1, R0);
     __syncthreads();
-    // Q4_K: one super-block (four stages) per pass; stage t computes out of
+    // Q4_K, Q5_K, Q8_K: one super-block (four stages) per pass; stage t computes out of
     // LDS buffer t & 1 while stage t + 1 is dequantized into the other and
     // the bytes of stage t + 3 load into the register set stage t + 1 freed.
     // The pass's first stage starts every tile's partial from zero.  Q6_K,
@@ -414,7 +459,7 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
     // the loop head instead of only for the stage about to be dequantized.
     const std::integral_constant<bool, true> opens{};
     const std::integral_constant<bool, false> cont{};
-    if constexpr (Q4) {
+    if constexpr (SBP) {
         for (uint32_t s = 0; s < S; s += 4) {
             compute(0, opens);
             dequant_stage(s + 1, R1, 1);
@@ -585,9 +630,10 @@ void launch_gemm(hipStream_t s, const uint8_t *w, const _Float16 *xh, float *y, 
 extern "C" int yule_hip_quantized_gemm(yule_hip_backend *be, yule_buffer weights, yule_buffer x_bf16, yule_buffer y,
                                        uint32_t m, uint32_t n_rows, uint32_t n_cols, uint32_t dtype) {
     if (!be) return set_error(YULE_ERR_INVALID, "null backend");
-    if (dtype != YULE_DTYPE_Q4_K && dtype != YULE_DTYPE_Q6_K && dtype != YULE_DTYPE_Q8_0 && dtype != YULE_DTYPE_Q4_0)
+    if (dtype != YULE_DTYPE_Q4_K && dtype != YULE_DTYPE_Q6_K && dtype != YULE_DTYPE_Q8_0 && dtype != YULE_DTYPE_Q4_0 &&
+        dtype != YULE_DTYPE_Q5_K && dtype != YULE_DTYPE_Q8_K)
         return set_error(YULE_ERR_UNSUPPORTED, "quantized_gemm: dtype " + std::to_string(dtype) +
-                                                   " not supported (Q4_0, Q4_K, Q6_K, Q8_0)");
+                                                   " not supported (Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, Q8_K)");
     if (n_cols % 256) return set_error(YULE_ERR_INVALID, "quantized_gemm: n_cols must be a multiple of 256");
     uint32_t bs, bb;
     quant_geometry(dtype, &bs, &bb);
@@ -600,7 +646,7 @@ extern "C" int yule_hip_quantized_gemm(yule_hip_backend *be, yule_buffer weights
     if (x_bf16 == y) return set_error(YULE_ERR_INVALID, "quantized_gemm: x and y alias");
     if (!m || !n_rows) return YULE_OK;
     if (!n_cols) return launch_fill(be->stream, (float *)py, 0.f, (uint64_t)m * n_rows);
-    const bool q4 = dtype == YULE_DTYPE_Q4_K;
+    const bool q4 = dtype == YULE_DTYPE_Q4_K || dtype == YULE_DTYPE_Q5_K;   // min term: X sub-block sums
     const uint32_t bn = gemm_bn(m, dtype), ks = gemm_splits(m, n_rows, n_cols, bn);
     const size_t n_x = (size_t)m * n_cols, n_sub = (size_t)m * (n_cols / 32), n_y = (size_t)m * n_rows;
     const size_t part_bytes = ks > 1 ? ((ks * n_y * sizeof(float) + 255) & ~(size_t)255) : 0;
@@ -620,6 +666,8 @@ extern "C" int yule_hip_quantized_gemm(yule_hip_backend *be, yule_buffer weights
     switch (dtype) {
     case YULE_DTYPE_Q4_K: launch_gemm<YULE_DTYPE_Q4_K>(be->stream, wq, xh, out, xs_hi, xs_lo, m, n_rows, n_cols, ks, bn); break;
     case YULE_DTYPE_Q6_K: launch_gemm<YULE_DTYPE_Q6_K>(be->stream, wq, xh, out, nullptr, nullptr, m, n_rows, n_cols, ks, bn); break;
+    case YULE_DTYPE_Q5_K: launch_gemm<YULE_DTYPE_Q5_K>(be->stream, wq, xh, out, xs_hi, xs_lo, m, n_rows, n_cols, ks, bn); break;
+    case YULE_DTYPE_Q8_K: launch_gemm<YULE_DTYPE_Q8_K>(be->stream, wq, xh, out, nullptr, nullptr, m, n_rows, n_cols, ks, bn); break;
     case YULE_DTYPE_Q8_0: launch_gemm<YULE_DTYPE_Q8_0>(be->stream, wq, xh, out, nullptr, nullptr, m, n_rows, n_cols, ks, bn); break;
     default: launch_gemm<YULE_DTYPE_Q4_0>(be->stream, wq, xh, out, nullptr, nullptr, m, n_rows, n_cols, ks, bn); break;
     }
