@@ -506,43 +506,70 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
 
     if constexpr (Q4) {
         // min term: acc -= sum_j xsum[m][j] * (dmin*mn)[r][j] over the K/32
-        // sub-blocks; a k-step of 32 covers 4 super-blocks, lane quarter q
-        // takes super-block 4*kk + q, i.e. its 8 sub-blocks.
+        // sub-blocks.  In chunks of four super-blocks the workgroup stages
+        // the operands once into the LDS the main loop no longer needs: each
+        // weight row's headers decoded to -(dmin * mn) split into f16 hi + lo
+        // (exact in f32), and each X row's sub-block sums (hi, lo).  A k-step
+        // of 32 then covers the chunk: lane quarter q takes super-block q's
+        // eight sub-blocks, and hi*hi + hi*lo + lo*hi reproduce the product.
+        // Loads come from clamped indices, with out-of-range operands zeroed.
+        // (Per-wave loads and decodes, where both m-waves fetched every header
+        // and all n-waves every X sum, were 1-4% slower; issuing several
+        // chunks' loads at once was 7% slower.)
         const uint32_t nsub = K / 32;
+        _Float16 *mb = &sw[0][0];                 // [BN rows][4 super-blocks][hi 8, lo 8]
+        _Float16 *ma = mb + BN * 64;              // [BM rows][4 super-blocks][hi 8, lo 8]
+        static_assert(BN * 64 + BM * 64 <= 2 * BN * GLD, "min-term staging fits the weight tile buffers");
         for (uint32_t kk = kb_lo; kk < kb_hi; kk += 4) {
-            const uint32_t sbk = kk + (lane >> 4);
+#pragma unroll
+            for (uint32_t it = 0; it < (uint32_t)(BN * 4) / NTH; it++) {
+                const uint32_t idx = tid + NTH * it, row = idx >> 2, sbq = idx & 3u, sb = kk + sbq;
+                const bool ok = r0 + row < N && sb < kb_hi;
+                const uint32_t rc = r0 + row < N ? r0 + row : N - 1u, sbc = sb < kb_hi ? sb : kb_hi - 1u;
+                const uint4 h4 = *reinterpret_cast<const uint4 *>(w + (size_t)rc * row_bytes + (size_t)sbc * BB);
+                const float dmin = f16_bits(h4.x >> 16);
+                const uint32_t hd[3] = {h4.y, h4.z, h4.w};
+                const uint8_t *q = reinterpret_cast<const uint8_t *>(hd);
+                half8 h, l;
+#pragma unroll
+                for (int s = 0; s < 8; s++) {
+                    const uint32_t mn = s < 4 ? (q[s + 4] & 63u)
+                                              : ((uint32_t)(q[s + 4] >> 4) | ((uint32_t)(q[s] >> 6) << 4));
+                    const float v = ok ? -(dmin * (float)mn) : 0.f;
+                    const _Float16 vh = (_Float16)v;
+                    h[s] = vh;
+                    l[s] = (_Float16)(v - (float)vh);
+                }
+                *reinterpret_cast<half8 *>(mb + idx * 16) = h;
+                *reinterpret_cast<half8 *>(mb + idx * 16 + 8) = l;
+            }
+#pragma unroll
+            for (uint32_t it = 0; it < (uint32_t)(BM * 4 + NTH - 1) / NTH; it++) {
+                const uint32_t idx = tid + NTH * it, row = idx >> 2, sbq = idx & 3u, sb = kk + sbq;
+                if (idx < (uint32_t)BM * 4) {
+                    const bool ok = m0 + row < M && sb < kb_hi;
+                    const uint32_t mc = m0 + row < M ? m0 + row : M - 1u, sbc = sb < kb_hi ? sb : kb_hi - 1u;
+                    const half8 xh8 = *reinterpret_cast<const half8 *>(xs_hi + (size_t)mc * nsub + 8 * sbc);
+                    const half8 xl8 = *reinterpret_cast<const half8 *>(xs_lo + (size_t)mc * nsub + 8 * sbc);
+                    const half8 zero = {};
+                    *reinterpret_cast<half8 *>(ma + idx * 16) = ok ? xh8 : zero;
+                    *reinterpret_cast<half8 *>(ma + idx * 16 + 8) = ok ? xl8 : zero;
+                }
+            }
+            __syncthreads();
+            const uint32_t q4 = lane >> 4;
             half8 bh[4], bl[4];
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const uint32_t r = r0 + wn * 64 + j * 16 + (lane & 15u);
-                half8 h = {}, l = {};
-                if (r < N && sbk < kb_hi) {
-                    const uint8_t *blk = w + (size_t)r * row_bytes + (size_t)sbk * BB;
-                    const uint4 h4 = *reinterpret_cast<const uint4 *>(blk);
-                    const float dmin = f16_bits(h4.x >> 16);
-                    const uint32_t hd[3] = {h4.y, h4.z, h4.w};
-                    const uint8_t *q = reinterpret_cast<const uint8_t *>(hd);
-#pragma unroll
-                    for (int s = 0; s < 8; s++) {
-                        const uint32_t mn = s < 4 ? (q[s + 4] & 63u)
-                                                  : ((uint32_t)(q[s + 4] >> 4) | ((uint32_t)(q[s] >> 6) << 4));
-                        const float v = -(dmin * (float)mn);     // exact in f32
-                        const _Float16 vh = (_Float16)v;
-                        h[s] = vh;
-                        l[s] = (_Float16)(v - (float)vh);
-                    }
-                }
-                bh[j] = h;
-                bl[j] = l;
+                const uint32_t nrow = wn * 64 + j * 16 + (lane & 15u);
+                bh[j] = *reinterpret_cast<const half8 *>(mb + (nrow * 4 + q4) * 16);
+                bl[j] = *reinterpret_cast<const half8 *>(mb + (nrow * 4 + q4) * 16 + 8);
             }
 #pragma unroll
             for (int i = 0; i < TM; i++) {
-                const uint32_t m = m0 + wm * (BM / 2) + i * 16 + (lane & 15u);
-                half8 ah = {}, al = {};
-                if (m < M && sbk < kb_hi) {
-                    ah = *reinterpret_cast<const half8 *>(xs_hi + (size_t)m * nsub + 8 * sbk);
-                    al = *reinterpret_cast<const half8 *>(xs_lo + (size_t)m * nsub + 8 * sbk);
-                }
+                const uint32_t mrow = wm * (BM / 2) + i * 16 + (lane & 15u);
+                const half8 ah = *reinterpret_cast<const half8 *>(ma + (mrow * 4 + q4) * 16);
+                const half8 al = *reinterpret_cast<const half8 *>(ma + (mrow * 4 + q4) * 16 + 8);
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh[j], acc[i][j], 0, 0, 0);
@@ -550,6 +577,7 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh[j], acc[i][j], 0, 0, 0);
                 }
             }
+            __syncthreads();   // before the next chunk overwrites the staging
         }
     }
 
