@@ -156,7 +156,12 @@ int yule_hip_device_info(yule_hip_backend *be, yule_device_info *out) {
     YULE_CHECK_BE(be);
     if (!out) return set_error(YULE_ERR_INVALID, "device_info: null out");
     std::memset(out, 0, sizeof(*out));
-    std::snprintf(out->name, sizeof(out->name), "%s (%s)", be->props.name, be->props.gcnArchName);
+    // the runtime's device name can be empty (seen on MI355X); ask the driver, else say "AMD GPU"
+    char name[256] = {0};
+    if (be->props.name[0]) std::snprintf(name, sizeof(name), "%s", be->props.name);
+    else if (hipDeviceGetName(name, sizeof(name), be->device) != hipSuccess || !name[0])
+        std::snprintf(name, sizeof(name), "AMD GPU");
+    std::snprintf(out->name, sizeof(out->name), "%s (%s)", name, be->props.gcnArchName);
     out->backend = 4;
     out->memory_bytes = be->props.totalGlobalMem;
     out->compute_units = (uint32_t)be->props.multiProcessorCount;
