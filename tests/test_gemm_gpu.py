@@ -103,6 +103,36 @@ def test_gemm_wide_tiles(hip, dt, M, N, K):
         hip.free(h)
 
 
+# Shapes whose tile count passes a whole round of resident workgroups (256
+# CUs: one 128 x 256 tile or two 128 x 128 tiles per CU) by at most half a
+# round: the last tiles then run as two K halves added into zeroed y.
+@pytest.mark.parametrize("dt,M,N,K", [(DType.Q4_K, 1024, 8348, 512), (DType.Q4_K, 1100, 7673, 768),
+                                      (DType.Q5_K, 1024, 8348, 512), (DType.Q6_K, 512, 16590, 512),
+                                      (DType.Q8_0, 512, 16512, 512), (DType.Q4_0, 1024, 8348, 512),
+                                      (DType.Q8_K, 1024, 8348, 512)],
+                         ids=lambda v: getattr(v, "name", str(v)))
+def test_gemm_tail_halves(hip, dt, M, N, K):
+    """The last m tiles (where the split tail tiles lie) vs the oracle, every
+    row vs the GPU matvec, and a second call bit-identical to the first."""
+    say(f"[gemm] tail halves {dt.name} M={M} N={N} K={K}")
+    w = synth.gen_quant(dt, 70 + M, N, K)
+    xb = bf16_bits(synth.gauss(71 + K, (M, K)))
+    y = run_gemm(hip, dt, w, xb, M, N, K)
+    assert np.array_equal(y, run_gemm(hip, dt, w, xb, M, N, K)), "second call differs"
+    xf = bf16_to_f32(xb).reshape(M, K)
+    for m in (0, M - 129, M - 128, M - 65, M - 2, M - 1):
+        ref = oracle.qmv_f64(int(dt), w, xf[m], N, K)
+        assert np.max(np.abs(y[m] - ref)) <= tolerance_bar(ref), f"row {m}"
+    hw, hx, hy = hip.upload(w), hip.allocate(4 * K), hip.allocate(4 * N)
+    for m in range(M):
+        hip.copy_to_device(xf[m], hx)
+        hip.quantized_matmul(hw, hx, hy, N, K, dt)
+        mv = hip.download(hy, N)
+        assert np.max(np.abs(y[m] - mv)) <= 2 * tolerance_bar(mv), f"row {m} vs matvec"
+    for h in (hw, hx, hy):
+        hip.free(h)
+
+
 def test_gemm_errors(hip):
     w = synth.gen_quant(DType.Q4_K, 1, 16, 256)
     hw, hx, hy = hip.upload(w), hip.allocate(2 * 256 * 4), hip.allocate(4 * 16 * 4)

@@ -146,7 +146,7 @@ template <uint32_t DT, int BM, int BN>
 __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YULE_DTYPE_Q6_K ? 1 : 2))) void gemm_kernel(
     const uint8_t *__restrict__ w, const _Float16 *__restrict__ xh, float *__restrict__ y,
     const _Float16 *__restrict__ xs_hi, const _Float16 *__restrict__ xs_lo, uint32_t M, uint32_t N, uint32_t K,
-    uint32_t xcd_remap) {
+    uint32_t xcd_remap, uint32_t tail) {
     constexpr bool Q5 = DT == YULE_DTYPE_Q5_K;
     constexpr bool Q4 = DT == YULE_DTYPE_Q4_K || Q5;   // Q5_K: Q4_K plus a fifth bit per weight from qh
     constexpr bool B32 = DT == YULE_DTYPE_Q8_0 || DT == YULE_DTYPE_Q4_0;   // 32-weight blocks, d per block
@@ -167,26 +167,41 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t wm = wave / WNN, wn = wave % WNN;
     // Tile of this workgroup.  The grid is one-dimensional over
-    // (split, m tile, n tile), n fastest; workgroups are dispatched to the
-    // eight XCDs round-robin by id, so ids are remapped to give each XCD a
-    // contiguous range of tiles: the workgroups resident on one XCD then
-    // share one m tile, whose X rows stay in that XCD's L2 instead of being
-    // re-read from the last-level cache by every n tile.
+    // (split, m tile, n tile), n fastest, in id order: workgroups go to the
+    // eight XCDs round-robin by id, so the ones resident together at any
+    // time cover a few whole m tiles across all XCDs.  xcd_remap instead
+    // gives each XCD a contiguous range of ids (its workgroups then share
+    // one m tile's X rows in its L2); that measured 2-10% slower on every
+    // format at M = 1024 and 2048 and is off unless YULE_GEMM_XCD_REMAP=1.
     const uint32_t nt = (N + BN - 1) / BN, mt = (M + BM - 1) / BM, tiles = nt * mt;
-    const uint32_t splits = gridDim.x / tiles;
-    uint32_t t = blockIdx.x;
-    if (xcd_remap) {
-        const uint32_t q = gridDim.x / 8u, rmd = gridDim.x % 8u, xcd = t % 8u;
-        t = xcd * q + (xcd < rmd ? xcd : rmd) + t / 8u;
+    // With tail > 0 the grid is instead the first tiles - tail tiles whole,
+    // then the last `tail` tiles as two K halves each, dispatched last: the
+    // last round of resident workgroups then runs half as long.  Both
+    // halves add into y, which the host zeroed: 0 + a + b is exact in
+    // either order.
+    const uint32_t whole = tiles - tail;
+    const bool halves = tail && blockIdx.x >= whole;
+    const uint32_t splits = tail ? (halves ? 2u : 1u) : gridDim.x / tiles;
+    const uint32_t span = tail ? whole : gridDim.x;
+    uint32_t t = blockIdx.x, zs;
+    if (halves) {
+        zs = (t - whole) & 1u;
+        t = whole + ((t - whole) >> 1);
+    } else {
+        if (xcd_remap) {
+            const uint32_t q = span / 8u, rmd = span % 8u, xcd = t % 8u;
+            t = xcd * q + (xcd < rmd ? xcd : rmd) + t / 8u;
+        }
+        zs = t / tiles;
     }
-    const uint32_t zs = t / tiles, tm = (t % tiles) / nt, tn = t % nt;
+    const uint32_t tm = (t % tiles) / nt, tn = t % nt;
     const uint32_t m0 = tm * BM, r0 = tn * BN;
     const uint32_t bpr = K / 256;
     const uint32_t kb_lo = (uint32_t)((uint64_t)bpr * zs / splits);
     const uint32_t kb_hi = (uint32_t)((uint64_t)bpr * (zs + 1) / splits);
     const uint32_t S = 4 * (kb_hi - kb_lo);     // stages of this split (>= 4)
     const size_t row_bytes = B32 ? (size_t)(K / 32) * BB : (size_t)bpr * BB;
-    if (splits > 1) y += (size_t)zs * M * N;
+    if (splits > 1 && !tail) y += (size_t)zs * M * N;
 
     floatx4 acc[TM][4], tmp[TM][4];
 #pragma unroll
@@ -590,9 +605,22 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const uint32_t m = m0 + wm * (BM / 2) + i * 16 + 4 * (lane >> 4) + e;
-                if (m < M && r < N) y[(size_t)m * N + r] = acc[i][j][e];
+                if (m < M && r < N) {
+                    if (halves) unsafeAtomicAdd(y + (size_t)m * N + r, acc[i][j][e]);
+                    else y[(size_t)m * N + r] = acc[i][j][e];
+                }
             }
         }
+}
+
+// zeroes the y blocks of tiles [first, first + gridDim.x / bm): one block per tile row
+__global__ void gemm_zero_tiles_kernel(float *__restrict__ y, uint32_t M, uint32_t N, uint32_t first, uint32_t nt,
+                                       uint32_t bm, uint32_t bn) {
+    const uint32_t t = first + blockIdx.x / bm, m = (t / nt) * bm + blockIdx.x % bm;
+    for (uint32_t c = threadIdx.x; c < bn; c += blockDim.x) {
+        const uint32_t r = (t % nt) * bn + c;
+        if (m < M && r < N) y[(size_t)m * N + r] = 0.f;
+    }
 }
 
 // y[i] = sum over z of part[z][i], z ascending
@@ -633,25 +661,48 @@ uint32_t gemm_splits(uint32_t m, uint32_t n, uint32_t k, uint32_t bn) {
     return ks < 1 ? 1 : ks > bpr ? bpr : ks;
 }
 
+// Tail tiles split in two K halves (zero: none).  Without splits, the tiles
+// past the last whole round of resident workgroups (one 256-wide or two
+// 128-wide per CU) form a partial round nearly as long as a full one (a
+// workgroup there ran 86-97% of its full-round time); when they fill at
+// most half a round, running them as K halves fills it and ends the
+// launch earlier (5% on 14336 x 4096 at M = 2048).  Needs two super-blocks
+// per row.  YULE_GEMM_TAIL=0 turns it off.
+uint32_t gemm_tail(uint32_t m, uint32_t n, uint32_t k, uint32_t bn, uint32_t ks) {
+    static const bool env = env_flag("YULE_GEMM_TAIL", true);
+    if (!env || ks > 1 || k / 256 < 2) return 0;
+    const uint32_t bm = m <= 64 ? 64 : 128;
+    const uint32_t tiles = ((n + bn - 1) / bn) * ((m + bm - 1) / bm);
+    const uint32_t round = (uint32_t)device_cus() * (bn == 256 ? 1u : 2u);
+    if (tiles <= round) return 0;
+    const uint32_t r = tiles % round;
+    return r <= round / 2 ? r : 0;
+}
+
 template <uint32_t DT, int BN>
 void launch_gemm_bn(hipStream_t s, const uint8_t *w, const _Float16 *xh, float *y, const _Float16 *xs_hi,
-                    const _Float16 *xs_lo, uint32_t m, uint32_t n, uint32_t k, uint32_t ks) {
-    static const uint32_t remap = (uint32_t)env_int("YULE_GEMM_XCD_REMAP", 1);
+                    const _Float16 *xs_lo, uint32_t m, uint32_t n, uint32_t k, uint32_t ks, uint32_t tail) {
+    static const uint32_t remap = env_flag("YULE_GEMM_XCD_REMAP", false) ? 1u : 0u;
     const uint32_t nt = (n + BN - 1) / BN;
+    const uint32_t bm = m <= 64 ? 64 : 128, tiles = nt * ((m + bm - 1) / bm);
+    const uint32_t grid = tail ? tiles + tail : tiles * ks;
+    if (tail)
+        hipLaunchKernelGGL(gemm_zero_tiles_kernel, dim3(tail * bm), dim3(256), 0, s, y, m, n, tiles - tail, nt, bm,
+                           (uint32_t)BN);
     if (m <= 64) {
-        hipLaunchKernelGGL((gemm_kernel<DT, 64, BN>), dim3(nt * ((m + 63) / 64) * ks), dim3(2 * BN), 0, s, w, xh, y,
-                           xs_hi, xs_lo, m, n, k, remap);
+        hipLaunchKernelGGL((gemm_kernel<DT, 64, BN>), dim3(grid), dim3(2 * BN), 0, s, w, xh, y, xs_hi, xs_lo, m, n, k,
+                           remap, tail);
     } else {
-        hipLaunchKernelGGL((gemm_kernel<DT, 128, BN>), dim3(nt * ((m + 127) / 128) * ks), dim3(2 * BN), 0, s, w, xh,
-                           y, xs_hi, xs_lo, m, n, k, remap);
+        hipLaunchKernelGGL((gemm_kernel<DT, 128, BN>), dim3(grid), dim3(2 * BN), 0, s, w, xh, y, xs_hi, xs_lo, m, n,
+                           k, remap, tail);
     }
 }
 
 template <uint32_t DT>
 void launch_gemm(hipStream_t s, const uint8_t *w, const _Float16 *xh, float *y, const _Float16 *xs_hi,
-                 const _Float16 *xs_lo, uint32_t m, uint32_t n, uint32_t k, uint32_t ks, uint32_t bn) {
-    if (bn == 256) launch_gemm_bn<DT, 256>(s, w, xh, y, xs_hi, xs_lo, m, n, k, ks);
-    else launch_gemm_bn<DT, 128>(s, w, xh, y, xs_hi, xs_lo, m, n, k, ks);
+                 const _Float16 *xs_lo, uint32_t m, uint32_t n, uint32_t k, uint32_t ks, uint32_t bn, uint32_t tail) {
+    if (bn == 256) launch_gemm_bn<DT, 256>(s, w, xh, y, xs_hi, xs_lo, m, n, k, ks, tail);
+    else launch_gemm_bn<DT, 128>(s, w, xh, y, xs_hi, xs_lo, m, n, k, ks, tail);
 }
 }  // namespace
 
@@ -676,6 +727,7 @@ extern "C" int yule_hip_quantized_gemm(yule_hip_backend *be, yule_buffer weights
     if (!n_cols) return launch_fill(be->stream, (float *)py, 0.f, (uint64_t)m * n_rows);
     const bool q4 = dtype == YULE_DTYPE_Q4_K || dtype == YULE_DTYPE_Q5_K;   // min term: X sub-block sums
     const uint32_t bn = gemm_bn(m, dtype), ks = gemm_splits(m, n_rows, n_cols, bn);
+    const uint32_t tail = gemm_tail(m, n_rows, n_cols, bn, ks);
     const size_t n_x = (size_t)m * n_cols, n_sub = (size_t)m * (n_cols / 32), n_y = (size_t)m * n_rows;
     const size_t part_bytes = ks > 1 ? ((ks * n_y * sizeof(float) + 255) & ~(size_t)255) : 0;
     const size_t need = part_bytes + (n_x + (q4 ? 2 * n_sub : 0)) * sizeof(_Float16) + 256;
@@ -692,12 +744,12 @@ extern "C" int yule_hip_quantized_gemm(yule_hip_backend *be, yule_buffer weights
     float *out = ks > 1 ? part : (float *)py;
     const uint8_t *wq = (const uint8_t *)pw;
     switch (dtype) {
-    case YULE_DTYPE_Q4_K: launch_gemm<YULE_DTYPE_Q4_K>(be->stream, wq, xh, out, xs_hi, xs_lo, m, n_rows, n_cols, ks, bn); break;
-    case YULE_DTYPE_Q6_K: launch_gemm<YULE_DTYPE_Q6_K>(be->stream, wq, xh, out, nullptr, nullptr, m, n_rows, n_cols, ks, bn); break;
-    case YULE_DTYPE_Q5_K: launch_gemm<YULE_DTYPE_Q5_K>(be->stream, wq, xh, out, xs_hi, xs_lo, m, n_rows, n_cols, ks, bn); break;
-    case YULE_DTYPE_Q8_K: launch_gemm<YULE_DTYPE_Q8_K>(be->stream, wq, xh, out, nullptr, nullptr, m, n_rows, n_cols, ks, bn); break;
-    case YULE_DTYPE_Q8_0: launch_gemm<YULE_DTYPE_Q8_0>(be->stream, wq, xh, out, nullptr, nullptr, m, n_rows, n_cols, ks, bn); break;
-    default: launch_gemm<YULE_DTYPE_Q4_0>(be->stream, wq, xh, out, nullptr, nullptr, m, n_rows, n_cols, ks, bn); break;
+    case YULE_DTYPE_Q4_K: launch_gemm<YULE_DTYPE_Q4_K>(be->stream, wq, xh, out, xs_hi, xs_lo, m, n_rows, n_cols, ks, bn, tail); break;
+    case YULE_DTYPE_Q6_K: launch_gemm<YULE_DTYPE_Q6_K>(be->stream, wq, xh, out, nullptr, nullptr, m, n_rows, n_cols, ks, bn, tail); break;
+    case YULE_DTYPE_Q5_K: launch_gemm<YULE_DTYPE_Q5_K>(be->stream, wq, xh, out, xs_hi, xs_lo, m, n_rows, n_cols, ks, bn, tail); break;
+    case YULE_DTYPE_Q8_K: launch_gemm<YULE_DTYPE_Q8_K>(be->stream, wq, xh, out, nullptr, nullptr, m, n_rows, n_cols, ks, bn, tail); break;
+    case YULE_DTYPE_Q8_0: launch_gemm<YULE_DTYPE_Q8_0>(be->stream, wq, xh, out, nullptr, nullptr, m, n_rows, n_cols, ks, bn, tail); break;
+    default: launch_gemm<YULE_DTYPE_Q4_0>(be->stream, wq, xh, out, nullptr, nullptr, m, n_rows, n_cols, ks, bn, tail); break;
     }
     if ((rc = check_launch("quantized_gemm"))) return rc;
     if (ks > 1) {

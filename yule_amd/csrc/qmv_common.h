@@ -49,6 +49,12 @@ static inline int env_int(const char *name, int dflt) {
     return v > 0 ? v : dflt;
 }
 
+// on/off switch: unset gives dflt, any set value other than 0 turns it on
+static inline bool env_flag(const char *name, bool dflt) {
+    const char *e = getenv(name);
+    return e ? atoi(e) != 0 : dflt;
+}
+
 // LDS per CU on gfx950
 constexpr size_t kLdsPerCu = 160 * 1024;
 
