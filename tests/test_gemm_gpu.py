@@ -105,11 +105,13 @@ def test_gemm_wide_tiles(hip, dt, M, N, K):
 
 # Shapes whose tile count passes a whole round of resident workgroups (256
 # CUs: one 128 x 256 tile or two 128 x 128 tiles per CU) by at most half a
-# round: the last tiles then run as two K halves added into zeroed y.
+# round: the last tiles then run as two K halves added into zeroed y.  The
+# last two cases take the 64-row tiles (M <= 64) with lm_head-like widths.
 @pytest.mark.parametrize("dt,M,N,K", [(DType.Q4_K, 1024, 8348, 512), (DType.Q4_K, 1100, 7673, 768),
                                       (DType.Q5_K, 1024, 8348, 512), (DType.Q6_K, 512, 16590, 512),
                                       (DType.Q8_0, 512, 16512, 512), (DType.Q4_0, 1024, 8348, 512),
-                                      (DType.Q8_K, 1024, 8348, 512)],
+                                      (DType.Q8_K, 1024, 8348, 512), (DType.Q4_K, 40, 66000, 512),
+                                      (DType.Q6_K, 64, 65800, 768)],
                          ids=lambda v: getattr(v, "name", str(v)))
 def test_gemm_tail_halves(hip, dt, M, N, K):
     """The last m tiles (where the split tail tiles lie) vs the oracle, every
@@ -120,7 +122,7 @@ def test_gemm_tail_halves(hip, dt, M, N, K):
     y = run_gemm(hip, dt, w, xb, M, N, K)
     assert np.array_equal(y, run_gemm(hip, dt, w, xb, M, N, K)), "second call differs"
     xf = bf16_to_f32(xb).reshape(M, K)
-    for m in (0, M - 129, M - 128, M - 65, M - 2, M - 1):
+    for m in sorted({0, max(M - 129, 0), max(M - 128, 0), max(M - 65, 0), M - 2, M - 1}):
         ref = oracle.qmv_f64(int(dt), w, xf[m], N, K)
         assert np.max(np.abs(y[m] - ref)) <= tolerance_bar(ref), f"row {m}"
     hw, hx, hy = hip.upload(w), hip.allocate(4 * K), hip.allocate(4 * N)
