@@ -313,10 +313,11 @@ def profile_dominant(hip, n, copies):
                       "calibration_copy_bytes": 64 << 20}), flush=True)
 
 
-def profile_gemm(hip, n):
-    """N launches of the Q4_K 14336x4096 prefill GEMM at M = 2048 (BASELINE
-    configs[3]), for rocprofv3 kernel-trace and MFMA counter runs."""
-    M, n_rows, n_cols = 2048, 14336, 4096
+def profile_gemm(hip, n, M=2048):
+    """N launches of the Q4_K 14336x4096 prefill GEMM at M tokens (BASELINE
+    M in {64, 512, 2048}), for rocprofv3 kernel-trace and MFMA
+    counter runs."""
+    n_rows, n_cols = 14336, 4096
     w = hip.upload(synth.gen_quant(DType.Q4_K, 81, n_rows, n_cols))
     xb = (synth.gauss(82, (M, n_cols)).view(np.uint32) >> 16).astype(np.uint16)
     hx, hy = hip.upload(xb), hip.allocate(4 * M * n_rows)
@@ -356,7 +357,9 @@ def main():
                     help="only run N launches of the dominant kernel (Q4_K 14336x4096 over rotating copies) and "
                          "one 64 MiB device copy, for rocprofv3 --pmc runs; prints a JSON line")
     ap.add_argument("--profile-gemm", type=int, default=0, metavar="N",
-                    help="only run N calls of the Q4_K 14336x4096 prefill GEMM at M=2048 (for rocprofv3)")
+                    help="only run N calls of the Q4_K 14336x4096 prefill GEMM (for rocprofv3)")
+    ap.add_argument("--gemm-m", type=int, default=2048, choices=(64, 512, 2048),
+                    help="tokens M of the --profile-gemm calls (default 2048)")
     ap.add_argument("--profile-decode", type=int, default=0, metavar="N",
                     help="only run N TinyLlama decode steps with kernels launched one by one (for rocprofv3)")
     args = ap.parse_args()
@@ -374,7 +377,7 @@ def main():
         profile_dominant(hip, args.profile_dominant, args.copies)
         return
     if args.profile_gemm:
-        profile_gemm(hip, args.profile_gemm)
+        profile_gemm(hip, args.profile_gemm, args.gemm_m)
         return
     if args.profile_decode:
         profile_decode(hip, args.profile_decode)

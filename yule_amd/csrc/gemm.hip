@@ -613,13 +613,17 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
         }
 }
 
-// zeroes the y blocks of tiles [first, first + gridDim.x / bm): one block per tile row
+// zeroes the y blocks of tiles [first, first + gridDim.x / (bm / 8)): one
+// workgroup per 8 rows of a tile, 32 lanes per row storing consecutive
+// floats (bm is 64 or 128, bn 128 or 256)
 __global__ void gemm_zero_tiles_kernel(float *__restrict__ y, uint32_t M, uint32_t N, uint32_t first, uint32_t nt,
                                        uint32_t bm, uint32_t bn) {
-    const uint32_t t = first + blockIdx.x / bm, m = (t / nt) * bm + blockIdx.x % bm;
-    for (uint32_t c = threadIdx.x; c < bn; c += blockDim.x) {
+    const uint32_t per_tile = bm / 8, t = first + blockIdx.x / per_tile;
+    const uint32_t m = (t / nt) * bm + (blockIdx.x % per_tile) * 8 + threadIdx.x / 32;
+    if (m >= M) return;
+    for (uint32_t c = threadIdx.x % 32; c < bn; c += 32) {
         const uint32_t r = (t % nt) * bn + c;
-        if (m < M && r < N) y[(size_t)m * N + r] = 0.f;
+        if (r < N) y[(size_t)m * N + r] = 0.f;
     }
 }
 
@@ -687,8 +691,8 @@ void launch_gemm_bn(hipStream_t s, const uint8_t *w, const _Float16 *xh, float *
     const uint32_t bm = m <= 64 ? 64 : 128, tiles = nt * ((m + bm - 1) / bm);
     const uint32_t grid = tail ? tiles + tail : tiles * ks;
     if (tail)
-        hipLaunchKernelGGL(gemm_zero_tiles_kernel, dim3(tail * bm), dim3(256), 0, s, y, m, n, tiles - tail, nt, bm,
-                           (uint32_t)BN);
+        hipLaunchKernelGGL(gemm_zero_tiles_kernel, dim3(tail * (bm / 8)), dim3(256), 0, s, y, m, n, tiles - tail, nt,
+                           bm, (uint32_t)BN);
     if (m <= 64) {
         hipLaunchKernelGGL((gemm_kernel<DT, 64, BN>), dim3(grid), dim3(2 * BN), 0, s, w, xh, y, xs_hi, xs_lo, m, n, k,
                            remap, tail);
