@@ -103,6 +103,24 @@ def test_gemm_wide_tiles(hip, dt, M, N, K):
         hip.free(h)
 
 
+@pytest.mark.parametrize("N,K", [(14336, 4096), (4096, 14336)])
+def test_gemm_config_shapes_m2048(hip, N, K):
+    """BASELINE configs[3] at M=2048: 14336x4096 is 896 tiles of 128 x 256,
+    so its last 128 tiles (m rows 1664-2047, from n 10240 at row 1664 on)
+    run as K halves; 4096x14336 is one whole round.  Rows in both kinds of
+    tile vs the oracle, and a repeat call bit-identical."""
+    dt, M = DType.Q4_K, 2048
+    say(f"[gemm] Q4_K {N}x{K} M={M}")
+    w = synth.gen_quant(dt, 72, N, K)
+    xb = bf16_bits(synth.gauss(73, (M, K)))
+    y = run_gemm(hip, dt, w, xb, M, N, K)
+    assert np.array_equal(y, run_gemm(hip, dt, w, xb, M, N, K)), "second call differs"
+    xf = bf16_to_f32(xb).reshape(M, K)
+    for m in (0, 1663, 1664, 1800, 2047):
+        ref = oracle.qmv_f64(int(dt), w, xf[m], N, K)
+        assert np.max(np.abs(y[m] - ref)) <= tolerance_bar(ref), f"row {m}"
+
+
 # Shapes whose tile count passes a whole round of resident workgroups (256
 # CUs: one 128 x 256 tile or two 128 x 128 tiles per CU) by at most half a
 # round: the last tiles then run as two K halves added into zeroed y.  The
