@@ -403,7 +403,7 @@ def main():
     dom_bytes = algo_bytes(DType.Q4_K, 14336, 4096)
     roofline = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(),
-                "kernel": "qmv_stream_kernel<Q4K,64,2,256> 14336x4096", "avg_launch_us": round(us, 3),
+                "kernel": "qmv_stream_kernel<Q4K,64,2,512> 14336x4096", "avg_launch_us": round(us, 3),
                 "algo_bytes_per_launch": dom_bytes}
     log(f"dominant kernel Q4_K 14336x4096: {us:.2f} us/launch, {gbs:.1f} GB/s")
     roofline["read_probe"] = read_probe(hip, q4k, "ffn_gate", n_dom)

@@ -737,8 +737,11 @@ static void launch_stream_nt(hipStream_t s, const Segs &sg, const float *x, uint
 
 template <class F, int W>
 static void launch_stream(hipStream_t s, const Segs &sg, const float *x, uint32_t bpr, const QmvXf &xf) {
+    // one-wave teams (the 4096-column projections) measured ~1% faster in
+    // 512-thread workgroups; narrower teams (2048 columns) 6% slower there
     static const int nt_narrow = env_int("YULE_QMV_THREADS", 256), nt_wide = env_int("YULE_QMV_THREADS_WIDE", 1024);
-    const int nt = W >= 512 ? 1024 : W >= 128 ? nt_wide : nt_narrow;
+    static const int nt_w64 = env_int("YULE_QMV_THREADS_W64", 512);
+    const int nt = W >= 512 ? 1024 : W >= 128 ? nt_wide : W == 64 ? nt_w64 : nt_narrow;
     if (nt >= 1024) return launch_stream_nt<F, W, 1024>(s, sg, x, bpr, xf);
     if constexpr (W >= 512) return;   // unreachable: 512-lane teams only run in 1024-thread workgroups
     else
