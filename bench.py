@@ -110,6 +110,7 @@ class Layer:
 
 
 USE_GRAPH = True
+DOM_COPIES = 32   # copies of the dominant matrix cycled by its roofline measurement
 
 
 def time_steps(hip, layer, steps, start=0, fused=True):
@@ -185,7 +186,7 @@ def cpu_baseline(layer, budget_s=12.0, max_passes=2000):
                 "sample": f"{passes} passes of the Q4_K Llama-3-8B layer (7 projections, "
                           f"{layer.step_bytes / 1e6:.1f} MB each pass) through the oracle's restatement of Yule's "
                           f"AVX2 qmv with a per-call std::thread row split, {threads} threads, {dt:.1f} s",
-                "host_cpu": _cpu_model()}
+                "host_cpu": host_cpu_record(threads)}
     port, _, _ = _time_qmv_layer(layer, threads, budget_s / 2, max_passes)
     oracle.set_q4k_dot(asm)
     try:
@@ -197,7 +198,7 @@ def cpu_baseline(layer, budget_s=12.0, max_passes=2000):
                       f"{layer.step_bytes / 1e6:.1f} MB each pass): the reference's q4k_gemv_avx2.S (assembled from "
                       f"its sources into oracle/_ref) for every block, inside the restatement of model_runner.rs "
                       f"qmv's per-call std::thread row split, {threads} threads, {dt:.1f} s",
-            "port_value": round(port, 3), "host_cpu": _cpu_model()}
+            "port_value": round(port, 3), "host_cpu": host_cpu_record(threads)}
 
 
 def decode_e2e(hip, cpu: bool):
@@ -227,11 +228,16 @@ def decode_e2e(hip, cpu: bool):
         if asm is not None:
             oracle.set_q4k_dot(asm)
         try:
+            # the GPU figure's workload: the 128-token prompt (untimed), then
+            # greedy decode steps from position 128 on, as many as fit ~12 s
             r = oracle.Runner(model, n_threads=threads)
-            r.forward(int(prompt[0]))
+            t0 = time.perf_counter()
+            for t in prompt:
+                logits = r.forward(int(t))
+            pre_s = time.perf_counter() - t0
             n, t0 = 0, time.perf_counter()
-            while n < 4 or (n < 48 and time.perf_counter() - t0 < 12.0):
-                r.forward(int(prompt[(n + 1) % 128]))
+            while n < 4 or (n < 256 and time.perf_counter() - t0 < 12.0):
+                logits = r.forward(oracle.argmax(logits))
                 n += 1
             cms = 1e3 * (time.perf_counter() - t0) / n
         finally:
@@ -240,8 +246,12 @@ def decode_e2e(hip, cpu: bool):
                 else "the Rust-fallback restatement of the AVX2 Q4_K body")
         res["cpu_decode"] = {"tok_s": round(1000.0 / cms, 2), "threads": threads,
                              "kind": "reference" if asm is not None else "port",
-                             "sample": f"{n} forward steps at positions 1..{n} of the same model through the "
-                                       f"oracle's restatement of Yule's CPU TransformerRunner with {what}"}
+                             "prompt_tok_s": round(len(prompt) / pre_s, 2),
+                             "sample": f"the same 128-token prompt (token by token, untimed in tok_s), then {n} "
+                                       f"greedy decode steps at positions 128..{127 + n} (the GPU run decodes "
+                                       f"128..383), through the oracle's restatement of Yule's CPU "
+                                       f"TransformerRunner with {what}",
+                             "host_cpu": host_cpu_record(threads)}
         res["decode_speedup_vs_cpu"] = round(cms / ms, 1)
     return res
 
@@ -286,6 +296,54 @@ def _cpu_model():
     return "unknown"
 
 
+def host_cpu_record(threads_used: int) -> dict:
+    """The host the CPU baseline ran on: model, logical CPUs the process may
+    use, physical cores behind them (distinct core ids per package), SMT
+    state, and the threads the baseline used."""
+    logical = sorted(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else list(range(os.cpu_count() or 1))
+    cores = set()
+    for c in logical:
+        try:
+            pkg = open(f"/sys/devices/system/cpu/cpu{c}/topology/physical_package_id").read().strip()
+            core = open(f"/sys/devices/system/cpu/cpu{c}/topology/core_id").read().strip()
+            cores.add((pkg, core))
+        except OSError:
+            cores.add(("?", str(c)))
+    try:
+        smt = open("/sys/devices/system/cpu/smt/active").read().strip() == "1"
+    except OSError:
+        smt = None
+    fam = {}
+    try:
+        for line in open("/proc/cpuinfo"):
+            k, _, v = line.partition(":")
+            k = k.strip()
+            if k in ("vendor_id", "cpu family", "model", "stepping") and k not in fam:
+                fam[k] = v.strip()
+            if not line.strip():
+                break
+    except OSError:
+        pass
+    return {"model": _cpu_model(), "cpuid": fam, "logical_cpus_available": len(logical), "physical_cores_available": len(cores),
+            "smt_active": smt, "threads_used": threads_used, "machine_logical_cpus": os.cpu_count()}
+
+
+def dominant_kernel_name():
+    """The kernel the library launches for a Q4_K 14336x4096 matvec under the
+    current environment (the switches qmv.hip reads: YULE_QMV_V1 selects the
+    column-looping kernel, YULE_QMV_THREADS_W64 the workgroup size of one-wave
+    teams; non-positive or unparsable values keep the default)."""
+    if os.environ.get("YULE_QMV_V1") is not None:
+        return "qmv_kernel<Q4K,64,*>"
+    try:
+        nt = int(os.environ.get("YULE_QMV_THREADS_W64", "512"))
+    except ValueError:
+        nt = 512
+    nt = nt if nt > 0 else 512
+    nt = 1024 if nt >= 1024 else 512 if nt >= 512 else 256
+    return f"qmv_stream_kernel<Q4K,64,2,{nt}>"
+
+
 def traffic_from_profiles():
     """HBM bytes per launch of the dominant kernel from the committed rocprofv3
     --pmc summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel factor)."""
@@ -303,7 +361,7 @@ def profile_dominant(hip, n, copies):
     the Q4_K 14336x4096 matvec (kernel launches, no graph) cycling `copies`
     weight copies, then one 64 MiB buffer copy whose counters calibrate the
     bytes-per-KiB scale of FETCH_SIZE / WRITE_SIZE."""
-    L = Layer(hip, DType.Q4_K, [("ffn_gate", 14336, 4096)], copies, seed=11)
+    L = Layer(hip, DType.Q4_K, [("ffn_gate", 14336, 4096)], max(copies, DOM_COPIES), seed=11)
     ms = hip.time_qmv_ops(L.ops_for_matrix("ffn_gate", n), 1, use_graph=False)
     src, dst = hip.allocate(64 << 20), hip.allocate(64 << 20)
     hip.copy_buffer(src, dst, 64 << 20)
@@ -311,6 +369,39 @@ def profile_dominant(hip, n, copies):
     print(json.dumps({"launches": n, "us_per_launch": round(1e3 * ms / n, 3),
                       "algo_bytes_per_launch": algo_bytes(DType.Q4_K, 14336, 4096),
                       "calibration_copy_bytes": 64 << 20}), flush=True)
+
+
+def probe_curve(hip, sizes_mb=(33, 128, 256, 558, 1024), n_wgs=(1024, 2048, 4096, 8192)):
+    """Single-launch streaming-read rate against launch size: yule_hip_read_probe
+    over rotating buffers totalling >= 2 GiB (beyond the 256 MB last-level
+    cache), median of the per-launch rates of 5 timed passes.  Prints one JSON line."""
+    out = {}
+    for mb in sizes_mb:
+        nbytes = (mb * 1000 * 1000) // 4096 * 4096
+        copies = max(2, -(-(2 << 30) // nbytes))
+        bufs = [hip.allocate(nbytes) for _ in range(copies)]
+        row = {}
+        for n_wg in n_wgs:
+            part = hip.allocate(4 * n_wg)
+            launches = max(2 * copies, min(2000, int(4e9 // nbytes)))
+            for i in range(copies):
+                hip.read_probe(bufs[i], nbytes, part, n_wg)
+            rates = []
+            for _ in range(5):
+                hip.timer_start()
+                for i in range(launches):
+                    hip.read_probe(bufs[i % copies], nbytes, part, n_wg)
+                us = hip.timer_stop() * 1e3 / launches
+                rates.append(nbytes / (us * 1e-6) / 1e9)
+            hip.free(part)
+            g = float(np.median(rates))
+            row[str(n_wg)] = {"us": round(nbytes / (g * 1e9) * 1e6, 3), "GB/s": round(g, 1)}
+            log(f"read probe {mb} MB, {n_wg} workgroups: {row[str(n_wg)]['us']} us, {g:.1f} GB/s")
+        for b in bufs:
+            hip.free(b)
+        out[f"{mb}MB"] = row
+    print(json.dumps({"read_probe_curve": out, "launch": "yule_hip_read_probe, 256-thread workgroups, "
+                      "back-to-back stream launches over rotating buffers, HIP events"}), flush=True)
 
 
 def profile_gemm(hip, n, M=2048):
@@ -360,6 +451,8 @@ def main():
                     help="only run N calls of the Q4_K 14336x4096 prefill GEMM (for rocprofv3)")
     ap.add_argument("--gemm-m", type=int, default=2048, choices=(64, 512, 2048),
                     help="tokens M of the --profile-gemm calls (default 2048)")
+    ap.add_argument("--probe-curve", action="store_true",
+                    help="only measure the single-launch streaming-read rate against launch size (JSON line)")
     ap.add_argument("--profile-decode", type=int, default=0, metavar="N",
                     help="only run N TinyLlama decode steps with kernels launched one by one (for rocprofv3)")
     args = ap.parse_args()
@@ -375,6 +468,9 @@ def main():
     info = hip.device_info()
     if args.profile_dominant:
         profile_dominant(hip, args.profile_dominant, args.copies)
+        return
+    if args.probe_curve:
+        probe_curve(hip)
         return
     if args.profile_gemm:
         profile_gemm(hip, args.profile_gemm, args.gemm_m)
@@ -397,21 +493,35 @@ def main():
     value7 = q4k.step_bytes * args.steps / (ms7 * 1e-3) / 1e9
     log(f"Q4_K layer as 7 separate calls: {value7:.1f} GB/s")
 
-    # dominant kernel: Q4_K 14336x4096 (gate/up), average launch duration
+    # dominant kernel: Q4_K 14336x4096 (gate/up), average launch duration over
+    # DOM_COPIES distinct copies (1.06 GB, four times the 256 MB last-level
+    # cache, so no launch finds its weights cached)
     n_dom = 1000
-    us, gbs = matrix_rate(hip, q4k, "ffn_gate", n_dom)
+    dom = Layer(hip, DType.Q4_K, [("ffn_gate", 14336, 4096)], DOM_COPIES, seed=11)
+    us, gbs = matrix_rate(hip, dom, "ffn_gate", n_dom)
     dom_bytes = algo_bytes(DType.Q4_K, 14336, 4096)
     roofline = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(),
-                "kernel": "qmv_stream_kernel<Q4K,64,2,512> 14336x4096", "avg_launch_us": round(us, 3),
+                "kernel": f"{dominant_kernel_name()} 14336x4096", "avg_launch_us": round(us, 3),
                 "algo_bytes_per_launch": dom_bytes}
     log(f"dominant kernel Q4_K 14336x4096: {us:.2f} us/launch, {gbs:.1f} GB/s")
-    roofline["read_probe"] = read_probe(hip, q4k, "ffn_gate", n_dom)
+    roofline["read_probe"] = read_probe(hip, dom, "ffn_gate", n_dom)
+    roofline["weight_copies"] = DOM_COPIES
+    dom.free()
     roofline["frac_of_read_probe"] = round(gbs / roofline["read_probe"]["GB/s"], 4)
     log(f"read probe over the same weight copies: {roofline['read_probe']['us']:.2f} us/launch, "
         f"{roofline['read_probe']['GB/s']:.1f} GB/s")
 
-    extra = {"layer_as_7_calls_GB/s": round(value7, 1), "per_matrix_q4k": {}}
+    # fixed cost of the step's kernel boundaries: the same number of empty
+    # kernels per step, replayed from one graph like the timed steps
+    n_launch = len(q4k.ops_for_step(0))
+    hip.time_empty_launches(n_launch * min(args.steps, 64), 1, use_graph=USE_GRAPH)        # warm-up
+    empty_ms = hip.time_empty_launches(n_launch * args.steps, 1, use_graph=USE_GRAPH)   # one graph, as the steps
+    launch_us = 1e3 * empty_ms / args.steps
+    extra = {"layer_as_7_calls_GB/s": round(value7, 1), "per_matrix_q4k": {},
+             "launch_overhead": {"empty_kernels_per_step": n_launch, "us_per_step": round(launch_us, 3),
+                                 "value_without_it_GB/s": round(q4k.step_bytes / ((ms_per_step * 1e3 - launch_us) * 1e-6) / 1e9, 1)}}
+    log(f"empty-kernel step ({n_launch} launches): {launch_us:.2f} us")
     for name, r, c in LLAMA3_LAYER:
         u, g = matrix_rate(hip, q4k, name, 400)
         extra["per_matrix_q4k"][f"{name} {r}x{c}"] = {"us": round(u, 2), "GB/s": round(g, 1)}

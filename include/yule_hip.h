@@ -320,6 +320,15 @@ int yule_hip_time_qmv_ops(yule_hip_backend *be, const yule_qmv_op *ops, uint32_t
 int yule_hip_read_probe(yule_hip_backend *be, yule_buffer src, uint64_t bytes, yule_buffer partials,
                         uint32_t n_partials);
 
+/* Launch-overhead probe: n_kernels launches of an empty kernel (one
+ * workgroup of 64 threads that returns at once), run `iters` times, captured
+ * into one HIP graph when use_graph != 0; writes the elapsed milliseconds
+ * between HIP events on the backend stream around all iterations.  It
+ * measures the fixed cost of a kernel boundary that every launch of a
+ * decode step pays.  No reference counterpart. */
+int yule_hip_time_empty_launches(yule_hip_backend *be, uint32_t n_kernels, uint32_t iters, int use_graph,
+                                 float *ms_total);
+
 /* Event timer on the backend stream: timer_start records a start event;
  * timer_stop records a stop event after everything enqueued since, waits
  * for it and writes the elapsed milliseconds. */

@@ -54,17 +54,18 @@ def test_gemm_rows_match_oracle(hip, dt, M, N, K):
         assert np.max(np.abs(y[m] - ref)) <= tolerance_bar(ref), f"row {m}"
 
 
+@pytest.mark.parametrize("M", [64, 512])
 @pytest.mark.parametrize("N,K", [(14336, 4096), (4096, 14336)])
-def test_gemm_config_shapes(hip, N, K):
-    """BASELINE configs[3] shapes at M=64, sampled rows vs the oracle; the
-    remaining rows against the GPU matvec of the same rows."""
-    dt, M = DType.Q4_K, 64
+def test_gemm_config_shapes(hip, N, K, M):
+    """BASELINE configs[3] shapes at M = 64 and 512, sampled rows vs the
+    oracle; every seventh row against the GPU matvec of the same row."""
+    dt = DType.Q4_K
     say(f"[gemm] Q4_K {N}x{K} M={M}")
     w = synth.gen_quant(dt, 70, N, K)
     xb = bf16_bits(synth.gauss(71, (M, K)))
     y = run_gemm(hip, dt, w, xb, M, N, K)
     xf = bf16_to_f32(xb).reshape(M, K)
-    for m in (0, 17, 63):
+    for m in (0, 17, 63, M - 1):
         ref = oracle.qmv_f64(int(dt), w, xf[m], N, K)
         assert np.max(np.abs(y[m] - ref)) <= tolerance_bar(ref), f"row {m}"
     hw, hx, hy = hip.upload(w), hip.allocate(4 * K), hip.allocate(4 * N)
@@ -162,5 +163,9 @@ def test_gemm_errors(hip):
         hip.quantized_gemm(hw, hx, hy, 5, 16, 256, DType.Q4_K)      # x too small
     with pytest.raises(YuleGpuError):
         hip.quantized_gemm(hw, hx, hx, 1, 16, 256, DType.Q4_K)      # x aliases y
+    with pytest.raises(YuleGpuError):
+        hip.quantized_gemm(hw, hx, hw, 1, 16, 256, DType.Q4_K)      # weights alias y
+    with pytest.raises(YuleGpuError):
+        hip.quantized_gemm(hw, hw, hy, 1, 16, 256, DType.Q4_K)      # weights alias x
     for h in (hw, hx, hy):
         hip.free(h)

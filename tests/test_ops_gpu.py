@@ -220,6 +220,22 @@ def test_argmax_kats(hip):
     hip.argmax(h, 32000, out)
     assert int(hip.download(out, 1, np.uint32)[0]) == oracle.argmax(v)
     hip.free(h)
+    # ties between infinities: argmax_ct's sign test keeps the first (inf - inf
+    # is a negative NaN on x86), equal finite maxima go to the last; the oracle
+    # runs the reference's scan
+    inf = np.inf
+    cases = [[inf, 1.0, inf], [-inf] * 5, [1.0, inf, 2.0, inf], [-inf, 3.0, 3.0], [2.0, -inf],
+             [-inf, -inf, 0.5, -inf], [inf] * 4000]
+    big = np.full(5000, -inf, np.float32)
+    big[[17, 2500, 4999]] = inf
+    cases.append(big)
+    for vals in cases:
+        a = f32(vals)
+        want = oracle.argmax(a)
+        h = hip.upload(a)
+        hip.argmax(h, len(a), out)
+        assert int(hip.download(out, 1, np.uint32)[0]) == want, vals
+        hip.free(h)
     hip.free(out)
 
 

@@ -305,6 +305,19 @@ def test_argmax_kats():
     assert oracle.argmax(v) == int(np.argmax(v))
 
 
+def test_argmax_infinite_ties():
+    """argmax_ct's test is the sign bit of (v - best) (sampler.rs:142-148).
+    inf - inf is the IEEE default NaN, which x86 produces with the sign bit
+    set, so an equal infinity never replaces the best: the first of several
+    +inf wins, and an all -inf input stays at index 0."""
+    inf = np.inf
+    nan = np.float32(inf) - np.float32(inf)
+    assert np.signbit(nan)          # the x86 default NaN this rule rests on
+    for vals, want in (([inf, 1.0, inf], 0), ([-inf] * 5, 0), ([1.0, inf, 2.0, inf], 1),
+                       ([-inf, 3.0, 3.0], 2), ([2.0, -inf], 0), ([-inf, -inf, 0.5, -inf], 2)):
+        assert oracle.argmax(np.array(vals, np.float32)) == want, vals
+
+
 def test_rope_table_kats():
     c, s = oracle.rope_table(8, 4, 10000.0)
     assert np.all(c[:2] == 1.0) and np.all(s[:2] == 0.0)

@@ -160,6 +160,33 @@ def test_qmv_rows_independent_and_linear(hip):
     assert np.array_equal(gpu_qmv(hip, dt, sub, x1, len(rows), n_cols), y1[rows])
 
 
+# BASELINE configs[2] (Llama-3-8B: FFN and the 128256-row lm_head, in each
+# of the layer formats) and configs[1]'s Q6_K lm_head, at full size.
+FULL = [(dt, 14336, 4096) for dt in (DType.Q6_K, DType.Q8_0)] + \
+       [(dt, 4096, 14336) for dt in (DType.Q4_K, DType.Q6_K, DType.Q8_0)] + \
+       [(dt, 128256, 4096) for dt in (DType.Q4_K, DType.Q6_K, DType.Q8_0)] + [(DType.Q6_K, 32000, 2048)]
+
+
+@pytest.mark.parametrize("dt,n_rows,n_cols", FULL, ids=lambda v: getattr(v, "name", str(v)))
+def test_qmv_config_shapes_full_size(hip, dt, n_rows, n_cols):
+    """The whole matrix on the GPU; 512 seeded rows (first and last included)
+    against the oracle's f64 dot of the same rows; and those rows run alone
+    give bit-identical outputs (each row depends only on its own weights)."""
+    say(f"[qmv] full size {dt.name} {n_rows}x{n_cols}")
+    bs, bb = oracle.GEOM[int(dt)]
+    row_bytes = n_cols // bs * bb
+    w = synth.gen_quant(dt, 300 + int(dt), n_rows, n_cols)
+    x = synth.gauss(301, n_cols)
+    y = gpu_qmv(hip, dt, w, x, n_rows, n_cols)
+    rows = np.unique(np.concatenate([[0, n_rows - 1],
+                                     np.random.default_rng(n_rows).integers(0, n_rows, 510)]))
+    sub = np.concatenate([w[r * row_bytes:(r + 1) * row_bytes] for r in rows])
+    ref = oracle.qmv_f64(int(dt), sub, x, len(rows), n_cols)
+    assert np.max(np.abs(y[rows] - ref)) <= tolerance_bar(ref)
+    assert np.array_equal(gpu_qmv(hip, dt, sub, x, len(rows), n_cols), y[rows])
+    assert np.all(np.isfinite(y))
+
+
 def test_qmv_edge_cases_and_errors(hip):
     say("[qmv] edge cases")
     dt = DType.Q4_K
@@ -180,6 +207,10 @@ def test_qmv_edge_cases_and_errors(hip):
         hip.quantized_matmul(hw, hx, hy, 5, 256, dt)  # weights too small
     with pytest.raises(YuleGpuError):
         hip.quantized_matmul(hw, hx, hx, 1, 256, dt)  # input aliases output
+    with pytest.raises(YuleGpuError):
+        hip.quantized_matmul(hw, hx, hw, 1, 256, dt)  # weights alias the output
+    with pytest.raises(YuleGpuError):
+        hip.quantized_matmul(hw, hw, hy, 1, 256, dt)  # weights alias the input
     with pytest.raises(YuleGpuError):
         hip.quantized_matmul(hw, hx, 999999, 4, 256, dt)  # unknown handle
     for h in (hw, hx, hy):

@@ -4,6 +4,7 @@ greedy tokens identical — on a small model live, and on the TinyLlama-shaped
 Q4_K_M model against the committed golden stream."""
 import json
 import sys
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -104,6 +105,21 @@ def test_runner_greedy_matches_oracle_small(hip, tiny):
     assert list(toks) == want
     assert ms > 0
     run.close()
+
+
+@pytest.mark.parametrize("threads_w64", ["256", "512"])
+def test_runner_wide_rows_fused_variants(hip, threads_w64):
+    """4096-wide rows: every fused matvec variant on one-wave teams, in both
+    workgroup sizes the launcher can pick for them (tests/runner_wide_check.py,
+    in a child process because the size is read once per process)."""
+    import os
+    import subprocess
+    say(f"[runner] 4096-wide model, one-wave teams in {threads_w64}-thread workgroups")
+    env = dict(os.environ, YULE_QMV_THREADS_W64=threads_w64)
+    r = subprocess.run([sys.executable, str(Path(__file__).with_name("runner_wide_check.py"))], env=env,
+                       capture_output=True, text=True, timeout=110)
+    assert r.returncode == 0 and r.stdout.startswith("ok"), r.stdout[-2000:] + r.stderr[-4000:]
+    say(f"[runner] {r.stdout.strip()}")
 
 
 def test_runner_prefill_determinism_reset_and_limits(hip, tiny):

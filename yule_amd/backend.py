@@ -74,6 +74,7 @@ _SIGS: dict[str, tuple] = {
     "yule_hip_runner_create_from_gguf": (C.c_int, [C.c_void_p, C.c_char_p, C.c_uint32, C.POINTER(C.c_void_p)]),
     "yule_hip_read_probe": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint32]),
     "yule_hip_timer_start": (C.c_int, [C.c_void_p]),
+    "yule_hip_time_empty_launches": (C.c_int, [C.c_void_p, C.c_uint32, C.c_uint32, C.c_int, C.POINTER(C.c_float)]),
     "yule_hip_timer_stop": (C.c_int, [C.c_void_p, C.POINTER(C.c_float)]),
     "yule_hip_time_qmv_ops": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_int,
                                         C.POINTER(C.c_float)]),
@@ -296,6 +297,14 @@ class HipBackend:
         arr = (QmvOp * len(ops))(*[mk(op) for op in ops])
         ms = C.c_float()
         self._check(self._lib.yule_hip_time_qmv_ops(self._be, arr, len(ops), iters, int(use_graph), C.byref(ms)))
+        return ms.value
+
+    def time_empty_launches(self, n_kernels: int, iters: int, use_graph: bool = True) -> float:
+        """Milliseconds for `iters` runs of n_kernels empty-kernel launches (one
+        graph replay each when use_graph), HIP events on the backend stream."""
+        ms = C.c_float()
+        self._check(self._lib.yule_hip_time_empty_launches(self._be, n_kernels, iters, int(use_graph),
+                                                          C.byref(ms)))
         return ms.value
 
     def timer_start(self) -> None:

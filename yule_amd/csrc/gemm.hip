@@ -727,6 +727,8 @@ extern "C" int yule_hip_quantized_gemm(yule_hip_backend *be, yule_buffer weights
         (rc = get_buffer(be, y, (size_t)m * n_rows * 4, &py, "quantized_gemm (y)")))
         return rc;
     if (x_bf16 == y) return set_error(YULE_ERR_INVALID, "quantized_gemm: x and y alias");
+    if (weights == y || weights == x_bf16)
+        return set_error(YULE_ERR_INVALID, "quantized_gemm: weights alias x or y");
     if (!m || !n_rows) return YULE_OK;
     if (!n_cols) return launch_fill(be->stream, (float *)py, 0.f, (uint64_t)m * n_rows);
     const bool q4 = dtype == YULE_DTYPE_Q4_K || dtype == YULE_DTYPE_Q5_K;   // min term: X sub-block sums

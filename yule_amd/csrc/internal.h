@@ -110,6 +110,8 @@ int launch_dequant(hipStream_t stream, uint32_t dtype, const uint8_t *src, float
 // table; the token is read on the device so the launch can sit in a graph
 int launch_embed_rows(hipStream_t stream, uint32_t dtype, const uint8_t *table, const uint32_t *token,
                       uint32_t n_rows, float *dst, uint32_t dim);
+// one launch of an empty kernel (launch-overhead probe)
+int launch_empty(hipStream_t stream);
 // out[i] = value for i < n
 int launch_fill(hipStream_t stream, float *out, float value, uint64_t n);
 // out[i] = i < n ? x[i] : 0 for i < n_out (a row staged zero-padded)

@@ -8,6 +8,7 @@
 
 #include "blocks.h"
 #include "internal.h"
+#include "qmv_common.h"
 
 namespace yule {
 
@@ -229,9 +230,14 @@ constexpr uint32_t kMaxHeadDim = 256;
 constexpr uint64_t kAttnMaxKvDim = 1u << 17;
 
 // ------------------------------------------------------------ argmax
-// argmax_ct (sampler.rs:150-163): the last maximal index wins.
+// argmax_ct (sampler.rs:142-163): an element replaces the best when the
+// sign bit of (v - best) is clear.  For equal finite values that is +0, so the
+// last maximal index wins; for equal infinities inf - inf is the default NaN,
+// sign bit set on x86, so the first one stays (an all -inf input gives 0).
+// NaN logits are outside this rule (the sequential scan is then not a
+// maximum over any order).
 __device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t bi) {
-    return v > bv || (v == bv && i > bi);
+    return v > bv || (v == bv && (__builtin_isinf(v) ? i < bi : i > bi));
 }
 
 __global__ __launch_bounds__(1024) void argmax_kernel(const float *__restrict__ in, uint32_t n,
@@ -287,6 +293,15 @@ __global__ __launch_bounds__(256) void read_probe_kernel(const uint4 *__restrict
     __syncthreads();
     if (threadIdx.x == 0) part[blockIdx.x] = red[0] ^ red[1] ^ red[2] ^ red[3];
 }
+
+namespace yule {
+__global__ __launch_bounds__(64) void empty_kernel() {}
+
+int launch_empty(hipStream_t s) {
+    hipLaunchKernelGGL(empty_kernel, dim3(1), dim3(64), 0, s);
+    return check_launch("empty kernel");
+}
+}  // namespace yule
 
 #define BE_OR_FAIL(be) \
     if (!(be)) return set_error(YULE_ERR_INVALID, "null backend")
@@ -1111,7 +1126,7 @@ __global__ __launch_bounds__(1024) void advance_kernel(const unsigned long long 
     __syncthreads();
     if (threadIdx.x == 0) {
         for (int w = 1; w < 16; w++) b = wbest[w] > b ? wbest[w] : b;
-        const uint32_t tok = (uint32_t)(b & 0xFFFFFFFFull), pos = ctl[0];
+        const uint32_t tok = argmax_row(b), pos = ctl[0];
         ctl[1] = tok;
         out_tokens[pos] = tok;
         ctl[0] = pos + 1;

@@ -556,7 +556,7 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const Segs sg, const flo
         if (xf.epi == kEpiAdd) v = yb[row] + v;   // residual + projection (model_runner.rs:782-784)
         yb[row] = v;
         if (xf.epi == kEpiArgmax) {
-            const unsigned long long key = ((unsigned long long)argmax_key(v) << 32) | row;
+            const unsigned long long key = argmax_pack(v, row);
             best = key > best ? key : best;
         }
     };

@@ -21,6 +21,22 @@ __device__ __forceinline__ uint32_t argmax_key(float v) {
     const uint32_t u = __builtin_bit_cast(uint32_t, v);
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
+// Keys of +inf and -inf.  argmax_ct's test is the sign of (v - best): equal
+// finite values give +0 and the later index wins, but inf - inf is the
+// default NaN, whose sign bit is set on x86, so among equal infinities the
+// first index stays.  The packed key therefore carries ~row for infinite
+// values (the first of them is the largest) and row otherwise.
+constexpr uint32_t kKeyPosInf = 0xFF800000u, kKeyNegInf = 0x007FFFFFu;
+__device__ __forceinline__ unsigned long long argmax_pack(float v, uint32_t row) {
+    const uint32_t k = argmax_key(v);
+    const bool inf = k == kKeyPosInf || k == kKeyNegInf;
+    return ((unsigned long long)k << 32) | (inf ? ~row : row);
+}
+// the row of a packed key
+__device__ __forceinline__ uint32_t argmax_row(unsigned long long key) {
+    const uint32_t k = (uint32_t)(key >> 32), lo = (uint32_t)(key & 0xFFFFFFFFull);
+    return k == kKeyPosInf || k == kKeyNegInf ? ~lo : lo;
+}
 
 // Up to kMaxSegs matrices sharing one activation vector (same n_cols and
 // format) run as one launch over their concatenated rows: Q/K/V, gate/up.

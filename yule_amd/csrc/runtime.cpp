@@ -272,6 +272,9 @@ static int check_qmv_args(yule_hip_backend *be, yule_buffer weights, yule_buffer
         return set_error(YULE_ERR_UNSUPPORTED,
                          std::string(what) + ": dtype " + std::to_string(dtype) + " not supported on this backend");
     if (input == output) return set_error(YULE_ERR_INVALID, std::string(what) + ": input and output alias");
+    // kernels of other workgroups still read the weights while y is written
+    if (weights == output || weights == input)
+        return set_error(YULE_ERR_INVALID, std::string(what) + ": weights alias the input or the output");
     void *pw, *px, *py;
     int rc;
     // ceil(n_cols / bs) blocks per row, as the reference's GPU backends
@@ -403,6 +406,48 @@ int yule_hip_time_qmv_ops(yule_hip_backend *be, const yule_qmv_op *ops, uint32_t
     auto enqueue = [&]() -> int {
         for (const Launch &l : L) {
             int rc = launch_qmv_multi(be->stream, l.dtype, l.segs, l.n, l.x, l.n_cols);
+            if (rc) return rc;
+        }
+        return YULE_OK;
+    };
+    int rc = YULE_OK;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    if (use_graph) {
+        if ((rc = hip_error(hipStreamBeginCapture(be->stream, hipStreamCaptureModeThreadLocal), "begin capture")))
+            return rc;
+        int erc = enqueue();
+        rc = hip_error(hipStreamEndCapture(be->stream, &graph), "end capture");
+        if (erc) rc = erc;
+        if (!rc) rc = hip_error(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0), "graph instantiate");
+        if (!rc) rc = hip_error(hipGraphLaunch(exec, be->stream), "graph warm-up launch");
+    }
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (!rc) rc = hip_error(hipEventCreate(&e0), "hipEventCreate");
+    if (!rc) rc = hip_error(hipEventCreate(&e1), "hipEventCreate");
+    if (!rc) rc = hip_error(hipEventRecord(e0, be->stream), "hipEventRecord");
+    for (uint32_t it = 0; it < iters && !rc; it++)
+        rc = use_graph ? hip_error(hipGraphLaunch(exec, be->stream), "graph launch") : enqueue();
+    if (!rc) rc = hip_error(hipEventRecord(e1, be->stream), "hipEventRecord");
+    if (!rc) rc = hip_error(hipEventSynchronize(e1), "hipEventSynchronize");
+    float ms = 0.f;
+    if (!rc) rc = hip_error(hipEventElapsedTime(&ms, e0, e1), "hipEventElapsedTime");
+    if (e0) hipEventDestroy(e0);
+    if (e1) hipEventDestroy(e1);
+    if (exec) hipGraphExecDestroy(exec);
+    if (graph) hipGraphDestroy(graph);
+    if (!rc) *ms_total = ms;
+    return rc;
+}
+
+int yule_hip_time_empty_launches(yule_hip_backend *be, uint32_t n_kernels, uint32_t iters, int use_graph,
+                                 float *ms_total) {
+    YULE_CHECK_BE(be);
+    if (!ms_total || n_kernels == 0 || n_kernels > 100000 || iters == 0)
+        return set_error(YULE_ERR_INVALID, "time_empty_launches: bad arguments");
+    auto enqueue = [&]() -> int {
+        for (uint32_t i = 0; i < n_kernels; i++) {
+            int rc = launch_empty(be->stream);
             if (rc) return rc;
         }
         return YULE_OK;
