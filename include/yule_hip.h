@@ -186,10 +186,25 @@ int yule_hip_argmax(yule_hip_backend *be, yule_buffer in, uint32_t n, yule_buffe
  * (row-major), W raw GGUF blocks as in quantized_matmul, Y f32 [M][n_rows].
  * Runs on the MFMA units; Q4_0, Q4_K, Q5_K, Q6_K, Q8_0 and Q8_K (other
  * dtypes return YULE_ERR_UNSUPPORTED), n_cols a multiple of 256, M any
- * positive size. */
+ * positive size.  Any finite bf16 row is accepted: each row is scaled by a
+ * power of two into f16 range for the matrix cores and the scale is undone
+ * exactly on Y (rows holding inf or NaN give inf/NaN outputs, as the f32 sum
+ * would).  Each row of Y meets the matvec bar against the f32 matvec of the
+ * same (bf16-valued) row.  Weights aliasing x or y are rejected. */
 int yule_hip_quantized_gemm(yule_hip_backend *be, yule_buffer weights, yule_buffer x_bf16,
                             yule_buffer y, uint32_t m, uint32_t n_rows, uint32_t n_cols,
                             uint32_t dtype);
+
+/* The same product for f32 X [M][n_cols] (no counterpart in the reference):
+ * each row is split into f16 hi + lo after its power-of-two scale
+ * (x = hi + lo to ~2^-22) and Y = X_hi W + X_lo W, two MFMA products, so
+ * each row matches the f32 matvec of the same row to the matvec bar at f32
+ * accuracy (the batched prefill of the runner, whose KV cache must equal
+ * token-by-token decode's).  Same formats, shapes, aliasing rules and
+ * workspace use as yule_hip_quantized_gemm. */
+int yule_hip_quantized_gemm_f32(yule_hip_backend *be, yule_buffer weights, yule_buffer x_f32,
+                                yule_buffer y, uint32_t m, uint32_t n_rows, uint32_t n_cols,
+                                uint32_t dtype);
 
 /* ---- decode runner (yule-infer GpuTransformerRunner counterpart) ---- */
 

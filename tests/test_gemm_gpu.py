@@ -154,6 +154,100 @@ def test_gemm_tail_halves(hip, dt, M, N, K):
         hip.free(h)
 
 
+ALL_GEMM = [DType.Q4_K, DType.Q6_K, DType.Q8_0, DType.Q4_0, DType.Q5_K, DType.Q8_K]
+
+
+def range_rows(K: int) -> np.ndarray:
+    """Rows that leave f16's range or precision unscaled: magnitudes 1e5 and
+    1e36, 1e-7 and 1e-30, a row of 2100s (sub-block sums of 67200 > 65504),
+    a row of small values holding two 3e38 elements, zeros, and N(0,1)."""
+    g = np.random.default_rng(K)
+    n = lambda: g.standard_normal(K)
+    big = 1e-3 * n()
+    big[[5, K - 7]] = 3e38
+    rows = [1e5 * n(), 1e36 * n(), 1e-7 * n(), 1e-30 * n(), np.full(K, 2100.0), big, np.zeros(K), n()]
+    return np.array(rows, np.float32)
+
+
+@pytest.mark.parametrize("dt", ALL_GEMM, ids=lambda d: d.name)
+@pytest.mark.parametrize("M", [8, 136])
+def test_gemm_bf16_full_range(hip, dt, M):
+    """Any finite bf16 row: each row against the oracle's f64 dot of the same
+    bf16-valued row (the per-row power-of-two scale is exact)."""
+    N, K = 160, 1024
+    say(f"[gemm] bf16 range rows {dt.name} M={M}")
+    w = synth.gen_quant(dt, 95, N, K)
+    base = range_rows(K)
+    xb = bf16_bits(np.concatenate([base] * (M // len(base)) + [base[:M % len(base)]]))
+    y = run_gemm(hip, dt, w, xb, M, N, K)
+    xf = bf16_to_f32(xb).reshape(M, K)
+    for m in range(M):
+        ref = oracle.qmv_f64(int(dt), w, xf[m], N, K)
+        if not np.any(xf[m]):
+            assert np.all(y[m] == 0.0), f"row {m}"
+            continue
+        assert np.all(np.isfinite(y[m])), f"row {m}"
+        assert np.max(np.abs(y[m] - ref)) <= tolerance_bar(ref), f"row {m}"
+
+
+def run_gemm_f32(hip, dt, w, x, M, N, K):
+    hw, hx, hy = hip.upload(w), hip.upload(np.ascontiguousarray(x, np.float32)), hip.allocate(4 * M * N)
+    hip.quantized_gemm_f32(hw, hx, hy, M, N, K, dt)
+    y = hip.download(hy, (M, N))
+    for h in (hw, hx, hy):
+        hip.free(h)
+    return y
+
+
+@pytest.mark.parametrize("dt", ALL_GEMM, ids=lambda d: d.name)
+@pytest.mark.parametrize("M,N,K", [(1, 128, 256), (7, 300, 512), (128, 2560, 2048), (128, 2048, 5632),
+                                   (130, 129, 2048), (1024, 300, 1024)])
+def test_gemm_f32_rows_match_oracle(hip, dt, M, N, K):
+    """f32 X (hi + lo on the matrix cores): rows against the oracle's f64 dot
+    of the same f32 row, and against the GPU's f32 matvec of that row."""
+    say(f"[gemm f32] {dt.name} M={M} N={N} K={K}")
+    w = synth.gen_quant(dt, 110 + M, N, K)
+    x = synth.gauss(111 + K, (M, K))
+    y = run_gemm_f32(hip, dt, w, x, M, N, K)
+    rows = sorted({0, M // 2, M - 1} | set(range(0, M, max(1, M // 8))))
+    for m in rows:
+        ref = oracle.qmv_f64(int(dt), w, x[m], N, K)
+        assert np.max(np.abs(y[m] - ref)) <= tolerance_bar(ref), f"row {m}"
+    hw, hx, hy = hip.upload(w), hip.allocate(4 * K), hip.allocate(4 * N)
+    for m in rows:
+        hip.copy_to_device(x[m], hx)
+        hip.quantized_matmul(hw, hx, hy, N, K, dt)
+        mv = hip.download(hy, N)
+        assert np.max(np.abs(y[m] - mv)) <= tolerance_bar(mv), f"row {m} vs matvec"
+    for h in (hw, hx, hy):
+        hip.free(h)
+
+
+@pytest.mark.parametrize("dt", [DType.Q4_K, DType.Q6_K, DType.Q8_0], ids=lambda d: d.name)
+def test_gemm_f32_full_range_and_repeat(hip, dt):
+    """f32 rows of any magnitude, and a second call bit-identical (the lo
+    product adds into Y in a fixed order: split-K at M = 16, whole tiles at
+    M = 1024 where the bf16 call would split its tail tiles)."""
+    K = 1024
+    say(f"[gemm f32] range rows and repeat {dt.name}")
+    w = synth.gen_quant(dt, 120, 160, K)
+    x = range_rows(K)
+    y = run_gemm_f32(hip, dt, w, x, len(x), 160, K)
+    for m in range(len(x)):
+        ref = oracle.qmv_f64(int(dt), w, x[m], 160, K)
+        if not np.any(x[m]):
+            assert np.all(y[m] == 0.0)
+            continue
+        assert np.all(np.isfinite(y[m])) and np.max(np.abs(y[m] - ref)) <= tolerance_bar(ref), f"row {m}"
+    for M, N, KK in ((16, 4096, 4096), (1024, 8348, 512)):
+        w2 = synth.gen_quant(dt, 121, N, KK)
+        x2 = synth.gauss(122, (M, KK))
+        a = run_gemm_f32(hip, dt, w2, x2, M, N, KK)
+        assert np.array_equal(a, run_gemm_f32(hip, dt, w2, x2, M, N, KK)), f"M={M}: second call differs"
+        ref = oracle.qmv_f64(int(dt), w2, x2[M - 1], N, KK)
+        assert np.max(np.abs(a[M - 1] - ref)) <= tolerance_bar(ref)
+
+
 def test_gemm_errors(hip):
     w = synth.gen_quant(DType.Q4_K, 1, 16, 256)
     hw, hx, hy = hip.upload(w), hip.allocate(2 * 256 * 4), hip.allocate(4 * 16 * 4)

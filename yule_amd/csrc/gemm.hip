@@ -26,10 +26,19 @@
 //    q - 8 (exact in f16, made from 1024 + q with one packed subtract), d
 //    applied per 32-weight block: a 32-k MFMA step is exactly one block, so
 //    acc += d * (that step's product).
-//  * X: bf16 -> f16 is exact for every bf16 in f16's normal range.  A pre-pass
-//    converts X once per call (not once per weight tile) and stores each group
-//    of four k in the order {0,2,1,3}, the order in which the dword nibble
-//    masks deliver weights, so neither side is shuffled in the main loop.
+//  * X: a pre-pass (one workgroup per row) scales each row by a power of two
+//    that puts its largest magnitude in [2^9, 2^10), converts it to f16 once
+//    per call (not once per weight tile) and stores each group of four k in
+//    the order {0,2,1,3}, the order in which the dword nibble masks deliver
+//    weights, so neither side is shuffled in the main loop.  A scaled bf16
+//    is exact in f16 down to 2^-26 of the row's maximum (everything a sum
+//    against that maximum can resolve), nothing overflows, and the Q4_K
+//    sub-block sums (at most 32 * 2^10) fit f16 too; the epilogue multiplies
+//    each Y row by the inverse power of two, which is exact.  f32 X
+//    (yule_hip_quantized_gemm_f32) is split the same way into f16 hi + lo
+//    (x = hi + lo to ~2^-22) and runs as two products, the second adding into
+//    Y: the accuracy of the f32 matvec, for callers that need it (prefill
+//    whose results must match token-by-token decode).
 //
 #include <mutex>
 #include <type_traits>
@@ -77,41 +86,88 @@ __device__ __forceinline__ void align_raw(const uint32_t *raw, uint32_t mis, uin
     for (int i = 0; i < N / 4; i++) out[i] = __builtin_amdgcn_alignbyte(raw[i + 1], raw[i], mis);
 }
 
-// X pre-pass, one thread per (row m, 32-column sub-block j): bf16 -> f16 with
-// each group of four k stored as {0,2,1,3}; optionally the sub-block sums of
-// X split into f16 hi + lo (the Q4_K min term).
-__global__ void gemm_xprep_kernel(const uint16_t *__restrict__ x, _Float16 *__restrict__ xh,
-                                  _Float16 *__restrict__ hi, _Float16 *__restrict__ lo, uint32_t M, uint32_t K) {
-    const uint32_t nsub = K / 32;
-    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (uint64_t)M * nsub) return;
-    const uint32_t m = (uint32_t)(i / nsub), j = (uint32_t)(i % nsub);
-    const size_t o = (size_t)m * K + 32 * j;
-    const uint4 *p = reinterpret_cast<const uint4 *>(x + o);
-    uint4 *q = reinterpret_cast<uint4 *>(xh + o);
-    float s = 0.f;
+// X pre-pass, one workgroup of 256 threads per row m (8-element chunks c =
+// tid + 256 i).  Pass 1: the row's largest magnitude, which sets the power of
+// two s = 2^(10 - e) with |x| max = f * 2^e, f in [0.5, 1), so that the
+// scaled row lies below 2^10 (a row of zeros, or one holding inf or NaN,
+// keeps s = 1).  Pass 2 (the row again, now from L2): xh = f16(x * s) in the
+// {0,2,1,3} order; for f32 input also xl = f16(x * s - xh); the Q4_K min
+// term's sub-block sums of x * s as f16 hi + lo; rowscale[m] = 1 / s.
+template <bool F32>
+__global__ __launch_bounds__(256) void gemm_xprep_kernel(const void *__restrict__ xin, _Float16 *__restrict__ xh,
+                                                         _Float16 *__restrict__ xl, _Float16 *__restrict__ hi,
+                                                         _Float16 *__restrict__ lo, float *__restrict__ rowscale,
+                                                         uint32_t K) {
+    __shared__ float red[4];
+    const uint32_t m = blockIdx.x, tid = threadIdx.x, nch = K / 8;
+    auto load8 = [&](uint32_t c, float *v) {
+        if constexpr (F32) {
+            const float4 *p = reinterpret_cast<const float4 *>(static_cast<const float *>(xin) + (size_t)m * K + 8 * c);
+            const float4 a = p[0], b = p[1];
+            v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+        } else {
+            const uint4 u = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(xin) + (size_t)m * K + 8 * c);
+            const uint32_t wv[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
-    for (int c = 0; c < 4; c++) {   // 8 elements: two groups of four
-        const uint4 v = p[c];
-        const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
-        uint16_t e[8];
+            for (int t = 0; t < 4; t++) {
+                v[2 * t] = __builtin_bit_cast(float, wv[t] << 16);
+                v[2 * t + 1] = __builtin_bit_cast(float, wv[t] & 0xFFFF0000u);
+            }
+        }
+    };
+    float amax = 0.f;
+    for (uint32_t c = tid; c < nch; c += 256) {
+        float v[8];
+        load8(c, v);
 #pragma unroll
-        for (int t = 0; t < 4; t++) { e[2 * t] = (uint16_t)(wv[t] & 0xFFFFu); e[2 * t + 1] = (uint16_t)(wv[t] >> 16); }
-#pragma unroll
-        for (int t = 0; t < 8; t++) s += __builtin_bit_cast(float, (uint32_t)e[t] << 16);
-        const int perm[8] = {0, 2, 1, 3, 4, 6, 5, 7};
-        uint32_t outw[4];
-#pragma unroll
-        for (int t = 0; t < 4; t++)
-            outw[t] = (uint32_t)__builtin_bit_cast(uint16_t, bf16_to_f16(e[perm[2 * t]])) |
-                      ((uint32_t)__builtin_bit_cast(uint16_t, bf16_to_f16(e[perm[2 * t + 1]])) << 16);
-        q[c] = make_uint4(outw[0], outw[1], outw[2], outw[3]);
+        for (int t = 0; t < 8; t++) amax = fmaxf(amax, fabsf(v[t]));   // NaN is dropped here, kept below
     }
-    if (hi) {
-        const _Float16 h = (_Float16)s;
-        hi[i] = h;
-        lo[i] = (_Float16)(s - (float)h);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+    if ((tid & 63) == 0) red[tid >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    int e = 0;
+    (void)frexpf(amax, &e);
+    const int es = 10 - e < 126 ? 10 - e : 126;   // rows below 2^-116 keep s = 2^126
+    const bool scaled = amax > 0.f && amax <= 3.402823466e38f;
+    const float sc = scaled ? ldexpf(1.0f, es) : 1.0f;
+    const int perm[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+    for (uint32_t c0 = 0; c0 < nch; c0 += 256) {   // uniform trip count: the quad sums below need every lane
+        const uint32_t c = c0 + tid;
+        const bool ok = c < nch;
+        float v[8];
+        load8(ok ? c : 0u, v);
+        float s = 0.f;
+        uint32_t oh[4], ol[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const float a = v[perm[2 * t]] * sc, b = v[perm[2 * t + 1]] * sc;
+            const h2v h = {(_Float16)a, (_Float16)b};
+            oh[t] = __builtin_bit_cast(uint32_t, h);
+            if constexpr (F32) {
+                const h2v l = {(_Float16)(a - (float)h.x), (_Float16)(b - (float)h.y)};
+                ol[t] = __builtin_bit_cast(uint32_t, l);
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < 8; t++) s += v[t] * sc;
+        // the four chunks of a 32-element sub-block are lanes 4j..4j+3
+        s += __shfl_xor(s, 1, 64);
+        s += __shfl_xor(s, 2, 64);
+        if (ok) {
+            const size_t o = (size_t)m * K + 8 * c;
+            *reinterpret_cast<uint4 *>(xh + o) = make_uint4(oh[0], oh[1], oh[2], oh[3]);
+            if constexpr (F32) *reinterpret_cast<uint4 *>(xl + o) = make_uint4(ol[0], ol[1], ol[2], ol[3]);
+            if (hi && (c & 3u) == 0) {
+                const size_t j = (size_t)m * (K / 32) + c / 4;
+                const _Float16 h = (_Float16)s;
+                hi[j] = h;
+                lo[j] = (_Float16)(s - (float)h);
+            }
+        }
     }
+    if (tid == 0) rowscale[m] = scaled ? ldexpf(1.0f, -es) : 1.0f;
 }
 
 // Per-stage register staging of one thread: XCH 16-byte chunks of X and the
@@ -145,8 +201,8 @@ __device__ __forceinline__ uint32_t u8pair_to_f16(uint32_t v, _Float16 bias) {
 template <uint32_t DT, int BM, int BN>
 __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YULE_DTYPE_Q6_K ? 1 : 2))) void gemm_kernel(
     const uint8_t *__restrict__ w, const _Float16 *__restrict__ xh, float *__restrict__ y,
-    const _Float16 *__restrict__ xs_hi, const _Float16 *__restrict__ xs_lo, uint32_t M, uint32_t N, uint32_t K,
-    uint32_t xcd_remap, uint32_t tail) {
+    const _Float16 *__restrict__ xs_hi, const _Float16 *__restrict__ xs_lo, const float *__restrict__ rowscale,
+    uint32_t M, uint32_t N, uint32_t K, uint32_t xcd_remap, uint32_t tail, uint32_t accumulate) {
     constexpr bool Q5 = DT == YULE_DTYPE_Q5_K;
     constexpr bool Q4 = DT == YULE_DTYPE_Q4_K || Q5;   // Q5_K: Q4_K plus a fifth bit per weight from qh
     constexpr bool B32 = DT == YULE_DTYPE_Q8_0 || DT == YULE_DTYPE_Q4_0;   // 32-weight blocks, d per block
@@ -519,7 +575,7 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
         }
     }
 
-    if constexpr (Q4) {
+    if (Q4 && xs_hi) {   // (no sums: the second, lo, product of an f32 X)
         // min term: acc -= sum_j xsum[m][j] * (dmin*mn)[r][j] over the K/32
         // sub-blocks.  In chunks of four super-blocks the workgroup stages
         // the operands once into the LDS the main loop no longer needs: each
@@ -606,8 +662,10 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
             for (int e = 0; e < 4; e++) {
                 const uint32_t m = m0 + wm * (BM / 2) + i * 16 + 4 * (lane >> 4) + e;
                 if (m < M && r < N) {
-                    if (halves) unsafeAtomicAdd(y + (size_t)m * N + r, acc[i][j][e]);
-                    else y[(size_t)m * N + r] = acc[i][j][e];
+                    const float v = acc[i][j][e] * rowscale[m];   // the row's power of two back out: exact
+                    if (halves) unsafeAtomicAdd(y + (size_t)m * N + r, v);
+                    else if (accumulate && splits == 1) y[(size_t)m * N + r] += v;
+                    else y[(size_t)m * N + r] = v;
                 }
             }
         }
@@ -627,13 +685,14 @@ __global__ void gemm_zero_tiles_kernel(float *__restrict__ y, uint32_t M, uint32
     }
 }
 
-// y[i] = sum over z of part[z][i], z ascending
-__global__ void gemm_reduce_kernel(const float *__restrict__ part, float *__restrict__ y, uint64_t n, uint32_t ks) {
+// y[i] = sum over z of part[z][i], z ascending (accumulate: y[i] + that sum)
+__global__ void gemm_reduce_kernel(const float *__restrict__ part, float *__restrict__ y, uint64_t n, uint32_t ks,
+                                   uint32_t accumulate) {
     const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
     float s = part[i];
     for (uint32_t z = 1; z < ks; z++) s += part[(uint64_t)z * n + i];
-    y[i] = s;
+    y[i] = accumulate ? y[i] + s : s;
 }
 
 }  // namespace yule
@@ -683,85 +742,146 @@ uint32_t gemm_tail(uint32_t m, uint32_t n, uint32_t k, uint32_t bn, uint32_t ks)
     return r <= round / 2 ? r : 0;
 }
 
+// One product over the tile grid.  Y rows are scaled by rowscale; with
+// accumulate the product adds into Y (the lo pass of an f32 X): its tiles run
+// whole (no K-half tail, whose atomic adds would then round in either order).
+struct GemmPass {
+    const uint8_t *w;
+    const _Float16 *xh, *xs_hi, *xs_lo;
+    const float *rowscale;
+    float *y;
+    uint32_t m, n, k, ks, bn, tail, accumulate;
+};
+
 template <uint32_t DT, int BN>
-void launch_gemm_bn(hipStream_t s, const uint8_t *w, const _Float16 *xh, float *y, const _Float16 *xs_hi,
-                    const _Float16 *xs_lo, uint32_t m, uint32_t n, uint32_t k, uint32_t ks, uint32_t tail) {
+void launch_gemm_bn(hipStream_t s, const GemmPass &p) {
     static const uint32_t remap = env_flag("YULE_GEMM_XCD_REMAP", false) ? 1u : 0u;
-    const uint32_t nt = (n + BN - 1) / BN;
-    const uint32_t bm = m <= 64 ? 64 : 128, tiles = nt * ((m + bm - 1) / bm);
-    const uint32_t grid = tail ? tiles + tail : tiles * ks;
-    if (tail)
-        hipLaunchKernelGGL(gemm_zero_tiles_kernel, dim3(tail * (bm / 8)), dim3(256), 0, s, y, m, n, tiles - tail, nt,
-                           bm, (uint32_t)BN);
-    if (m <= 64) {
-        hipLaunchKernelGGL((gemm_kernel<DT, 64, BN>), dim3(grid), dim3(2 * BN), 0, s, w, xh, y, xs_hi, xs_lo, m, n, k,
-                           remap, tail);
+    const uint32_t nt = (p.n + BN - 1) / BN;
+    const uint32_t bm = p.m <= 64 ? 64 : 128, tiles = nt * ((p.m + bm - 1) / bm);
+    const uint32_t grid = p.tail ? tiles + p.tail : tiles * p.ks;
+    if (p.tail)
+        hipLaunchKernelGGL(gemm_zero_tiles_kernel, dim3(p.tail * (bm / 8)), dim3(256), 0, s, p.y, p.m, p.n,
+                           tiles - p.tail, nt, bm, (uint32_t)BN);
+    if (p.m <= 64) {
+        hipLaunchKernelGGL((gemm_kernel<DT, 64, BN>), dim3(grid), dim3(2 * BN), 0, s, p.w, p.xh, p.y, p.xs_hi,
+                           p.xs_lo, p.rowscale, p.m, p.n, p.k, remap, p.tail, p.accumulate);
     } else {
-        hipLaunchKernelGGL((gemm_kernel<DT, 128, BN>), dim3(grid), dim3(2 * BN), 0, s, w, xh, y, xs_hi, xs_lo, m, n,
-                           k, remap, tail);
+        hipLaunchKernelGGL((gemm_kernel<DT, 128, BN>), dim3(grid), dim3(2 * BN), 0, s, p.w, p.xh, p.y, p.xs_hi,
+                           p.xs_lo, p.rowscale, p.m, p.n, p.k, remap, p.tail, p.accumulate);
     }
 }
 
 template <uint32_t DT>
-void launch_gemm(hipStream_t s, const uint8_t *w, const _Float16 *xh, float *y, const _Float16 *xs_hi,
-                 const _Float16 *xs_lo, uint32_t m, uint32_t n, uint32_t k, uint32_t ks, uint32_t bn, uint32_t tail) {
-    if (bn == 256) launch_gemm_bn<DT, 256>(s, w, xh, y, xs_hi, xs_lo, m, n, k, ks, tail);
-    else launch_gemm_bn<DT, 128>(s, w, xh, y, xs_hi, xs_lo, m, n, k, ks, tail);
+void launch_gemm(hipStream_t s, const GemmPass &p) {
+    if (p.bn == 256) launch_gemm_bn<DT, 256>(s, p);
+    else launch_gemm_bn<DT, 128>(s, p);
 }
+
+int launch_gemm_dt(hipStream_t s, uint32_t dtype, const GemmPass &p) {
+    switch (dtype) {
+    case YULE_DTYPE_Q4_K: launch_gemm<YULE_DTYPE_Q4_K>(s, p); break;
+    case YULE_DTYPE_Q6_K: launch_gemm<YULE_DTYPE_Q6_K>(s, p); break;
+    case YULE_DTYPE_Q5_K: launch_gemm<YULE_DTYPE_Q5_K>(s, p); break;
+    case YULE_DTYPE_Q8_K: launch_gemm<YULE_DTYPE_Q8_K>(s, p); break;
+    case YULE_DTYPE_Q8_0: launch_gemm<YULE_DTYPE_Q8_0>(s, p); break;
+    default: launch_gemm<YULE_DTYPE_Q4_0>(s, p); break;
+    }
+    return check_launch("quantized_gemm");
+}
+
+bool gemm_dtype_ok(uint32_t dtype) {
+    return dtype == YULE_DTYPE_Q4_K || dtype == YULE_DTYPE_Q6_K || dtype == YULE_DTYPE_Q8_0 ||
+           dtype == YULE_DTYPE_Q4_0 || dtype == YULE_DTYPE_Q5_K || dtype == YULE_DTYPE_Q8_K;
+}
+
 }  // namespace
 
-extern "C" int yule_hip_quantized_gemm(yule_hip_backend *be, yule_buffer weights, yule_buffer x_bf16, yule_buffer y,
-                                       uint32_t m, uint32_t n_rows, uint32_t n_cols, uint32_t dtype) {
+// Workspace of one call (bytes) and the pieces inside it: split-K partials,
+// then X in f16 (hi, and lo for f32 X), the Q4_K/Q5_K sub-block sums (hi, lo)
+// and the per-row scales.
+struct GemmWork {
+    size_t part_bytes, total;
+    size_t n_x, n_sub, n_y;
+    uint32_t ks, bn, tail;
+    bool q4;
+};
+
+static GemmWork gemm_work(uint32_t m, uint32_t n_rows, uint32_t n_cols, uint32_t dtype, bool f32x) {
+    GemmWork g;
+    g.q4 = dtype == YULE_DTYPE_Q4_K || dtype == YULE_DTYPE_Q5_K;   // min term: X sub-block sums
+    g.bn = gemm_bn(m, dtype);
+    g.ks = gemm_splits(m, n_rows, n_cols, g.bn);
+    g.tail = gemm_tail(m, n_rows, n_cols, g.bn, g.ks);
+    g.n_x = (size_t)m * n_cols;
+    g.n_sub = (size_t)m * (n_cols / 32);
+    g.n_y = (size_t)m * n_rows;
+    g.part_bytes = g.ks > 1 ? ((g.ks * g.n_y * sizeof(float) + 255) & ~(size_t)255) : 0;
+    g.total = g.part_bytes + ((f32x ? 2 : 1) * g.n_x + (g.q4 ? 2 * g.n_sub : 0)) * sizeof(_Float16) + 256 +
+              (size_t)m * sizeof(float) + 256;
+    return g;
+}
+
+// Enqueue the pre-pass and the product(s) of one call into workspace ws.
+static int gemm_enqueue(hipStream_t s, const uint8_t *w, const void *x, bool f32x, float *y, uint32_t m,
+                        uint32_t n_rows, uint32_t n_cols, uint32_t dtype, const GemmWork &g, void *ws) {
+    uint8_t *b = static_cast<uint8_t *>(ws);
+    float *part = g.ks > 1 ? reinterpret_cast<float *>(b) : nullptr;
+    _Float16 *xh = reinterpret_cast<_Float16 *>(b + g.part_bytes);
+    _Float16 *xl = f32x ? xh + g.n_x : nullptr;
+    _Float16 *xs_hi = g.q4 ? xh + (f32x ? 2 : 1) * g.n_x : nullptr, *xs_lo = g.q4 ? xs_hi + g.n_sub : nullptr;
+    float *rowscale = reinterpret_cast<float *>(
+        (reinterpret_cast<uintptr_t>(xh + (f32x ? 2 : 1) * g.n_x + (g.q4 ? 2 * g.n_sub : 0)) + 255) & ~(uintptr_t)255);
+    if (f32x)
+        hipLaunchKernelGGL(gemm_xprep_kernel<true>, dim3(m), dim3(256), 0, s, x, xh, xl, xs_hi, xs_lo, rowscale, n_cols);
+    else
+        hipLaunchKernelGGL(gemm_xprep_kernel<false>, dim3(m), dim3(256), 0, s, x, xh, xl, xs_hi, xs_lo, rowscale,
+                           n_cols);
+    int rc = check_launch("quantized_gemm: x pre-pass");
+    if (rc) return rc;
+    for (int pass = 0; pass < (f32x ? 2 : 1); pass++) {
+        GemmPass p{w, pass ? xl : xh, pass ? nullptr : xs_hi, pass ? nullptr : xs_lo, rowscale,
+                   g.ks > 1 ? part : y, m, n_rows, n_cols, g.ks, g.bn, pass ? 0u : g.tail, (uint32_t)pass};
+        if ((rc = launch_gemm_dt(s, dtype, p))) return rc;
+        if (g.ks > 1) {
+            hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)((g.n_y + 255) / 256)), dim3(256), 0, s, part, y,
+                               (uint64_t)g.n_y, g.ks, (uint32_t)pass);
+            if ((rc = check_launch("quantized_gemm: split-K reduction"))) return rc;
+        }
+    }
+    return YULE_OK;
+}
+
+static int gemm_entry(yule_hip_backend *be, yule_buffer weights, yule_buffer x, bool f32x, yule_buffer y, uint32_t m,
+                      uint32_t n_rows, uint32_t n_cols, uint32_t dtype, const char *what) {
     if (!be) return set_error(YULE_ERR_INVALID, "null backend");
-    if (dtype != YULE_DTYPE_Q4_K && dtype != YULE_DTYPE_Q6_K && dtype != YULE_DTYPE_Q8_0 && dtype != YULE_DTYPE_Q4_0 &&
-        dtype != YULE_DTYPE_Q5_K && dtype != YULE_DTYPE_Q8_K)
-        return set_error(YULE_ERR_UNSUPPORTED, "quantized_gemm: dtype " + std::to_string(dtype) +
+    if (!gemm_dtype_ok(dtype))
+        return set_error(YULE_ERR_UNSUPPORTED, std::string(what) + ": dtype " + std::to_string(dtype) +
                                                    " not supported (Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, Q8_K)");
-    if (n_cols % 256) return set_error(YULE_ERR_INVALID, "quantized_gemm: n_cols must be a multiple of 256");
+    if (n_cols % 256) return set_error(YULE_ERR_INVALID, std::string(what) + ": n_cols must be a multiple of 256");
     uint32_t bs, bb;
     quant_geometry(dtype, &bs, &bb);
     void *pw, *px, *py;
     int rc;
-    if ((rc = get_buffer(be, weights, (size_t)n_rows * (n_cols / bs) * bb, &pw, "quantized_gemm (weights)")) ||
-        (rc = get_buffer(be, x_bf16, (size_t)m * n_cols * 2, &px, "quantized_gemm (x)")) ||
-        (rc = get_buffer(be, y, (size_t)m * n_rows * 4, &py, "quantized_gemm (y)")))
+    if ((rc = get_buffer(be, weights, (size_t)n_rows * (n_cols / bs) * bb, &pw, what)) ||
+        (rc = get_buffer(be, x, (size_t)m * n_cols * (f32x ? 4 : 2), &px, what)) ||
+        (rc = get_buffer(be, y, (size_t)m * n_rows * 4, &py, what)))
         return rc;
-    if (x_bf16 == y) return set_error(YULE_ERR_INVALID, "quantized_gemm: x and y alias");
-    if (weights == y || weights == x_bf16)
-        return set_error(YULE_ERR_INVALID, "quantized_gemm: weights alias x or y");
+    if (x == y) return set_error(YULE_ERR_INVALID, std::string(what) + ": x and y alias");
+    if (weights == y || weights == x) return set_error(YULE_ERR_INVALID, std::string(what) + ": weights alias x or y");
     if (!m || !n_rows) return YULE_OK;
     if (!n_cols) return launch_fill(be->stream, (float *)py, 0.f, (uint64_t)m * n_rows);
-    const bool q4 = dtype == YULE_DTYPE_Q4_K || dtype == YULE_DTYPE_Q5_K;   // min term: X sub-block sums
-    const uint32_t bn = gemm_bn(m, dtype), ks = gemm_splits(m, n_rows, n_cols, bn);
-    const uint32_t tail = gemm_tail(m, n_rows, n_cols, bn, ks);
-    const size_t n_x = (size_t)m * n_cols, n_sub = (size_t)m * (n_cols / 32), n_y = (size_t)m * n_rows;
-    const size_t part_bytes = ks > 1 ? ((ks * n_y * sizeof(float) + 255) & ~(size_t)255) : 0;
-    const size_t need = part_bytes + (n_x + (q4 ? 2 * n_sub : 0)) * sizeof(_Float16) + 256;
-    // workspace: split-K partials, then X in f16 (permuted) and its sub-block sums
+    const GemmWork g = gemm_work(m, n_rows, n_cols, dtype, f32x);
     ScratchLease lease;   // held until every launch below is enqueued
-    if ((rc = get_scratch(be, need, &lease))) return rc;
-    void *ws = lease.ptr;
-    float *part = ks > 1 ? static_cast<float *>(ws) : nullptr;
-    _Float16 *xh = reinterpret_cast<_Float16 *>(static_cast<uint8_t *>(ws) + part_bytes);
-    _Float16 *xs_hi = q4 ? xh + n_x : nullptr, *xs_lo = q4 ? xs_hi + n_sub : nullptr;
-    hipLaunchKernelGGL(gemm_xprep_kernel, dim3((unsigned)((n_sub + 255) / 256)), dim3(256), 0, be->stream,
-                       (const uint16_t *)px, xh, xs_hi, xs_lo, m, n_cols);
-    if ((rc = check_launch("quantized_gemm: x pre-pass"))) return rc;
-    float *out = ks > 1 ? part : (float *)py;
-    const uint8_t *wq = (const uint8_t *)pw;
-    switch (dtype) {
-    case YULE_DTYPE_Q4_K: launch_gemm<YULE_DTYPE_Q4_K>(be->stream, wq, xh, out, xs_hi, xs_lo, m, n_rows, n_cols, ks, bn, tail); break;
-    case YULE_DTYPE_Q6_K: launch_gemm<YULE_DTYPE_Q6_K>(be->stream, wq, xh, out, nullptr, nullptr, m, n_rows, n_cols, ks, bn, tail); break;
-    case YULE_DTYPE_Q5_K: launch_gemm<YULE_DTYPE_Q5_K>(be->stream, wq, xh, out, xs_hi, xs_lo, m, n_rows, n_cols, ks, bn, tail); break;
-    case YULE_DTYPE_Q8_K: launch_gemm<YULE_DTYPE_Q8_K>(be->stream, wq, xh, out, nullptr, nullptr, m, n_rows, n_cols, ks, bn, tail); break;
-    case YULE_DTYPE_Q8_0: launch_gemm<YULE_DTYPE_Q8_0>(be->stream, wq, xh, out, nullptr, nullptr, m, n_rows, n_cols, ks, bn, tail); break;
-    default: launch_gemm<YULE_DTYPE_Q4_0>(be->stream, wq, xh, out, nullptr, nullptr, m, n_rows, n_cols, ks, bn, tail); break;
-    }
-    if ((rc = check_launch("quantized_gemm"))) return rc;
-    if (ks > 1) {
-        hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)((n_y + 255) / 256)), dim3(256), 0, be->stream, part,
-                           (float *)py, (uint64_t)n_y, ks);
-        rc = check_launch("quantized_gemm: split-K reduction");
-    }
-    return rc;
+    if ((rc = get_scratch(be, g.total, &lease))) return rc;
+    return gemm_enqueue(be->stream, (const uint8_t *)pw, px, f32x, (float *)py, m, n_rows, n_cols, dtype, g, lease.ptr);
+}
+
+extern "C" int yule_hip_quantized_gemm(yule_hip_backend *be, yule_buffer weights, yule_buffer x_bf16, yule_buffer y,
+                                       uint32_t m, uint32_t n_rows, uint32_t n_cols, uint32_t dtype) {
+    return gemm_entry(be, weights, x_bf16, false, y, m, n_rows, n_cols, dtype, "quantized_gemm");
+}
+
+extern "C" int yule_hip_quantized_gemm_f32(yule_hip_backend *be, yule_buffer weights, yule_buffer x_f32, yule_buffer y,
+                                           uint32_t m, uint32_t n_rows, uint32_t n_cols, uint32_t dtype) {
+    return gemm_entry(be, weights, x_f32, true, y, m, n_rows, n_cols, dtype, "quantized_gemm_f32");
 }
