@@ -206,6 +206,22 @@ int yule_hip_quantized_gemm_f32(yule_hip_backend *be, yule_buffer weights, yule_
                                 yule_buffer y, uint32_t m, uint32_t n_rows, uint32_t n_cols,
                                 uint32_t dtype);
 
+/* Allocation-free variant of yule_hip_quantized_gemm (no counterpart in the
+ * reference; for callers that cannot allocate device memory: code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * It runs the same kernels with its workspace in a static 32 MiB device
+ * array per GPU (the library holds it until the process ends) instead of
+ * the backend's grown-on-demand workspace; it calls no allocator.  Calls
+ * whose workspace would exceed 32 MiB (X in f16 plus split-K partials, e.g.
+ * M = 2048 at n_cols = 14336) return YULE_ERR_INVALID.  Every call on a GPU
+ * shares that GPU's array: calls that can overlap on one GPU (other streams,
+ * other backends on the same device) race; calls on one stream are ordered.
+ * The array needs no clearing between calls (every byte a call reads was
+ * written by that call). */
+int yule_hip_quantized_gemm_noalloc(yule_hip_backend *be, yule_buffer weights, yule_buffer x_bf16,
+                                    yule_buffer y, uint32_t m, uint32_t n_rows, uint32_t n_cols,
+                                    uint32_t dtype);
+
 /* ---- decode runner (yule-infer GpuTransformerRunner counterpart) ---- */
 
 /* One transformer layer's tensors as host pointers to raw GGUF data

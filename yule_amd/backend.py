@@ -55,6 +55,7 @@ _SIGS: dict[str, tuple] = {
     "yule_hip_argmax": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint32, C.c_uint64]),
     "yule_hip_quantized_gemm": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint64] + [C.c_uint32] * 4),
     "yule_hip_quantized_gemm_f32": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint64] + [C.c_uint32] * 4),
+    "yule_hip_quantized_gemm_noalloc": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint64] + [C.c_uint32] * 4),
     "yule_hip_runner_create": (C.c_int, [C.c_void_p, C.c_void_p, C.POINTER(C.c_void_p)]),
     "yule_hip_runner_destroy": (C.c_int, [C.c_void_p]),
     "yule_hip_runner_reset": (C.c_int, [C.c_void_p]),
@@ -289,6 +290,12 @@ class HipBackend:
         """Y = X W^T for f32 X [m][n_cols] (split f16 hi + lo on the matrix cores)."""
         self._check(self._lib.yule_hip_quantized_gemm_f32(self._be, _h(weights), _h(x_f32), _h(y), m, n_rows, n_cols,
                                                           int(dtype)))
+
+    def quantized_gemm_noalloc(self, weights, x_bf16, y, m: int, n_rows: int, n_cols: int,
+                               dtype: DType | int) -> None:
+        """quantized_gemm with its workspace in the library's static per-GPU array (no allocation)."""
+        self._check(self._lib.yule_hip_quantized_gemm_noalloc(self._be, _h(weights), _h(x_bf16), _h(y), m, n_rows,
+                                                              n_cols, int(dtype)))
 
     def time_qmv_ops(self, ops, iters: int, use_graph: bool = True) -> float:
         """Milliseconds (HIP events on the backend stream) for `iters` passes over

@@ -851,8 +851,38 @@ static int gemm_enqueue(hipStream_t s, const uint8_t *w, const void *x, bool f32
     return YULE_OK;
 }
 
+// ---- static workspace of the allocation-free entry point
+// One array per GPU, in the code object, alive until the process ends.  Its
+// device address is looked up once per device, with that device current, at
+// backend creation (gemm_static_workspace_init); host code uses that
+// address, never the array's name.
+constexpr size_t kStaticWorkspaceBytes = (size_t)32 << 20;
+static __device__ __align__(256) uint8_t scratch[kStaticWorkspaceBytes];
+constexpr int kMaxDevices = 64;
+static std::mutex g_static_mu;
+static void *g_static_ptr[kMaxDevices];
+
+int yule::gemm_static_workspace_init(int device) {
+    if (device < 0 || device >= kMaxDevices)
+        return set_error(YULE_ERR_NO_DEVICE, "static workspace: device index above " + std::to_string(kMaxDevices - 1));
+    std::lock_guard<std::mutex> lk(g_static_mu);
+    if (g_static_ptr[device]) return YULE_OK;
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_error(e, "hipGetSymbolAddress (static workspace)");
+    if (!p) return set_error(YULE_ERR_HIP, "static workspace: null device address");
+    g_static_ptr[device] = p;
+    return YULE_OK;
+}
+
+static void *static_workspace(int device) {
+    if (device < 0 || device >= kMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> lk(g_static_mu);
+    return g_static_ptr[device];
+}
+
 static int gemm_entry(yule_hip_backend *be, yule_buffer weights, yule_buffer x, bool f32x, yule_buffer y, uint32_t m,
-                      uint32_t n_rows, uint32_t n_cols, uint32_t dtype, const char *what) {
+                      uint32_t n_rows, uint32_t n_cols, uint32_t dtype, const char *what, bool noalloc = false) {
     if (!be) return set_error(YULE_ERR_INVALID, "null backend");
     if (!gemm_dtype_ok(dtype))
         return set_error(YULE_ERR_UNSUPPORTED, std::string(what) + ": dtype " + std::to_string(dtype) +
@@ -871,6 +901,15 @@ static int gemm_entry(yule_hip_backend *be, yule_buffer weights, yule_buffer x, 
     if (!m || !n_rows) return YULE_OK;
     if (!n_cols) return launch_fill(be->stream, (float *)py, 0.f, (uint64_t)m * n_rows);
     const GemmWork g = gemm_work(m, n_rows, n_cols, dtype, f32x);
+    if (noalloc) {
+        if (g.total > kStaticWorkspaceBytes)
+            return set_error(YULE_ERR_INVALID, std::string(what) + ": this call needs " + std::to_string(g.total) +
+                                                   " bytes of workspace, above the static " +
+                                                   std::to_string(kStaticWorkspaceBytes) + "-byte one");
+        void *ws = static_workspace(be->device);
+        if (!ws) return set_error(YULE_ERR_HIP, std::string(what) + ": static workspace not set up for this device");
+        return gemm_enqueue(be->stream, (const uint8_t *)pw, px, f32x, (float *)py, m, n_rows, n_cols, dtype, g, ws);
+    }
     ScratchLease lease;   // held until every launch below is enqueued
     if ((rc = get_scratch(be, g.total, &lease))) return rc;
     return gemm_enqueue(be->stream, (const uint8_t *)pw, px, f32x, (float *)py, m, n_rows, n_cols, dtype, g, lease.ptr);
@@ -884,4 +923,10 @@ extern "C" int yule_hip_quantized_gemm(yule_hip_backend *be, yule_buffer weights
 extern "C" int yule_hip_quantized_gemm_f32(yule_hip_backend *be, yule_buffer weights, yule_buffer x_f32, yule_buffer y,
                                            uint32_t m, uint32_t n_rows, uint32_t n_cols, uint32_t dtype) {
     return gemm_entry(be, weights, x_f32, true, y, m, n_rows, n_cols, dtype, "quantized_gemm_f32");
+}
+
+extern "C" int yule_hip_quantized_gemm_noalloc(yule_hip_backend *be, yule_buffer weights, yule_buffer x_bf16,
+                                               yule_buffer y, uint32_t m, uint32_t n_rows, uint32_t n_cols,
+                                               uint32_t dtype) {
+    return gemm_entry(be, weights, x_bf16, false, y, m, n_rows, n_cols, dtype, "quantized_gemm_noalloc", true);
 }

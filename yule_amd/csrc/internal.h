@@ -110,6 +110,9 @@ int launch_dequant(hipStream_t stream, uint32_t dtype, const uint8_t *src, float
 // table; the token is read on the device so the launch can sit in a graph
 int launch_embed_rows(hipStream_t stream, uint32_t dtype, const uint8_t *table, const uint32_t *token,
                       uint32_t n_rows, float *dst, uint32_t dim);
+// device address of the allocation-free GEMM's static workspace on `device`,
+// looked up once with that device current (yule_hip_create)
+int gemm_static_workspace_init(int device);
 // one launch of an empty kernel (launch-overhead probe)
 int launch_empty(hipStream_t stream);
 // out[i] = value for i < n

@@ -127,6 +127,10 @@ int yule_hip_create(int device, yule_hip_backend **out) {
         delete be;
         return set_error(YULE_ERR_NO_DEVICE, "create: device is " + arch + ", this build targets gfx950");
     }
+    if ((rc = gemm_static_workspace_init(device))) {   // with `device` current
+        delete be;
+        return rc;
+    }
     // default-priority stream (no priority games); non-blocking w.r.t. the null stream
     if ((rc = hip_error(hipStreamCreateWithFlags(&be->stream, hipStreamNonBlocking), "hipStreamCreate"))) {
         delete be;
