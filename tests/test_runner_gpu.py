@@ -107,6 +107,51 @@ def test_runner_greedy_matches_oracle_small(hip, tiny):
     run.close()
 
 
+HD64 = None
+
+
+@pytest.mark.parametrize("chunks,split_min", [("1", None), ("1", "100"), ("0", None)],
+                         ids=["chunked", "chunked-then-split", "per-head"])
+def test_runner_hd64_attention_paths(hip, chunks, split_min, monkeypatch):
+    """Head size 64 on narrow teams: the Q/K/V launch applies RoPE and writes
+    the cache (kEpiRope) and attention runs chunked with its in-launch
+    combine, over 1..150 positions (one to three 64-position chunks); then the
+    same with split-KV from position 99 on, and with the one-workgroup-per-head
+    kernel.  Logits vs the oracle and the float64 forward at every step, then
+    greedy tokens."""
+    from yule_amd.model import LlamaConfig
+    global HD64
+    if HD64 is None:
+        HD64 = SyntheticModel.generate(LlamaConfig(n_layers=2, dim=512, n_heads=8, n_kv_heads=2, ff_dim=1024,
+                                                   vocab=1024, max_seq=160), seed=9)
+    m = HD64
+    say(f"[runner] hd 64 model, chunked attention {chunks}, split from {split_min}")
+    monkeypatch.setenv("YULE_ATTN_CHUNKS", chunks)
+    if split_min:
+        monkeypatch.setenv("YULE_ATTN_SPLIT_MIN", split_min)
+    run = HipRunner(hip, m)
+    ref, f64 = oracle.Runner(m, n_threads=4), NpForward(m)
+    toks = synth.uniform_tokens(31, 150, m.cfg.vocab)
+    for i, t in enumerate(toks):
+        got, want, exact = run.decode_step(int(t)), ref.forward(int(t)), f64.forward(int(t))
+        assert np.max(np.abs(got - want)) <= tolerance_bar(want), f"step {i}"
+        assert np.max(np.abs(got - exact)) <= tolerance_bar(exact), f"step {i}"
+    run.close()
+    prompt = synth.uniform_tokens(32, 70, m.cfg.vocab)
+    run = HipRunner(hip, m)
+    out, _ = run.generate_greedy(prompt, 80)
+    run.close()
+    ref = oracle.Runner(m, n_threads=4)
+    for t in prompt:
+        logits = ref.forward(int(t))
+    want = []
+    for i in range(81):
+        want.append(oracle.argmax(logits))
+        if i < 80:
+            logits = ref.forward(want[-1])
+    assert [int(t) for t in out] == want
+
+
 @pytest.mark.parametrize("threads_w64", ["256", "512"])
 def test_runner_wide_rows_fused_variants(hip, threads_w64):
     """4096-wide rows: every fused matvec variant on one-wave teams, in both

@@ -80,7 +80,7 @@ struct QmvSeg {
 // Optional fusions of the streaming matvec: a transform applied to the
 // activation vector while it is staged, and an epilogue.
 constexpr uint32_t kXfNone = 0, kXfRmsNorm = 1, kXfSwiGlu = 2;
-constexpr uint32_t kEpiStore = 0, kEpiAdd = 1, kEpiArgmax = 2;
+constexpr uint32_t kEpiStore = 0, kEpiAdd = 1, kEpiArgmax = 2, kEpiRope = 3;
 // argmax epilogue slots (one per workgroup of the launch; zero-filled once)
 constexpr uint32_t kArgmaxSlots = 2048;
 struct QmvXf {
@@ -90,6 +90,14 @@ struct QmvXf {
     uint32_t epi = kEpiStore;        // kEpiAdd: y += result; kEpiArgmax: store, and each workgroup's
     unsigned long long *amax = nullptr;  // best (key << 32 | row) into amax[blockIdx.x] (kArgmaxSlots)
     bool pair = false;               // gate/up pair: segment 0 output = silu(gate)*up
+    // kEpiRope (the Q/K/V launch of a decode step; segments q, k, v, teams of
+    // at most 32 lanes): RoPE with the table row of position ctl[0] applied to
+    // q (stored to segment 0's output) and k, and k and v stored straight into
+    // the KV cache row ctl[0] (model_runner.rs:654-669, 277-293)
+    const uint32_t *ctl = nullptr;
+    const float *cos_t = nullptr, *sin_t = nullptr;   // [max_seq][hd / 2]
+    float *kc = nullptr, *vc = nullptr;               // [max_seq][n_kv * hd]
+    uint32_t hd = 0;
 };
 
 // Kernel launchers (device code in qmv.hip / ops.hip / attn.hip / gemm.hip).
@@ -102,6 +110,10 @@ int launch_qmv_multi(hipStream_t stream, uint32_t dtype, const QmvSeg *segs, uin
 bool qmv_fusable(uint32_t dtype, uint32_t n_cols);
 // true when gate/up of this shape can run as one paired launch (xf.pair)
 bool qmv_pairable(uint32_t dtype, uint32_t n_cols);
+// lanes per row of the streaming matvec for this shape
+uint32_t qmv_team_width(uint32_t dtype, uint32_t n_cols);
+// true when the Q/K/V launch can apply RoPE and write the KV cache (kEpiRope)
+bool qmv_rope_ok(uint32_t dtype, uint32_t n_cols, uint32_t hd);
 int launch_qmv_fused(hipStream_t stream, uint32_t dtype, const QmvSeg *segs, uint32_t n_seg, const float *x,
                      uint32_t n_cols, const QmvXf &xf);
 int launch_dequant(hipStream_t stream, uint32_t dtype, const uint8_t *src, float *dst,
@@ -113,6 +125,14 @@ int launch_embed_rows(hipStream_t stream, uint32_t dtype, const uint8_t *table, 
 // device address of the allocation-free GEMM's static workspace on `device`,
 // looked up once with that device current (yule_hip_create)
 int gemm_static_workspace_init(int device);
+// decode-step attention over a cache that already holds row ctl[0] and a
+// rotated q (after a kEpiRope Q/K/V launch): one workgroup per (query head,
+// chunk), chunks combined in-launch; hd 64 or 128 (attn_chunk_len != 0)
+uint32_t attn_chunk_len(uint32_t hd);
+size_t attn_chunk_scratch_bytes(uint32_t n_heads, uint32_t hd, uint32_t max_rows);
+int launch_attn_chunks(hipStream_t stream, const float *q, const float *kc, const float *vc, const uint32_t *ctl,
+                       float *out, void *scratch, uint32_t n_heads, uint32_t n_kv, uint32_t hd, uint32_t max_rows,
+                       uint32_t seq_host);
 // one launch of an empty kernel (launch-overhead probe)
 int launch_empty(hipStream_t stream);
 // out[i] = value for i < n

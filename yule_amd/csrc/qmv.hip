@@ -571,6 +571,8 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const Segs sg, const flo
     // kernels hold fewer, keeping their register count)
     constexpr uint32_t kXPer = PAIR ? 4 : 8;
     Buf buf[D];
+    uint32_t rpos = 0;
+    float rcos = 0.f, rsin = 0.f;
     // TWO: a fused input transform is on (its operand is loaded with x); a
     // template parameter, so the plain kernels carry none of its code
     {
@@ -588,6 +590,15 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const Segs sg, const flo
 #pragma unroll
         for (int j = 0; j < D - 1; j++)
             if (r0 + j * stride < n_rows) buf[j] = fetch(r0 + j * stride);
+        if (W < 64) {
+            // RoPE epilogue: lane l keeps cos / sin of pair l of the position's
+            // table row (unconditional loads from a valid address either way)
+            const bool rope = xf.epi == kEpiRope;
+            rpos = rope ? xf.ctl[0] : 0u;
+            const uint32_t half = rope ? xf.hd / 2 : 1u, li = (tid & 63u) % half;
+            rcos = (rope ? xf.cos_t : x)[(size_t)rpos * half + li];
+            rsin = (rope ? xf.sin_t : x)[(size_t)rpos * half + li];
+        }
         float inv = 1.0f;
         if (TWO && xf.mode == kXfRmsNorm) {
             // rms_norm (model_runner.rs:246-275) computed by every workgroup
@@ -636,7 +647,24 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const Segs sg, const flo
     __shared__ float ring[16][NWV];
     auto finish = [&](float acc, uint32_t rbase, uint32_t it, bool last) {
         acc = team_sum<(W < 64 ? W : 64)>(active ? acc : 0.f);
-        if (WPT == 1) {
+        if (W < 64 && xf.epi == kEpiRope) {
+            // rows 2i and 2i + 1 of a head are teams 2j and 2j + 1 of one wave
+            // (row bases are even): the pair meets across lane W
+            const float other = __shfl_xor(acc, W, 64);
+            const uint32_t row = rbase + team;
+            const uint32_t s = seg_of(row < n_rows ? row : n_rows - 1), loc = row - sg.start[s < kMaxSegs ? s : 0];
+            const uint32_t i = (loc % xf.hd) / 2;
+            const float c = __shfl(rcos, (int)i, 64), sn = __shfl(rsin, (int)i, 64);
+            const bool even = (loc & 1u) == 0;
+            const float x0 = even ? acc : other, x1 = even ? other : acc;
+            float v = acc;
+            if (s < 2) v = even ? x0 * c - x1 * sn : x0 * sn + x1 * c;
+            if (t == 0 && row < n_rows) {
+                const size_t kvd = (size_t)(sg.start[2] - sg.start[1]);
+                if (s == 0) sg.y[0][loc] = v;
+                else (s == 1 ? xf.kc : xf.vc)[(size_t)rpos * kvd + loc] = v;
+            }
+        } else if (WPT == 1) {
             const uint32_t row = uni(rbase + team);
             if (t == 0 && row < n_rows) store(row, acc);
         } else {
@@ -802,6 +830,24 @@ bool qmv_pairable(uint32_t dtype, uint32_t n_cols) {
     return units <= 64;
 }
 
+// The Q/K/V launch can apply RoPE and write the cache itself (kEpiRope) when
+// its teams are at most 32 lanes wide (the two rows of a rotation pair then
+// sit in one wave) and a head's rotation pairs fit one wave's lanes.
+bool qmv_rope_ok(uint32_t dtype, uint32_t n_cols, uint32_t hd) {
+    if (!qmv_fusable(dtype, n_cols) || hd == 0 || hd % 2 || hd / 2 > 64) return false;
+    return qmv_pairable(dtype, n_cols) && qmv_team_width(dtype, n_cols) <= 32;
+}
+
+uint32_t qmv_team_width(uint32_t dtype, uint32_t n_cols) {
+    uint32_t bs, bb;
+    if (!quant_geometry(dtype, &bs, &bb)) return 0;
+    const uint32_t upb = dtype == YULE_DTYPE_Q4_K || dtype == YULE_DTYPE_Q5_K   ? 4u
+                         : dtype == YULE_DTYPE_Q6_K || dtype == YULE_DTYPE_Q8_K ? 8u
+                                                                               : 1u;
+    const uint32_t units = (n_cols / bs) * upb;
+    return units <= 16 ? 16 : units <= 32 ? 32 : units <= 64 ? 64 : units <= 128 ? 128 : units <= 256 ? 256 : 512;
+}
+
 bool qmv_fusable(uint32_t dtype, uint32_t n_cols) {
     switch (dtype) {
     case YULE_DTYPE_Q4_K: return stream_ok<Q4K>(n_cols);
@@ -819,6 +865,9 @@ int launch_qmv_fused(hipStream_t s, uint32_t dtype, const QmvSeg *segs, uint32_t
     if (n_seg == 0 || n_seg > kMaxSegs) return set_error(YULE_ERR_INVALID, "quantized_matmul: bad segment count");
     if (xf.epi == kEpiArgmax && n_seg != 1)
         return set_error(YULE_ERR_INVALID, "quantized_matmul: argmax epilogue needs a single matrix");
+    if (xf.epi == kEpiRope && (n_seg != 3 || !qmv_rope_ok(dtype, n_cols, xf.hd) || segs[1].n_rows != segs[2].n_rows ||
+                               segs[0].n_rows % xf.hd || segs[1].n_rows % xf.hd || xf.pair))
+        return set_error(YULE_ERR_INVALID, "quantized_matmul: RoPE epilogue needs q, k, v of whole heads on narrow teams");
     if (xf.pair && (n_seg != 2 || segs[0].n_rows != segs[1].n_rows || !qmv_pairable(dtype, n_cols) ||
                     xf.mode == kXfNone))
         return set_error(YULE_ERR_INVALID, "quantized_matmul: paired gate/up needs two equal single-wave matrices and an input transform");

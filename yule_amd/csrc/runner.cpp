@@ -47,6 +47,10 @@ struct yule_hip_runner {
     // per variant: [0] short, [1] split.
     uint32_t split_min = 0;
     void *attn_ws = nullptr;
+    // shorter steps, when the Q/K/V launch can rotate and write the cache
+    // itself (kEpiRope): chunked attention with in-launch combine (partials
+    // and per-head tickets in chunk_ws, zeroed at creation)
+    void *chunk_ws = nullptr;
     hipGraph_t graph[2] = {nullptr, nullptr};
     hipGraphExec_t exec[2] = {nullptr, nullptr};
     uint32_t pos = 0;  // host mirror of ctl[0]
@@ -136,6 +140,17 @@ int enqueue_step(yule_hip_runner *r, bool split) {
         } else {
             xin = r->hidden;
         }
+        const bool chunked = fuse && !split && r->chunk_ws && L.tq == L.tk && L.tk == L.tv &&
+                             qmv_rope_ok(L.tq, r->dim, r->hd);
+        if (chunked) {   // RoPE and the cache write in the Q/K/V launch's epilogue
+            norm.epi = kEpiRope;
+            norm.ctl = r->ctl;
+            norm.cos_t = r->cos_t;
+            norm.sin_t = r->sin_t;
+            norm.kc = L.kc;
+            norm.vc = L.vc;
+            norm.hd = r->hd;
+        }
         if (L.tq == L.tk && L.tk == L.tv) {
             const QmvSeg segs[3] = {{L.wq, r->q, qd}, {L.wk, r->k, kvd}, {L.wv, r->v, kvd}};
             if ((rc = launch_qmv_fused(s, L.tq, segs, 3, xin, r->dim, norm))) return rc;
@@ -146,7 +161,10 @@ int enqueue_step(yule_hip_runner *r, bool split) {
                 (rc = launch_qmv_fused(s, L.tv, &sv, 1, xin, r->dim, norm)))
                 return rc;
         }
-        if (split)
+        if (chunked)
+            rc = launch_attn_chunks(s, r->q, L.kc, L.vc, r->ctl, r->attn, r->chunk_ws, r->n_heads, r->n_kv, r->hd,
+                                    std::min(r->max_seq, r->split_min), 0u);
+        else if (split)
             rc = launch_attn_split(s, r->q, r->k, r->v, L.kc, L.vc, r->cos_t, r->sin_t, r->ctl, r->attn, r->attn_ws,
                                    r->n_heads, r->n_kv, r->hd, r->max_seq);
         else
@@ -326,6 +344,12 @@ int yule_hip_runner_create(yule_hip_backend *be, const yule_model_desc *d, yule_
         (rc = dev_alloc(r, (size_t)r->max_seq * 4, reinterpret_cast<void **>(&r->tokens))))
         return fail(rc);
     if ((rc = dev_alloc(r, kArgmaxSlots * sizeof(unsigned long long), reinterpret_cast<void **>(&r->amax))))
+        return fail(rc);
+    // chunked attention for steps below the split threshold (YULE_ATTN_CHUNKS=0
+    // at creation: the one-workgroup-per-head kernel instead)
+    const char *ce = getenv("YULE_ATTN_CHUNKS");
+    if ((!ce || atoi(ce) != 0) && attn_chunk_len(hd) &&
+        (rc = dev_alloc(r, attn_chunk_scratch_bytes(r->n_heads, hd, std::min(r->max_seq, r->split_min)), &r->chunk_ws)))
         return fail(rc);
     if (r->max_seq >= r->split_min &&
         (rc = dev_alloc(r, split_scratch_bytes(r->n_heads, hd, r->max_seq), &r->attn_ws)))
