@@ -214,8 +214,12 @@ def decode_e2e(hip, cpu: bool):
     run = HipRunner(hip, model)
     run.generate_greedy(prompt, 16)                       # warm-up (graph capture)
     toks, ms = run.generate_greedy(prompt, 256)
+    pre_ms = run.last_prefill_ms
     run.close()
     res = {"decode_tok_s": round(1000.0 / ms, 1), "decode_ms_per_step": round(ms, 4),
+           # the 128-token prompt as one batched pass (GEMM projections, causal
+           # attention per row), prompt tokens / wall ms of that pass
+           "prefill_tok_s": round(len(prompt) * 1000.0 / pre_ms, 1), "prefill_ms": round(pre_ms, 3),
            "decode_weight_bytes_per_step": model.bytes_per_token(),
            "decode_effective_GB/s": round(model.bytes_per_token() / (ms * 1e-3) / 1e9, 1)}
     golden = ROOT / "tests" / "golden" / "e2e_tinyllama_greedy.json"

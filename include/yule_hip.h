@@ -271,6 +271,20 @@ int yule_hip_runner_decode_step(yule_hip_runner *r, uint32_t token, float *logit
 /* ModelRunner::prefill (model_runner.rs:1075-1081): token by token; logits
  * of the last token when non-null. */
 int yule_hip_runner_prefill(yule_hip_runner *r, const uint32_t *tokens, uint32_t n, float *logits);
+/* The same prefill with the n tokens as one batch (no counterpart in the
+ * reference, which prefills token by token): each layer runs its projections
+ * as f32-X GEMMs on the matrix cores (yule_hip_quantized_gemm_f32), RoPE and
+ * the KV-cache rows for all n positions, and causal attention per row; the
+ * last row then goes through the final norm, lm_head and argmax as the
+ * token-by-token prefill's last step would.  KV cache and logits equal the
+ * token-by-token ones to f32 rounding.  Needs every projection in a GEMM
+ * format with columns a multiple of 256 and head_dim 32, 64, 128 or 256;
+ * otherwise YULE_ERR_UNSUPPORTED.  generate_greedy prefills this way whenever
+ * it can (environment YULE_RUNNER_TOKEN_PREFILL at runner creation: token by
+ * token). */
+int yule_hip_runner_prefill_batched(yule_hip_runner *r, const uint32_t *tokens, uint32_t n, float *logits);
+/* Milliseconds the prompt pass of the last generate_greedy took (HIP events). */
+float yule_hip_runner_last_prefill_ms(const yule_hip_runner *r);
 /* Greedy generation from position 0 entirely on the device: n_prompt
  * prompt tokens, then n_decode decode steps fed by argmax_ct
  * (sampler.rs:150-163).  out_tokens receives n_decode + 1 ids: the argmax

@@ -152,6 +152,62 @@ def test_runner_hd64_attention_paths(hip, chunks, split_min, monkeypatch):
     assert [int(t) for t in out] == want
 
 
+@pytest.mark.parametrize("which", ["tiny", "hd64"])
+def test_runner_prefill_batched_matches_oracle(hip, tiny, which):
+    """The prompt as one batched pass (GEMM projections, causal attention
+    per row): last-token logits vs the oracle's token-by-token prefill, a
+    second batch from position 20 on, then decode steps over the cache the
+    batches wrote."""
+    from yule_amd.model import LlamaConfig
+    global HD64
+    if which == "hd64" and HD64 is None:
+        HD64 = SyntheticModel.generate(LlamaConfig(n_layers=2, dim=512, n_heads=8, n_kv_heads=2, ff_dim=1024,
+                                                   vocab=1024, max_seq=160), seed=9)
+    m = tiny if which == "tiny" else HD64
+    say(f"[runner] batched prefill vs oracle ({which})")
+    toks = synth.uniform_tokens(41, 44, m.cfg.vocab)
+    run, ref = HipRunner(hip, m), oracle.Runner(m, n_threads=4)
+    got = run.prefill_batched(toks[:20])
+    for t in toks[:20]:
+        want = ref.forward(int(t))
+    assert run.pos == 20
+    assert np.max(np.abs(got - want)) <= tolerance_bar(want)
+    got = run.prefill_batched(toks[20:37])
+    for t in toks[20:37]:
+        want = ref.forward(int(t))
+    assert np.max(np.abs(got - want)) <= tolerance_bar(want)
+    for i, t in enumerate(toks[37:]):
+        got, want = run.decode_step(int(t)), ref.forward(int(t))
+        assert np.max(np.abs(got - want)) <= tolerance_bar(want), f"decode step {i}"
+    run.close()
+
+
+def test_runner_greedy_token_prefill_path(hip, tiny, monkeypatch):
+    """generate_greedy with the token-by-token prompt pass (the runner's
+    fallback when a projection has no batched path) gives the oracle's tokens,
+    as the batched pass does."""
+    say("[runner] greedy with token-by-token prefill")
+    prompt = synth.uniform_tokens(43, 24, tiny.cfg.vocab)
+    outs = []
+    for env in ("1", None):
+        if env:
+            monkeypatch.setenv("YULE_RUNNER_TOKEN_PREFILL", env)
+        else:
+            monkeypatch.delenv("YULE_RUNNER_TOKEN_PREFILL", raising=False)
+        run = HipRunner(hip, tiny)
+        outs.append([int(t) for t in run.generate_greedy(prompt, 30)[0]])
+        run.close()
+    ref = oracle.Runner(tiny, n_threads=4)
+    for t in prompt:
+        logits = ref.forward(int(t))
+    want = []
+    for i in range(31):
+        want.append(oracle.argmax(logits))
+        if i < 30:
+            logits = ref.forward(want[-1])
+    assert outs[0] == want and outs[1] == want
+
+
 @pytest.mark.parametrize("threads_w64", ["256", "512"])
 def test_runner_wide_rows_fused_variants(hip, threads_w64):
     """4096-wide rows: every fused matvec variant on one-wave teams, in both

@@ -62,6 +62,8 @@ _SIGS: dict[str, tuple] = {
     "yule_hip_runner_pos": (C.c_uint32, [C.c_void_p]),
     "yule_hip_runner_decode_step": (C.c_int, [C.c_void_p, C.c_uint32, C.c_void_p]),
     "yule_hip_runner_prefill": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p]),
+    "yule_hip_runner_prefill_batched": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p]),
+    "yule_hip_runner_last_prefill_ms": (C.c_float, [C.c_void_p]),
     "yule_hip_runner_generate_greedy": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p,
                                                   C.POINTER(C.c_float)]),
     "yule_hip_gguf_open": (C.c_int, [C.c_char_p, C.POINTER(C.c_void_p)]),
@@ -435,6 +437,18 @@ class HipRunner:
         out = np.empty(self.vocab, np.float32)
         self._be._check(self._lib.yule_hip_runner_prefill(self._r, t.ctypes.data, t.size, out.ctypes.data))
         return out
+
+    def prefill_batched(self, tokens) -> np.ndarray:
+        """The tokens as one batched pass (GEMM projections); logits of the last one."""
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        out = np.empty(self.vocab, np.float32)
+        self._be._check(self._lib.yule_hip_runner_prefill_batched(self._r, t.ctypes.data, t.size, out.ctypes.data))
+        return out
+
+    @property
+    def last_prefill_ms(self) -> float:
+        """Milliseconds of the prompt pass of the last generate_greedy."""
+        return float(self._lib.yule_hip_runner_last_prefill_ms(self._r))
 
     def generate_greedy(self, prompt, n_decode: int):
         """-> (tokens[n_decode + 1], ms per decode step)"""

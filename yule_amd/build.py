@@ -25,7 +25,7 @@ LIB_SYNTH = PKG / "libyule_synth.so"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
-HIP_SOURCES = ["runtime.cpp", "qmv.hip", "ops.hip", "gemm.hip", "runner.cpp", "gguf.cpp"]
+HIP_SOURCES = ["runtime.cpp", "qmv.hip", "ops.hip", "gemm.hip", "prefill.hip", "runner.cpp", "gguf.cpp"]
 
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",

@@ -915,6 +915,21 @@ static int gemm_entry(yule_hip_backend *be, yule_buffer weights, yule_buffer x, 
     return gemm_enqueue(be->stream, (const uint8_t *)pw, px, f32x, (float *)py, m, n_rows, n_cols, dtype, g, lease.ptr);
 }
 
+// the f32-X product for library callers that own their workspace (the
+// runner's batched prefill)
+bool yule::gemm_supports(uint32_t dtype, uint32_t n_cols) { return gemm_dtype_ok(dtype) && n_cols % 256 == 0; }
+
+size_t yule::gemm_f32_workspace_bytes(uint32_t m, uint32_t n_rows, uint32_t n_cols, uint32_t dtype) {
+    return gemm_work(m, n_rows, n_cols, dtype, true).total;
+}
+
+int yule::launch_gemm_f32(hipStream_t s, const uint8_t *w, const float *x, float *y, uint32_t m, uint32_t n_rows,
+                          uint32_t n_cols, uint32_t dtype, void *ws) {
+    if (!gemm_dtype_ok(dtype) || n_cols % 256) return set_error(YULE_ERR_UNSUPPORTED, "gemm: format or shape");
+    if (!m || !n_rows) return YULE_OK;
+    return gemm_enqueue(s, w, x, true, y, m, n_rows, n_cols, dtype, gemm_work(m, n_rows, n_cols, dtype, true), ws);
+}
+
 extern "C" int yule_hip_quantized_gemm(yule_hip_backend *be, yule_buffer weights, yule_buffer x_bf16, yule_buffer y,
                                        uint32_t m, uint32_t n_rows, uint32_t n_cols, uint32_t dtype) {
     return gemm_entry(be, weights, x_bf16, false, y, m, n_rows, n_cols, dtype, "quantized_gemm");

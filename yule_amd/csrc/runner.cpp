@@ -51,12 +51,23 @@ struct yule_hip_runner {
     // itself (kEpiRope): chunked attention with in-launch combine (partials
     // and per-head tickets in chunk_ws, zeroed at creation)
     void *chunk_ws = nullptr;
+    // batched prefill (prefill_rows): row buffers for max_seq rows and the
+    // GEMM workspace, allocated at the first batched prefill
+    bool batchable = false;
+    float *bx = nullptr, *bn = nullptr, *bq = nullptr, *bk = nullptr, *bv = nullptr, *ba = nullptr, *bp = nullptr,
+          *bg = nullptr, *bu = nullptr;
+    void *bws = nullptr;
+    size_t bws_size = 0;
+    float last_prefill_ms = 0.f;
     hipGraph_t graph[2] = {nullptr, nullptr};
     hipGraphExec_t exec[2] = {nullptr, nullptr};
     uint32_t pos = 0;  // host mirror of ctl[0]
 };
 
 namespace {
+
+int set_ctl(yule_hip_runner *r, uint32_t pos, uint32_t token, uint32_t prompt_len);
+int enqueue_head(yule_hip_runner *r);
 
 int dev_alloc(yule_hip_runner *r, size_t bytes, void **p) {
     int rc = hip_error(hipMalloc(p, bytes + kAllocSlack), "runner: allocate");
@@ -111,6 +122,27 @@ int upload_matrix(yule_hip_runner *r, const void *src, uint32_t dtype, uint32_t 
     if (cols % bs)
         return set_error(YULE_ERR_INVALID, std::string("runner: ") + name + " columns not a block multiple");
     return upload(r, src, (size_t)rows * (cols / bs) * bb, reinterpret_cast<void **>(const_cast<uint8_t **>(dst)));
+}
+
+// Final norm + lm_head + argmax over r->hidden, then advance the control
+// block (model_runner.rs:1008-1025, sampler.rs:150-163).
+int enqueue_head(yule_hip_runner *r) {
+    hipStream_t s = r->be->stream;
+    int rc;
+    if (r->fused) {
+        QmvXf head;
+        head.mode = kXfRmsNorm;
+        head.a = r->out_norm;
+        head.eps = r->eps;
+        head.epi = kEpiArgmax;
+        head.amax = r->amax;
+        const QmvSeg so{r->out_w, r->logits, r->vocab};
+        if ((rc = launch_qmv_fused(s, r->out_t, &so, 1, r->hidden, r->dim, head))) return rc;
+        return launch_advance(s, r->amax, r->ctl, r->tokens);
+    }
+    if ((rc = launch_rms_norm(s, r->hidden, r->out_norm, r->normed, r->dim, r->eps))) return rc;
+    if ((rc = launch_qmv(s, r->out_t, r->out_w, r->normed, r->logits, r->vocab, r->dim))) return rc;
+    return launch_argmax_advance(s, r->logits, r->vocab, r->ctl, r->tokens);
 }
 
 // One decode step for the token selected by ctl, entirely on r->be->stream.
@@ -216,20 +248,7 @@ int enqueue_step(yule_hip_runner *r, bool split) {
             if ((rc = launch_eltwise(s, 2, r->hidden, r->ffn, r->hidden, r->dim))) return rc;
         }
     }
-    if (fuse) {  // final norm + lm_head + argmax (model_runner.rs:1008-1025, sampler.rs:150-163)
-        QmvXf head;
-        head.mode = kXfRmsNorm;
-        head.a = r->out_norm;
-        head.eps = r->eps;
-        head.epi = kEpiArgmax;
-        head.amax = r->amax;
-        const QmvSeg so{r->out_w, r->logits, r->vocab};
-        if ((rc = launch_qmv_fused(s, r->out_t, &so, 1, r->hidden, r->dim, head))) return rc;
-        return launch_advance(s, r->amax, r->ctl, r->tokens);
-    }
-    if ((rc = launch_rms_norm(s, r->hidden, r->out_norm, r->normed, r->dim, r->eps))) return rc;
-    if ((rc = launch_qmv(s, r->out_t, r->out_w, r->normed, r->logits, r->vocab, r->dim))) return rc;
-    return launch_argmax_advance(s, r->logits, r->vocab, r->ctl, r->tokens);
+    return enqueue_head(r);
 }
 
 int ensure_graph(yule_hip_runner *r, bool split) {
@@ -255,6 +274,84 @@ int run_step(yule_hip_runner *r, uint32_t pos) {
     int rc = ensure_graph(r, split);
     if (rc) return rc;
     return hip_error(hipGraphLaunch(r->exec[split], r->be->stream), "runner: graph launch");
+}
+
+// GEMM workspace the batched pass over n rows needs (the largest of its
+// products)
+size_t batch_workspace(const yule_hip_runner *r, uint32_t n) {
+    const uint32_t qd = r->n_heads * r->hd, kvd = r->n_kv * r->hd;
+    size_t need = 0;
+    for (const auto &L : r->layers) {
+        const size_t w[7] = {gemm_f32_workspace_bytes(n, qd, r->dim, L.tq), gemm_f32_workspace_bytes(n, kvd, r->dim, L.tk),
+                             gemm_f32_workspace_bytes(n, kvd, r->dim, L.tv), gemm_f32_workspace_bytes(n, r->dim, qd, L.to),
+                             gemm_f32_workspace_bytes(n, r->ff, r->dim, L.tg), gemm_f32_workspace_bytes(n, r->ff, r->dim, L.tu),
+                             gemm_f32_workspace_bytes(n, r->dim, r->ff, L.td)};
+        for (size_t v : w) need = std::max(need, v);
+    }
+    return need;
+}
+
+int ensure_batch(yule_hip_runner *r, uint32_t n) {
+    const uint32_t qd = r->n_heads * r->hd, kvd = r->n_kv * r->hd;
+    int rc;
+    if (!r->bx) {
+        struct { float **p; size_t n; } bufs[] = {
+            {&r->bx, r->dim}, {&r->bn, r->dim}, {&r->bq, qd}, {&r->bk, kvd}, {&r->bv, kvd},
+            {&r->ba, qd}, {&r->bp, r->dim}, {&r->bg, r->ff}, {&r->bu, r->ff}};
+        for (auto &b : bufs)
+            if ((rc = dev_alloc(r, (size_t)r->max_seq * b.n * 4, reinterpret_cast<void **>(b.p)))) return rc;
+    }
+    const size_t need = batch_workspace(r, n);
+    if (need > r->bws_size) {
+        if (r->bws) {
+            if ((rc = hip_error(hipStreamSynchronize(r->be->stream), "runner: synchronize"))) return rc;
+            hipFree(r->bws);
+            r->bws = nullptr;
+            r->bws_size = 0;
+        }
+        if ((rc = hip_error(hipMalloc(&r->bws, need), "runner: prefill workspace"))) return rc;
+        r->bws_size = need;
+    }
+    return YULE_OK;
+}
+
+// The prompt tokens at r->prompt[pos0, pos0 + n) through every layer as n
+// rows at once (prefill.hip; each projection one f32-X GEMM), writing KV rows
+// pos0.. pos0 + n - 1; then the head over the last row, as the decode step
+// for position pos0 + n - 1 would run it, with ctl = {pos0 + n - 1, -,
+// prompt_len}: the argmax lands in tokens[pos0 + n - 1] and ctl[1], and ctl[0]
+// moves to pos0 + n.
+int prefill_rows(yule_hip_runner *r, uint32_t pos0, uint32_t n, uint32_t prompt_len) {
+    hipStream_t s = r->be->stream;
+    const uint32_t qd = r->n_heads * r->hd, kvd = r->n_kv * r->hd;
+    int rc;
+    if ((rc = ensure_batch(r, n))) return rc;
+    // the control block only feeds the head and advance at the end
+    if ((rc = set_ctl(r, pos0 + n - 1, 0, prompt_len))) return rc;
+    void *ws = r->bws;
+    if ((rc = launch_embed_rows_batch(s, r->embd_t, r->embd, r->prompt + pos0, r->vocab, r->bx, r->dim, n))) return rc;
+    for (const auto &L : r->layers) {
+        if ((rc = launch_rms_rows(s, r->bx, L.attn_norm, r->bn, r->dim, n, r->eps)) ||
+            (rc = launch_gemm_f32(s, L.wq, r->bn, r->bq, n, qd, r->dim, L.tq, ws)) ||
+            (rc = launch_gemm_f32(s, L.wk, r->bn, r->bk, n, kvd, r->dim, L.tk, ws)) ||
+            (rc = launch_gemm_f32(s, L.wv, r->bn, r->bv, n, kvd, r->dim, L.tv, ws)) ||
+            (rc = launch_rope_rows(s, r->bq, r->bk, r->bv, L.kc, L.vc, r->cos_t, r->sin_t, pos0, n, qd, kvd, r->hd)) ||
+            (rc = launch_attn_prefill(s, r->bq, L.kc, L.vc, r->ba, pos0, n, r->n_heads, r->n_kv, r->hd)) ||
+            (rc = launch_gemm_f32(s, L.wo, r->ba, r->bp, n, r->dim, qd, L.to, ws)) ||
+            (rc = launch_eltwise(s, 2, r->bx, r->bp, r->bx, n * r->dim)) ||
+            (rc = launch_rms_rows(s, r->bx, L.ffn_norm, r->bn, r->dim, n, r->eps)) ||
+            (rc = launch_gemm_f32(s, L.wg, r->bn, r->bg, n, r->ff, r->dim, L.tg, ws)) ||
+            (rc = launch_gemm_f32(s, L.wu, r->bn, r->bu, n, r->ff, r->dim, L.tu, ws)) ||
+            (rc = launch_eltwise(s, 3, r->bg, r->bu, r->bg, n * r->ff)) ||
+            (rc = launch_gemm_f32(s, L.wd, r->bg, r->bp, n, r->dim, r->ff, L.td, ws)) ||
+            (rc = launch_eltwise(s, 2, r->bx, r->bp, r->bx, n * r->dim)))
+            return rc;
+    }
+    if ((rc = hip_error(hipMemcpyAsync(r->hidden, r->bx + (size_t)(n - 1) * r->dim, (size_t)r->dim * 4,
+                                       hipMemcpyDeviceToDevice, s),
+                        "runner: last prompt row")))
+        return rc;
+    return enqueue_head(r);
 }
 
 int set_ctl(yule_hip_runner *r, uint32_t pos, uint32_t token, uint32_t prompt_len) {
@@ -359,6 +456,13 @@ int yule_hip_runner_create(yule_hip_backend *be, const yule_model_desc *d, yule_
         r->fused = r->fused && qmv_fusable(L.tq, r->dim) && qmv_fusable(L.tk, r->dim) && qmv_fusable(L.tv, r->dim) &&
                    qmv_fusable(L.to, qd) && qmv_fusable(L.tg, r->dim) && qmv_fusable(L.tu, r->dim) &&
                    qmv_fusable(L.td, r->ff);
+    // batched prefill: every projection on the GEMM, attention head size served,
+    // unless YULE_RUNNER_TOKEN_PREFILL is set (then prompts go token by token)
+    r->batchable = getenv("YULE_RUNNER_TOKEN_PREFILL") == nullptr && attn_prefill_supported(hd);
+    for (const auto &L : r->layers)
+        r->batchable = r->batchable && gemm_supports(L.tq, r->dim) && gemm_supports(L.tk, r->dim) &&
+                       gemm_supports(L.tv, r->dim) && gemm_supports(L.to, qd) && gemm_supports(L.tg, r->dim) &&
+                       gemm_supports(L.tu, r->dim) && gemm_supports(L.td, r->ff);
     if ((rc = hip_error(hipHostMalloc(reinterpret_cast<void **>(&r->ctl_host), 4 * sizeof(uint32_t), 0),
                         "runner: pinned control block")))
         return fail(rc);
@@ -374,6 +478,7 @@ int yule_hip_runner_destroy(yule_hip_runner *r) {
         if (r->graph[i]) hipGraphDestroy(r->graph[i]);
     }
     for (void *p : r->allocs) hipFree(p);
+    if (r->bws) hipFree(r->bws);
     if (r->ctl_host) hipHostFree(r->ctl_host);
     delete r;
     return YULE_OK;
@@ -432,12 +537,19 @@ int yule_hip_runner_generate_greedy(yule_hip_runner *r, const uint32_t *prompt, 
     if ((rc = hip_error(hipMemcpyAsync(r->prompt, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice, s),
                         "runner: prompt upload")))
         return rc;
-    if ((rc = set_ctl(r, 0, 0, n_prompt))) return rc;
-    for (uint32_t i = 0; i < n_prompt; i++)
-        if ((rc = run_step(r, i))) return rc;
-    hipEvent_t e0 = nullptr, e1 = nullptr;
-    if ((rc = hip_error(hipEventCreate(&e0), "hipEventCreate")) || (rc = hip_error(hipEventCreate(&e1), "hipEventCreate")))
+    hipEvent_t e0 = nullptr, e1 = nullptr, p0 = nullptr;
+    if ((rc = hip_error(hipEventCreate(&e0), "hipEventCreate")) || (rc = hip_error(hipEventCreate(&e1), "hipEventCreate")) ||
+        (rc = hip_error(hipEventCreate(&p0), "hipEventCreate")))
         goto done;
+    if (r->batchable && n_prompt >= 2 && (rc = ensure_batch(r, n_prompt))) goto done;
+    if ((rc = hip_error(hipEventRecord(p0, s), "hipEventRecord"))) goto done;
+    if (r->batchable && n_prompt >= 2) {   // the prompt as one batched pass
+        if ((rc = prefill_rows(r, 0, n_prompt, n_prompt))) goto done;
+    } else {
+        if ((rc = set_ctl(r, 0, 0, n_prompt))) goto done;
+        for (uint32_t i = 0; i < n_prompt && !rc; i++) rc = run_step(r, i);
+        if (rc) goto done;
+    }
     if ((rc = hip_error(hipEventRecord(e0, s), "hipEventRecord"))) goto done;
     for (uint32_t i = 0; i < n_decode && !rc; i++) rc = run_step(r, n_prompt + i);
     if (rc || (rc = hip_error(hipEventRecord(e1, s), "hipEventRecord"))) goto done;
@@ -447,6 +559,7 @@ int yule_hip_runner_generate_greedy(yule_hip_runner *r, const uint32_t *prompt, 
         if ((rc = hip_error(hipEventElapsedTime(&ms, e0, e1), "hipEventElapsedTime"))) goto done;
         *ms_per_decode_step = n_decode ? ms / (float)n_decode : 0.f;
     }
+    if ((rc = hip_error(hipEventElapsedTime(&r->last_prefill_ms, p0, e0), "hipEventElapsedTime"))) goto done;
     // the argmax after the last prompt token and after every decode step
     rc = hip_error(hipMemcpy(out_tokens, r->tokens + (n_prompt - 1), (size_t)(n_decode + 1) * 4,
                              hipMemcpyDeviceToHost),
@@ -455,7 +568,34 @@ int yule_hip_runner_generate_greedy(yule_hip_runner *r, const uint32_t *prompt, 
 done:
     if (e0) hipEventDestroy(e0);
     if (e1) hipEventDestroy(e1);
+    if (p0) hipEventDestroy(p0);
     return rc;
 }
+
+// Batched counterpart of yule_hip_runner_prefill: the n tokens through every
+// layer at once (each projection one GEMM), from the current position.
+int yule_hip_runner_prefill_batched(yule_hip_runner *r, const uint32_t *tokens, uint32_t n, float *logits) {
+    if (!r || !tokens || !n) return set_error(YULE_ERR_INVALID, "runner_prefill_batched: null argument or no tokens");
+    if (!r->batchable) return set_error(YULE_ERR_UNSUPPORTED, "runner_prefill_batched: a projection format or head "
+                                                                "size has no batched path (use runner_prefill)");
+    if ((uint64_t)r->pos + n > r->max_seq) return set_error(YULE_ERR_INVALID, "context length exceeded");
+    for (uint32_t i = 0; i < n; i++)
+        if (tokens[i] >= r->vocab) return set_error(YULE_ERR_INVALID, "token id out of range");
+    hipStream_t s = r->be->stream;
+    int rc;
+    if ((rc = hip_error(hipMemcpyAsync(r->prompt + r->pos, tokens, (size_t)n * 4, hipMemcpyHostToDevice, s),
+                        "runner: prompt upload")) ||
+        (rc = hip_error(hipStreamSynchronize(s), "runner: synchronize")))   // `tokens` is pageable host memory
+        return rc;
+    if ((rc = prefill_rows(r, r->pos, n, 0))) return rc;
+    r->pos += n;
+    if (logits &&
+        (rc = hip_error(hipMemcpyAsync(logits, r->logits, (size_t)r->vocab * 4, hipMemcpyDeviceToHost, s),
+                        "runner: logits copy")))
+        return rc;
+    return hip_error(hipStreamSynchronize(s), "runner: synchronize");
+}
+
+float yule_hip_runner_last_prefill_ms(const yule_hip_runner *r) { return r ? r->last_prefill_ms : 0.f; }
 
 }  // extern "C"
