@@ -152,6 +152,41 @@ def test_runner_hd64_attention_paths(hip, chunks, split_min, monkeypatch):
     assert [int(t) for t in out] == want
 
 
+@pytest.mark.parametrize("scheme,dim,hd", [("Q4_K", 512, 64), ("Q6_K", 1024, 64), ("Q8_0", 512, 128),
+                                            ("Q6_K", 512, 128), ("Q4_K", 2048, 128)])
+def test_runner_attention_formats_and_head_sizes(hip, scheme, dim, hd):
+    """The decode step with RoPE and the cache write in the Q/K/V launch and
+    chunked attention, on Q4_K, Q6_K and Q8_0 Q/K/V, head sizes 64 and 128
+    and both narrow team widths (16 and 32 lanes), over 1..140 positions:
+    logits vs the oracle at every step, then greedy tokens vs the oracle."""
+    from yule_amd.model import LlamaConfig
+    cfg = LlamaConfig(n_layers=1, dim=dim, n_heads=dim // hd, n_kv_heads=2, ff_dim=512, vocab=512, max_seq=200)
+    m = SyntheticModel.generate(cfg, seed=21, scheme=scheme)
+    say(f"[runner] attention paths, {scheme} dim {dim} hd {hd}")
+    toks = synth.uniform_tokens(33, 140, cfg.vocab)
+    run = HipRunner(hip, m)
+    ref = oracle.Runner(m, n_threads=4)
+    try:
+        for i, t in enumerate(toks):
+            got, want = run.decode_step(int(t)), ref.forward(int(t))
+            assert np.max(np.abs(got - want)) <= tolerance_bar(want), f"step {i}"
+    finally:
+        run.close()
+    prompt = synth.uniform_tokens(34, 20, cfg.vocab)
+    run = HipRunner(hip, m)
+    out, _ = run.generate_greedy(prompt, 60)
+    run.close()
+    ref = oracle.Runner(m, n_threads=4)
+    for t in prompt:
+        logits = ref.forward(int(t))
+    want = []
+    for i in range(61):
+        want.append(oracle.argmax(logits))
+        if i < 60:
+            logits = ref.forward(want[-1])
+    assert [int(t) for t in out] == want
+
+
 @pytest.mark.parametrize("which", ["tiny", "hd64"])
 def test_runner_prefill_batched_matches_oracle(hip, tiny, which):
     """The prompt as one batched pass (GEMM projections, causal attention

@@ -715,6 +715,8 @@ uint32_t gemm_bn(uint32_t m, uint32_t dtype) {
 }
 
 uint32_t gemm_splits(uint32_t m, uint32_t n, uint32_t k, uint32_t bn) {
+    static const int env = env_int("YULE_GEMM_SPLITS", 0);
+    if (env > 0) return (uint32_t)env < k / 256 ? (uint32_t)env : k / 256;
     const uint32_t bm = m <= 64 ? 64 : 128;
     const uint32_t tiles = ((n + bn - 1) / bn) * ((m + bm - 1) / bm);
     const uint32_t cus = (uint32_t)device_cus();
