@@ -60,6 +60,19 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 // rows are padded (72 or 80 halves) so that the 16 rows one ds_read_b128
 // reads spread over the banks.
 constexpr int GSK = 64;
+// Offset (halves) of 16-byte chunk c of row r in a swizzled 64-half-wide
+// LDS tile: chunk c ^ f(r), f a permutation of r & 7.  A group of eight lanes
+// of an MFMA operand read takes chunk c of eight consecutive rows (distinct
+// f(r): distinct slots).  A weight store takes rows r..r+3 (r % 4 == 0) x
+// the two threads of a row, at chunks (k, k + 2) for the Q4_K/Q5_K nibble
+// halves and (k, k + 4) for the other formats; f = the bit order (0, 2, 1)
+// of r & 7 for the first and the identity for the second keep those eight
+// slots distinct too.  X stores take the eight chunks of one row.
+template <bool Q4>
+__device__ __forceinline__ uint32_t swz(uint32_t r, uint32_t c) {
+    const uint32_t f = Q4 ? ((r & 1u) | ((r >> 1) & 2u) | ((r << 1) & 4u)) : (r & 7u);
+    return r * GSK + ((c ^ f) << 3);
+}
 
 __device__ __forceinline__ _Float16 bf16_to_f16(uint16_t b) {
     return (_Float16)__builtin_bit_cast(float, (uint32_t)b << 16);
@@ -213,10 +226,11 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
     constexpr uint32_t NTH = 2 * BN;            // threads: two per weight row of the tile
     constexpr uint32_t WNN = BN / 64;           // waves along n (two along m)
     constexpr int XCH = BM * GSK / 8 / NTH;     // 16-byte X chunks per thread per stage
-    // LDS row pitch in halves: 72 keeps two 128-wide workgroups per CU; the
-    // 256-wide tile (one per CU) measured 6-7% faster at 80 than at 72, 88,
-    // 96 or 104
-    constexpr int GLD = BN == 256 ? 80 : GSK + 8;
+    // LDS tiles: rows of GSK = 64 halves (128 bytes, eight 16-byte chunks),
+    // XOR-swizzled (swz) instead of padded: each group of eight lanes of a
+    // load or store covers the eight chunk positions of a 128-byte bank line
+    // once, and the 64 x 128 tile keeps three workgroups per CU.
+    constexpr int GLD = GSK;
     __shared__ __align__(16) _Float16 sx[2][BM * GLD];
     __shared__ __align__(16) _Float16 sw[2][BN * GLD];
     __shared__ float sd[2][B32 ? 2 : 1][BN];   // d per weight row: super-block slot, or the stage's two blocks
@@ -265,13 +279,20 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
 #pragma unroll
         for (int j = 0; j < 4; j++) { acc[i][j] = floatx4{0, 0, 0, 0}; tmp[i][j] = floatx4{0, 0, 0, 0}; }
 
-    // weight role: two threads per weight row, 32 weights of the stage each
+    // weight role: two threads per weight row (adjacent lanes: each pair
+    // loads one 32-byte run), 32 weights of the stage each
     const uint32_t wr = tid >> 1, part = tid & 1u;
-    const bool wrow_ok = r0 + wr < N;
-    const uint8_t *wrow = w + (size_t)(wrow_ok ? r0 + wr : 0) * row_bytes;
+    // Rows past M or N load from a valid row (X rows clamped to M - 1, weight
+    // rows to row 0) and are used as they are: a row of the product depends
+    // only on its own X row and a column only on its own weight row, and the
+    // epilogue stores neither, so no masking is needed.
+    const uint8_t *wrow = w + (size_t)(r0 + wr < N ? r0 + wr : 0) * row_bytes;
 
-    auto load_stage = [&](uint32_t s, GemmRegs<DT, XCH> &R) {
-        const uint32_t kb = kb_lo + (s >> 2), st = s & 3u, k0 = kb * 256u + st * GSK;
+    // stc: std::integral_constant<int, ST>, the stage's index in its
+    // super-block when the caller knows it at compile time (ST >= 0), else -1
+    auto load_stage = [&](uint32_t s, GemmRegs<DT, XCH> &R, auto stc) {
+        constexpr int STC = decltype(stc)::value;
+        const uint32_t kb = kb_lo + (s >> 2), st = STC >= 0 ? (uint32_t)STC : (s & 3u), k0 = kb * 256u + st * GSK;
 #pragma unroll
         for (int i = 0; i < XCH; i++) {
             const uint32_t idx = tid + NTH * i, row = idx >> 3, c = idx & 7u;
@@ -313,23 +334,19 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
         }
     };
 
-    auto dequant_stage = [&](uint32_t s, const GemmRegs<DT, XCH> &R, int b) {
-        const uint32_t kb = s >> 2, st = s & 3u;   // kb relative to the split (LDS slot parity only)
+    auto dequant_stage = [&](uint32_t s, const GemmRegs<DT, XCH> &R, int b, auto stc) {
+        constexpr int STC = decltype(stc)::value;
+        // kb relative to the split (LDS slot parity only)
+        const uint32_t kb = s >> 2, st = STC >= 0 ? (uint32_t)STC : (s & 3u);
 #pragma unroll
         for (int i = 0; i < XCH; i++) {
             const uint32_t idx = tid + NTH * i, row = idx >> 3, c = idx & 7u;
-            if constexpr (Q4 || B32 || Q8K) {
-                // rows past M are stored as zeros with a mask: the select
-                // below compiles to branches and register copies around every
-                // stage (10% at M = 512); Q6_K keeps it, its masks spill
-                const uint32_t mk = 0u - (uint32_t)(m0 + row < M);
-                *reinterpret_cast<uint4 *>(sx[b] + row * GLD + 8u * c) =
-                    make_uint4(R.x[i].x & mk, R.x[i].y & mk, R.x[i].z & mk, R.x[i].w & mk);
-            } else {
-                *reinterpret_cast<uint4 *>(sx[b] + row * GLD + 8u * c) = m0 + row < M ? R.x[i] : make_uint4(0, 0, 0, 0);
-            }
+            // copied element by element: storing R.x[i] whole kept the
+            // register staging in scratch memory (80-450 bytes per lane)
+            const uint4 v = R.x[i];
+            *reinterpret_cast<uint4 *>(sx[b] + swz<Q4>(row, c)) = make_uint4(v.x, v.y, v.z, v.w);
         }
-        _Float16 *dst = sw[b] + wr * GLD;
+        _Float16 *wt = sw[b];
         uint4 o[4];
         if constexpr (Q8K) {
             uint32_t outw[16];
@@ -339,12 +356,11 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
                 outw[2 * t] = u8pair_to_f16((q & 0x00FF00FFu) ^ 0x00800080u, (_Float16)128.0f);
                 outw[2 * t + 1] = u8pair_to_f16(((q >> 8) & 0x00FF00FFu) ^ 0x00800080u, (_Float16)128.0f);
             }
-            const uint32_t wk = 0u - (uint32_t)wrow_ok;
 #pragma unroll
             for (int c = 0; c < 4; c++)
-                *reinterpret_cast<uint4 *>(dst + 32u * part + 8u * c) =
-                    make_uint4(outw[4 * c] & wk, outw[4 * c + 1] & wk, outw[4 * c + 2] & wk, outw[4 * c + 3] & wk);
-            if (st == 0 && part == 0) sd[kb & 1u][0][wr] = wrow_ok ? __builtin_bit_cast(float, R.d[0]) : 0.f;
+                *reinterpret_cast<uint4 *>(wt + swz<Q4>(wr, 4u * part + c)) =
+                    make_uint4(outw[4 * c], outw[4 * c + 1], outw[4 * c + 2], outw[4 * c + 3]);
+            if (st == 0 && part == 0) sd[kb & 1u][0][wr] = __builtin_bit_cast(float, R.d[0]);
         } else if constexpr (B32) {
             // d, then the quants from byte 2 of the block (mqb = 0: the block
             // starts at raw dword 0; mqb = 2: at its upper half)
@@ -373,12 +389,11 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
                     outw[4 * t + 3] = u8pair_to_f16(__builtin_amdgcn_perm(0u, hi, 0x0C030C02u), (_Float16)8.0f);
                 }
             }
-            const uint32_t wk = 0u - (uint32_t)wrow_ok;
 #pragma unroll
             for (int c = 0; c < 4; c++)
-                *reinterpret_cast<uint4 *>(dst + 32u * part + 8u * c) =
-                    make_uint4(outw[4 * c] & wk, outw[4 * c + 1] & wk, outw[4 * c + 2] & wk, outw[4 * c + 3] & wk);
-            sd[b][part][wr] = wrow_ok ? f16_bits(dbits) : 0.f;
+                *reinterpret_cast<uint4 *>(wt + swz<Q4>(wr, 4u * part + c)) =
+                    make_uint4(outw[4 * c], outw[4 * c + 1], outw[4 * c + 2], outw[4 * c + 3]);
+            sd[b][part][wr] = f16_bits(dbits);
         } else if constexpr (Q4) {
             // 6-bit scales of sub-blocks 2st (low nibbles) and 2st+1 (high),
             // get_scale_min_k4 (dequant.rs:176-190)
@@ -419,15 +434,12 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
             o[1] = make_uint4(lo[4], lo[5], lo[6], lo[7]);
             o[2] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
             o[3] = make_uint4(hi[4], hi[5], hi[6], hi[7]);
-            const uint32_t wk = 0u - (uint32_t)wrow_ok;
-#pragma unroll
-            for (int c = 0; c < 4; c++) o[c] = make_uint4(o[c].x & wk, o[c].y & wk, o[c].z & wk, o[c].w & wk);
             // this thread's 16 bytes: k = 16 part + 0..15 (low), 32 + 16 part + 0..15 (high)
-            *reinterpret_cast<uint4 *>(dst + 16u * part) = o[0];
-            *reinterpret_cast<uint4 *>(dst + 16u * part + 8u) = o[1];
-            *reinterpret_cast<uint4 *>(dst + 32u + 16u * part) = o[2];
-            *reinterpret_cast<uint4 *>(dst + 32u + 16u * part + 8u) = o[3];
-            if (st == 0 && part == 0) sd[kb & 1u][0][wr] = wrow_ok ? f16_bits(hd.x) * 16384.0f : 0.f;
+            *reinterpret_cast<uint4 *>(wt + swz<Q4>(wr, 2u * part)) = o[0];
+            *reinterpret_cast<uint4 *>(wt + swz<Q4>(wr, 2u * part + 1u)) = o[1];
+            *reinterpret_cast<uint4 *>(wt + swz<Q4>(wr, 4u + 2u * part)) = o[2];
+            *reinterpret_cast<uint4 *>(wt + swz<Q4>(wr, 5u + 2u * part)) = o[3];
+            if (st == 0 && part == 0) sd[kb & 1u][0][wr] = f16_bits(hd.x) * 16384.0f;
         } else {
             // Q6_K (dequant.rs:340-372): k = 32 part + l, quarter g = 2(st&1)+part of half st/2
             uint32_t ql[8], qh[8], scw[1], dw[1];
@@ -453,11 +465,10 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
             }
 #pragma unroll
             for (int c = 0; c < 4; c++) {
-                const uint4 v = wrow_ok ? make_uint4(outw[4 * c], outw[4 * c + 1], outw[4 * c + 2], outw[4 * c + 3])
-                                        : make_uint4(0, 0, 0, 0);
-                *reinterpret_cast<uint4 *>(dst + 32u * part + 8u * c) = v;
+                *reinterpret_cast<uint4 *>(wt + swz<Q4>(wr, 4u * part + c)) =
+                    make_uint4(outw[4 * c], outw[4 * c + 1], outw[4 * c + 2], outw[4 * c + 3]);
             }
-            if (st == 0 && part == 0) sd[kb & 1u][0][wr] = wrow_ok ? f16_bits(dw[0]) : 0.f;
+            if (st == 0 && part == 0) sd[kb & 1u][0][wr] = f16_bits(dw[0]);
         }
     };
 
@@ -470,12 +481,11 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
             half8 a[TM], bw[4];
 #pragma unroll
             for (int i = 0; i < TM; i++)
-                a[i] = *reinterpret_cast<const half8 *>(sx[b] + (wm * (BM / 2) + i * 16 + (lane & 15u)) * GLD +
-                                                        ks * 32 + 8u * (lane >> 4));
+                a[i] = *reinterpret_cast<const half8 *>(
+                    sx[b] + swz<Q4>(wm * (BM / 2) + i * 16 + (lane & 15u), ks * 4 + (lane >> 4)));
 #pragma unroll
             for (int j = 0; j < 4; j++)
-                bw[j] = *reinterpret_cast<const half8 *>(sw[b] + (wn * 64 + j * 16 + (lane & 15u)) * GLD + ks * 32 +
-                                                         8u * (lane >> 4));
+                bw[j] = *reinterpret_cast<const half8 *>(sw[b] + swz<Q4>(wn * 64 + j * 16 + (lane & 15u), ks * 4 + (lane >> 4)));
             if constexpr (B32) {
                 // one k-step is one block: acc += d[r][block] * (its MFMA from zero)
 #pragma unroll
@@ -512,10 +522,10 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
     };
 
     GemmRegs<DT, XCH> R0, R1;
-    load_stage(0, R0);
-    load_stage(1, R1);
-    dequant_stage(0, R0, 0);
-    load_stage(2 < S ? 2 : S - 1, R0);
+    load_stage(0, R0, std::integral_constant<int, 0>{});
+    load_stage(1, R1, std::integral_constant<int, 1>{});
+    dequant_stage(0, R0, 0, std::integral_constant<int, 0>{});
+    load_stage(2, R0, std::integral_constant<int, 2>{});   // S >= 4
     __syncthreads();
     // Q4_K, Q5_K, Q8_K: one super-block (four stages) per pass; stage t computes out of
     // LDS buffer t & 1 while stage t + 1 is dequantized into the other and
@@ -528,49 +538,50 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
     // which nothing reads any more, and the load re-reads stage S - 1): a
     // branch there would make the compiler wait for every load in flight at
     // the loop head instead of only for the stage about to be dequantized.
+    const std::integral_constant<int, -1> rt{};   // stage index known only at run time
     const std::integral_constant<bool, true> opens{};
     const std::integral_constant<bool, false> cont{};
     if constexpr (SBP) {
         for (uint32_t s = 0; s < S; s += 4) {
             compute(0, opens);
-            dequant_stage(s + 1, R1, 1);
-            load_stage(s + 3 < S ? s + 3 : S - 1, R1);
+            dequant_stage(s + 1, R1, 1, std::integral_constant<int, 1>{});
+            load_stage(s + 3 < S ? s + 3 : S - 1, R1, std::integral_constant<int, 3>{});
             __syncthreads();
             compute(1, cont);
-            dequant_stage(s + 2, R0, 0);
-            load_stage(s + 4 < S ? s + 4 : S - 1, R0);
+            dequant_stage(s + 2, R0, 0, std::integral_constant<int, 2>{});
+            load_stage(s + 4 < S ? s + 4 : S - 1, R0, std::integral_constant<int, 0>{});
             __syncthreads();
             compute(0, cont);
-            dequant_stage(s + 3, R1, 1);
-            load_stage(s + 5 < S ? s + 5 : S - 1, R1);
+            dequant_stage(s + 3, R1, 1, std::integral_constant<int, 3>{});
+            load_stage(s + 5 < S ? s + 5 : S - 1, R1, std::integral_constant<int, 1>{});
             __syncthreads();
             compute(1, cont);
             block_done(s >> 2);
-            dequant_stage(s + 4, R0, 0);
-            load_stage(s + 6 < S ? s + 6 : S - 1, R0);
+            dequant_stage(s + 4, R0, 0, std::integral_constant<int, 0>{});
+            load_stage(s + 6 < S ? s + 6 : S - 1, R0, std::integral_constant<int, 2>{});
             __syncthreads();
         }
     } else if constexpr (B32) {
         for (uint32_t s = 0; s < S; s += 2) {
             compute(0, cont);
-            dequant_stage(s + 1, R1, 1);
-            load_stage(s + 3 < S ? s + 3 : S - 1, R1);
+            dequant_stage(s + 1, R1, 1, rt);
+            load_stage(s + 3 < S ? s + 3 : S - 1, R1, rt);
             __syncthreads();
             compute(1, cont);
-            dequant_stage(s + 2, R0, 0);
-            load_stage(s + 4 < S ? s + 4 : S - 1, R0);
+            dequant_stage(s + 2, R0, 0, rt);
+            load_stage(s + 4 < S ? s + 4 : S - 1, R0, rt);
             __syncthreads();
         }
     } else {
         for (uint32_t s = 0; s < S; s += 2) {
             compute(0, cont);
-            dequant_stage(s + 1, R1, 1);
-            load_stage(s + 3 < S ? s + 3 : S - 1, R1);
+            dequant_stage(s + 1, R1, 1, rt);
+            load_stage(s + 3 < S ? s + 3 : S - 1, R1, rt);
             __syncthreads();
             compute(1, cont);
             if (((s + 1) & 3u) == 3u) block_done((s + 1) >> 2);
-            dequant_stage(s + 2, R0, 0);
-            load_stage(s + 4 < S ? s + 4 : S - 1, R0);
+            dequant_stage(s + 2, R0, 0, rt);
+            load_stage(s + 4 < S ? s + 4 : S - 1, R0, rt);
             __syncthreads();
         }
     }
@@ -764,8 +775,9 @@ void launch_gemm_bn(hipStream_t s, const GemmPass &p) {
     if (p.tail)
         hipLaunchKernelGGL(gemm_zero_tiles_kernel, dim3(p.tail * (bm / 8)), dim3(256), 0, s, p.y, p.m, p.n,
                            tiles - p.tail, nt, bm, (uint32_t)BN);
+    static const size_t pad = (size_t)env_int("YULE_GEMM_LDS_PAD_KB", 0) * 1024;
     if (p.m <= 64) {
-        hipLaunchKernelGGL((gemm_kernel<DT, 64, BN>), dim3(grid), dim3(2 * BN), 0, s, p.w, p.xh, p.y, p.xs_hi,
+        hipLaunchKernelGGL((gemm_kernel<DT, 64, BN>), dim3(grid), dim3(2 * BN), pad, s, p.w, p.xh, p.y, p.xs_hi,
                            p.xs_lo, p.rowscale, p.m, p.n, p.k, remap, p.tail, p.accumulate);
     } else {
         hipLaunchKernelGGL((gemm_kernel<DT, 128, BN>), dim3(grid), dim3(2 * BN), 0, s, p.w, p.xh, p.y, p.xs_hi,
