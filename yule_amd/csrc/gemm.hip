@@ -36,9 +36,10 @@
 //    sub-block sums (at most 32 * 2^10) fit f16 too; the epilogue multiplies
 //    each Y row by the inverse power of two, which is exact.  f32 X
 //    (yule_hip_quantized_gemm_f32) is split the same way into f16 hi + lo
-//    (x = hi + lo to ~2^-22) and runs as two products, the second adding into
-//    Y: the accuracy of the f32 matvec, for callers that need it (prefill
-//    whose results must match token-by-token decode).
+//    (x = hi + lo to ~2^-22) and each workgroup sweeps its K range twice,
+//    against hi and then lo, into the same accumulators: the accuracy of the
+//    f32 matvec, for callers that need it (prefill whose results must match
+//    token-by-token decode), in one launch.
 //
 #include <mutex>
 #include <type_traits>
@@ -211,11 +212,11 @@ __device__ __forceinline__ uint32_t u8pair_to_f16(uint32_t v, _Float16 bias) {
 // fixed order by gemm_reduce_kernel, so results do not depend on timing).
 // Q4_K, Q8_0 and Q4_0 run two waves per SIMD (Q4_K's register budget holds
 // with a few spilled bytes); Q6_K's larger dequant state keeps it at one.
-template <uint32_t DT, int BM, int BN>
+template <uint32_t DT, int BM, int BN, int SWEEPS>
 __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YULE_DTYPE_Q6_K ? 1 : 2))) void gemm_kernel(
-    const uint8_t *__restrict__ w, const _Float16 *__restrict__ xh, float *__restrict__ y,
-    const _Float16 *__restrict__ xs_hi, const _Float16 *__restrict__ xs_lo, const float *__restrict__ rowscale,
-    uint32_t M, uint32_t N, uint32_t K, uint32_t xcd_remap, uint32_t tail, uint32_t accumulate) {
+    const uint8_t *__restrict__ w, const _Float16 *__restrict__ xh, const _Float16 *__restrict__ xl,
+    float *__restrict__ y, const _Float16 *__restrict__ xs_hi, const _Float16 *__restrict__ xs_lo,
+    const float *__restrict__ rowscale, uint32_t M, uint32_t N, uint32_t K, uint32_t xcd_remap, uint32_t tail) {
     constexpr bool Q5 = DT == YULE_DTYPE_Q5_K;
     constexpr bool Q4 = DT == YULE_DTYPE_Q4_K || Q5;   // Q5_K: Q4_K plus a fifth bit per weight from qh
     constexpr bool B32 = DT == YULE_DTYPE_Q8_0 || DT == YULE_DTYPE_Q4_0;   // 32-weight blocks, d per block
@@ -290,6 +291,9 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
 
     // stc: std::integral_constant<int, ST>, the stage's index in its
     // super-block when the caller knows it at compile time (ST >= 0), else -1
+    // X of the current sweep: xh, then (f32 X) xl, both into the same
+    // accumulators (the weight tile's second sweep reads it from L2)
+    const _Float16 *xcur = xh;
     auto load_stage = [&](uint32_t s, GemmRegs<DT, XCH> &R, auto stc) {
         constexpr int STC = decltype(stc)::value;
         const uint32_t kb = kb_lo + (s >> 2), st = STC >= 0 ? (uint32_t)STC : (s & 3u), k0 = kb * 256u + st * GSK;
@@ -297,7 +301,7 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
         for (int i = 0; i < XCH; i++) {
             const uint32_t idx = tid + NTH * i, row = idx >> 3, c = idx & 7u;
             const uint32_t m = m0 + row < M ? m0 + row : M - 1u;
-            R.x[i] = *reinterpret_cast<const uint4 *>(xh + (size_t)m * K + k0 + 8u * c);
+            R.x[i] = *reinterpret_cast<const uint4 *>(xcur + (size_t)m * K + k0 + 8u * c);
         }
         if constexpr (B32) {
             // block 2 (kb*4 + st) + part of the row: k = 64 stage + 32 part
@@ -521,6 +525,12 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
         }
     };
 
+    const std::integral_constant<int, -1> rt{};   // stage index known only at run time
+    const std::integral_constant<bool, true> opens{};
+    const std::integral_constant<bool, false> cont{};
+#pragma unroll
+    for (int sweep = 0; sweep < SWEEPS; sweep++) {
+    xcur = sweep ? xl : xh;
     GemmRegs<DT, XCH> R0, R1;
     load_stage(0, R0, std::integral_constant<int, 0>{});
     load_stage(1, R1, std::integral_constant<int, 1>{});
@@ -538,9 +548,6 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
     // which nothing reads any more, and the load re-reads stage S - 1): a
     // branch there would make the compiler wait for every load in flight at
     // the loop head instead of only for the stage about to be dequantized.
-    const std::integral_constant<int, -1> rt{};   // stage index known only at run time
-    const std::integral_constant<bool, true> opens{};
-    const std::integral_constant<bool, false> cont{};
     if constexpr (SBP) {
         for (uint32_t s = 0; s < S; s += 4) {
             compute(0, opens);
@@ -585,6 +592,7 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
             __syncthreads();
         }
     }
+    }   // sweeps
 
     if (Q4 && xs_hi) {   // (no sums: the second, lo, product of an f32 X)
         // min term: acc -= sum_j xsum[m][j] * (dmin*mn)[r][j] over the K/32
@@ -675,7 +683,6 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
                 if (m < M && r < N) {
                     const float v = acc[i][j][e] * rowscale[m];   // the row's power of two back out: exact
                     if (halves) unsafeAtomicAdd(y + (size_t)m * N + r, v);
-                    else if (accumulate && splits == 1) y[(size_t)m * N + r] += v;
                     else y[(size_t)m * N + r] = v;
                 }
             }
@@ -696,14 +703,13 @@ __global__ void gemm_zero_tiles_kernel(float *__restrict__ y, uint32_t M, uint32
     }
 }
 
-// y[i] = sum over z of part[z][i], z ascending (accumulate: y[i] + that sum)
-__global__ void gemm_reduce_kernel(const float *__restrict__ part, float *__restrict__ y, uint64_t n, uint32_t ks,
-                                   uint32_t accumulate) {
+// y[i] = sum over z of part[z][i], z ascending
+__global__ void gemm_reduce_kernel(const float *__restrict__ part, float *__restrict__ y, uint64_t n, uint32_t ks) {
     const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
     float s = part[i];
     for (uint32_t z = 1; z < ks; z++) s += part[(uint64_t)z * n + i];
-    y[i] = accumulate ? y[i] + s : s;
+    y[i] = s;
 }
 
 }  // namespace yule
@@ -755,15 +761,15 @@ uint32_t gemm_tail(uint32_t m, uint32_t n, uint32_t k, uint32_t bn, uint32_t ks)
     return r <= round / 2 ? r : 0;
 }
 
-// One product over the tile grid.  Y rows are scaled by rowscale; with
-// accumulate the product adds into Y (the lo pass of an f32 X): its tiles run
-// whole (no K-half tail, whose atomic adds would then round in either order).
+// One product over the tile grid: X in f16 (xh), or for f32 X its hi and lo
+// halves (xh, xl) swept in turn into the same accumulators.  Y rows are
+// scaled by rowscale.
 struct GemmPass {
     const uint8_t *w;
-    const _Float16 *xh, *xs_hi, *xs_lo;
+    const _Float16 *xh, *xl, *xs_hi, *xs_lo;
     const float *rowscale;
     float *y;
-    uint32_t m, n, k, ks, bn, tail, accumulate;
+    uint32_t m, n, k, ks, bn, tail;
 };
 
 template <uint32_t DT, int BN>
@@ -776,12 +782,19 @@ void launch_gemm_bn(hipStream_t s, const GemmPass &p) {
         hipLaunchKernelGGL(gemm_zero_tiles_kernel, dim3(p.tail * (bm / 8)), dim3(256), 0, s, p.y, p.m, p.n,
                            tiles - p.tail, nt, bm, (uint32_t)BN);
     static const size_t pad = (size_t)env_int("YULE_GEMM_LDS_PAD_KB", 0) * 1024;
-    if (p.m <= 64) {
-        hipLaunchKernelGGL((gemm_kernel<DT, 64, BN>), dim3(grid), dim3(2 * BN), pad, s, p.w, p.xh, p.y, p.xs_hi,
-                           p.xs_lo, p.rowscale, p.m, p.n, p.k, remap, p.tail, p.accumulate);
+    if (p.xl) {   // f32 X: the hi and lo sweeps
+        if (p.m <= 64)
+            hipLaunchKernelGGL((gemm_kernel<DT, 64, BN, 2>), dim3(grid), dim3(2 * BN), pad, s, p.w, p.xh, p.xl, p.y,
+                               p.xs_hi, p.xs_lo, p.rowscale, p.m, p.n, p.k, remap, p.tail);
+        else
+            hipLaunchKernelGGL((gemm_kernel<DT, 128, BN, 2>), dim3(grid), dim3(2 * BN), 0, s, p.w, p.xh, p.xl, p.y,
+                               p.xs_hi, p.xs_lo, p.rowscale, p.m, p.n, p.k, remap, p.tail);
+    } else if (p.m <= 64) {
+        hipLaunchKernelGGL((gemm_kernel<DT, 64, BN, 1>), dim3(grid), dim3(2 * BN), pad, s, p.w, p.xh, p.xl, p.y, p.xs_hi,
+                           p.xs_lo, p.rowscale, p.m, p.n, p.k, remap, p.tail);
     } else {
-        hipLaunchKernelGGL((gemm_kernel<DT, 128, BN>), dim3(grid), dim3(2 * BN), 0, s, p.w, p.xh, p.y, p.xs_hi,
-                           p.xs_lo, p.rowscale, p.m, p.n, p.k, remap, p.tail, p.accumulate);
+        hipLaunchKernelGGL((gemm_kernel<DT, 128, BN, 1>), dim3(grid), dim3(2 * BN), 0, s, p.w, p.xh, p.xl, p.y, p.xs_hi,
+                           p.xs_lo, p.rowscale, p.m, p.n, p.k, remap, p.tail);
     }
 }
 
@@ -852,15 +865,12 @@ static int gemm_enqueue(hipStream_t s, const uint8_t *w, const void *x, bool f32
                            n_cols);
     int rc = check_launch("quantized_gemm: x pre-pass");
     if (rc) return rc;
-    for (int pass = 0; pass < (f32x ? 2 : 1); pass++) {
-        GemmPass p{w, pass ? xl : xh, pass ? nullptr : xs_hi, pass ? nullptr : xs_lo, rowscale,
-                   g.ks > 1 ? part : y, m, n_rows, n_cols, g.ks, g.bn, pass ? 0u : g.tail, (uint32_t)pass};
-        if ((rc = launch_gemm_dt(s, dtype, p))) return rc;
-        if (g.ks > 1) {
-            hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)((g.n_y + 255) / 256)), dim3(256), 0, s, part, y,
-                               (uint64_t)g.n_y, g.ks, (uint32_t)pass);
-            if ((rc = check_launch("quantized_gemm: split-K reduction"))) return rc;
-        }
+    const GemmPass p{w, xh, xl, xs_hi, xs_lo, rowscale, g.ks > 1 ? part : y, m, n_rows, n_cols, g.ks, g.bn, g.tail};
+    if ((rc = launch_gemm_dt(s, dtype, p))) return rc;
+    if (g.ks > 1) {
+        hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)((g.n_y + 255) / 256)), dim3(256), 0, s, part, y,
+                           (uint64_t)g.n_y, g.ks);
+        if ((rc = check_launch("quantized_gemm: split-K reduction"))) return rc;
     }
     return YULE_OK;
 }
