@@ -438,6 +438,25 @@ def profile_decode(hip, n):
     print(json.dumps({"steps": n, "ms_per_step_ungraphed": round(ms, 4)}), flush=True)
 
 
+def profile_prefill(hip, n):
+    """N batched prefills of the 128-token prompt through the TinyLlama-shaped
+    runner (each projection one f32-input GEMM), for rocprofv3."""
+    from yule_amd.backend import HipRunner
+    from yule_amd.model import TINYLLAMA, SyntheticModel
+    model = SyntheticModel.generate(TINYLLAMA, seed=0)
+    prompt = synth.uniform_tokens(1, 128, TINYLLAMA.vocab)
+    run = HipRunner(hip, model)
+    hip.synchronize()
+    hip.timer_start()
+    for _ in range(n):
+        run.reset()
+        run.prefill_batched(prompt)
+    ms = hip.timer_stop() / n
+    run.close()
+    print(json.dumps({"prefills": n, "ms_per_prefill": round(ms, 3),
+                      "prefill_tok_s": round(len(prompt) * 1000.0 / ms, 1)}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -459,6 +478,8 @@ def main():
                     help="only measure the single-launch streaming-read rate against launch size (JSON line)")
     ap.add_argument("--profile-decode", type=int, default=0, metavar="N",
                     help="only run N TinyLlama decode steps with kernels launched one by one (for rocprofv3)")
+    ap.add_argument("--profile-prefill", type=int, default=0, metavar="N",
+                    help="only run N batched 128-token TinyLlama prefills (for rocprofv3)")
     args = ap.parse_args()
     global USE_GRAPH
     USE_GRAPH = not args.no_graph
@@ -481,6 +502,9 @@ def main():
         return
     if args.profile_decode:
         profile_decode(hip, args.profile_decode)
+        return
+    if args.profile_prefill:
+        profile_prefill(hip, args.profile_prefill)
         return
     log(f"device: {info.name}, {info.compute_units} CUs, {info.memory_bytes / 2**30:.0f} GiB")
 

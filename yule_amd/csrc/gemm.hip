@@ -528,9 +528,9 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
     const std::integral_constant<int, -1> rt{};   // stage index known only at run time
     const std::integral_constant<bool, true> opens{};
     const std::integral_constant<bool, false> cont{};
-#pragma unroll
-    for (int sweep = 0; sweep < SWEEPS; sweep++) {
-    xcur = sweep ? xl : xh;
+    // one sweep over this split's K range (called once, or for f32 X twice:
+    // xh, then xl, into the same accumulators)
+    auto sweep = [&]() {
     GemmRegs<DT, XCH> R0, R1;
     load_stage(0, R0, std::integral_constant<int, 0>{});
     load_stage(1, R1, std::integral_constant<int, 1>{});
@@ -592,7 +592,12 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
             __syncthreads();
         }
     }
-    }   // sweeps
+    };
+    sweep();
+    if constexpr (SWEEPS == 2) {
+        xcur = xl;
+        sweep();
+    }
 
     if (Q4 && xs_hi) {   // (no sums: the second, lo, product of an f32 X)
         // min term: acc -= sum_j xsum[m][j] * (dmin*mn)[r][j] over the K/32
@@ -781,16 +786,15 @@ void launch_gemm_bn(hipStream_t s, const GemmPass &p) {
     if (p.tail)
         hipLaunchKernelGGL(gemm_zero_tiles_kernel, dim3(p.tail * (bm / 8)), dim3(256), 0, s, p.y, p.m, p.n,
                            tiles - p.tail, nt, bm, (uint32_t)BN);
-    static const size_t pad = (size_t)env_int("YULE_GEMM_LDS_PAD_KB", 0) * 1024;
     if (p.xl) {   // f32 X: the hi and lo sweeps
         if (p.m <= 64)
-            hipLaunchKernelGGL((gemm_kernel<DT, 64, BN, 2>), dim3(grid), dim3(2 * BN), pad, s, p.w, p.xh, p.xl, p.y,
+            hipLaunchKernelGGL((gemm_kernel<DT, 64, BN, 2>), dim3(grid), dim3(2 * BN), 0, s, p.w, p.xh, p.xl, p.y,
                                p.xs_hi, p.xs_lo, p.rowscale, p.m, p.n, p.k, remap, p.tail);
         else
             hipLaunchKernelGGL((gemm_kernel<DT, 128, BN, 2>), dim3(grid), dim3(2 * BN), 0, s, p.w, p.xh, p.xl, p.y,
                                p.xs_hi, p.xs_lo, p.rowscale, p.m, p.n, p.k, remap, p.tail);
     } else if (p.m <= 64) {
-        hipLaunchKernelGGL((gemm_kernel<DT, 64, BN, 1>), dim3(grid), dim3(2 * BN), pad, s, p.w, p.xh, p.xl, p.y, p.xs_hi,
+        hipLaunchKernelGGL((gemm_kernel<DT, 64, BN, 1>), dim3(grid), dim3(2 * BN), 0, s, p.w, p.xh, p.xl, p.y, p.xs_hi,
                            p.xs_lo, p.rowscale, p.m, p.n, p.k, remap, p.tail);
     } else {
         hipLaunchKernelGGL((gemm_kernel<DT, 128, BN, 1>), dim3(grid), dim3(2 * BN), 0, s, p.w, p.xh, p.xl, p.y, p.xs_hi,
