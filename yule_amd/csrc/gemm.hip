@@ -736,10 +736,18 @@ uint32_t gemm_bn(uint32_t m, uint32_t dtype) {
     return m >= 1024 || (dtype == YULE_DTYPE_Q6_K && m >= 512) ? 256u : 128u;
 }
 
-uint32_t gemm_splits(uint32_t m, uint32_t n, uint32_t k, uint32_t bn) {
+// Tile height: 64 rows for M <= 64, and for f32 X up to M = 128 (its two
+// sweeps make the 128-row tile spill; the 64-row one keeps three
+// workgroups per CU and twice the workgroups); 128 otherwise.
+// YULE_GEMM_F32_BM64 sets that f32 bound.
+uint32_t gemm_bm(uint32_t m, bool f32x) {
+    static const int env = env_int("YULE_GEMM_F32_BM64", 128);
+    return m <= 64 || (f32x && m <= (uint32_t)env) ? 64u : 128u;
+}
+
+uint32_t gemm_splits(uint32_t m, uint32_t n, uint32_t k, uint32_t bn, uint32_t bm) {
     static const int env = env_int("YULE_GEMM_SPLITS", 0);
     if (env > 0) return (uint32_t)env < k / 256 ? (uint32_t)env : k / 256;
-    const uint32_t bm = m <= 64 ? 64 : 128;
     const uint32_t tiles = ((n + bn - 1) / bn) * ((m + bm - 1) / bm);
     const uint32_t cus = (uint32_t)device_cus();
     if (tiles >= cus) return 1;
@@ -755,10 +763,9 @@ uint32_t gemm_splits(uint32_t m, uint32_t n, uint32_t k, uint32_t bn) {
 // most half a round, running them as K halves fills it and ends the
 // launch earlier (5% on 14336 x 4096 at M = 2048).  Needs two super-blocks
 // per row.  YULE_GEMM_TAIL=0 turns it off.
-uint32_t gemm_tail(uint32_t m, uint32_t n, uint32_t k, uint32_t bn, uint32_t ks) {
+uint32_t gemm_tail(uint32_t m, uint32_t n, uint32_t k, uint32_t bn, uint32_t bm, uint32_t ks) {
     static const bool env = env_flag("YULE_GEMM_TAIL", true);
     if (!env || ks > 1 || k / 256 < 2) return 0;
-    const uint32_t bm = m <= 64 ? 64 : 128;
     const uint32_t tiles = ((n + bn - 1) / bn) * ((m + bm - 1) / bm);
     const uint32_t round = (uint32_t)device_cus() * (bn == 256 ? 1u : 2u);
     if (tiles <= round) return 0;
@@ -774,26 +781,26 @@ struct GemmPass {
     const _Float16 *xh, *xl, *xs_hi, *xs_lo;
     const float *rowscale;
     float *y;
-    uint32_t m, n, k, ks, bn, tail;
+    uint32_t m, n, k, ks, bn, bm, tail;
 };
 
 template <uint32_t DT, int BN>
 void launch_gemm_bn(hipStream_t s, const GemmPass &p) {
     static const uint32_t remap = env_flag("YULE_GEMM_XCD_REMAP", false) ? 1u : 0u;
     const uint32_t nt = (p.n + BN - 1) / BN;
-    const uint32_t bm = p.m <= 64 ? 64 : 128, tiles = nt * ((p.m + bm - 1) / bm);
+    const uint32_t bm = p.bm, tiles = nt * ((p.m + bm - 1) / bm);
     const uint32_t grid = p.tail ? tiles + p.tail : tiles * p.ks;
     if (p.tail)
         hipLaunchKernelGGL(gemm_zero_tiles_kernel, dim3(p.tail * (bm / 8)), dim3(256), 0, s, p.y, p.m, p.n,
                            tiles - p.tail, nt, bm, (uint32_t)BN);
     if (p.xl) {   // f32 X: the hi and lo sweeps
-        if (p.m <= 64)
+        if (bm == 64)
             hipLaunchKernelGGL((gemm_kernel<DT, 64, BN, 2>), dim3(grid), dim3(2 * BN), 0, s, p.w, p.xh, p.xl, p.y,
                                p.xs_hi, p.xs_lo, p.rowscale, p.m, p.n, p.k, remap, p.tail);
         else
             hipLaunchKernelGGL((gemm_kernel<DT, 128, BN, 2>), dim3(grid), dim3(2 * BN), 0, s, p.w, p.xh, p.xl, p.y,
                                p.xs_hi, p.xs_lo, p.rowscale, p.m, p.n, p.k, remap, p.tail);
-    } else if (p.m <= 64) {
+    } else if (bm == 64) {
         hipLaunchKernelGGL((gemm_kernel<DT, 64, BN, 1>), dim3(grid), dim3(2 * BN), 0, s, p.w, p.xh, p.xl, p.y, p.xs_hi,
                            p.xs_lo, p.rowscale, p.m, p.n, p.k, remap, p.tail);
     } else {
@@ -833,7 +840,7 @@ bool gemm_dtype_ok(uint32_t dtype) {
 struct GemmWork {
     size_t part_bytes, total;
     size_t n_x, n_sub, n_y;
-    uint32_t ks, bn, tail;
+    uint32_t ks, bn, bm, tail;
     bool q4;
 };
 
@@ -841,8 +848,9 @@ static GemmWork gemm_work(uint32_t m, uint32_t n_rows, uint32_t n_cols, uint32_t
     GemmWork g;
     g.q4 = dtype == YULE_DTYPE_Q4_K || dtype == YULE_DTYPE_Q5_K;   // min term: X sub-block sums
     g.bn = gemm_bn(m, dtype);
-    g.ks = gemm_splits(m, n_rows, n_cols, g.bn);
-    g.tail = gemm_tail(m, n_rows, n_cols, g.bn, g.ks);
+    g.bm = gemm_bm(m, f32x);
+    g.ks = gemm_splits(m, n_rows, n_cols, g.bn, g.bm);
+    g.tail = gemm_tail(m, n_rows, n_cols, g.bn, g.bm, g.ks);
     g.n_x = (size_t)m * n_cols;
     g.n_sub = (size_t)m * (n_cols / 32);
     g.n_y = (size_t)m * n_rows;
@@ -869,7 +877,7 @@ static int gemm_enqueue(hipStream_t s, const uint8_t *w, const void *x, bool f32
                            n_cols);
     int rc = check_launch("quantized_gemm: x pre-pass");
     if (rc) return rc;
-    const GemmPass p{w, xh, xl, xs_hi, xs_lo, rowscale, g.ks > 1 ? part : y, m, n_rows, n_cols, g.ks, g.bn, g.tail};
+    const GemmPass p{w, xh, xl, xs_hi, xs_lo, rowscale, g.ks > 1 ? part : y, m, n_rows, n_cols, g.ks, g.bn, g.bm, g.tail};
     if ((rc = launch_gemm_dt(s, dtype, p))) return rc;
     if (g.ks > 1) {
         hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)((g.n_y + 255) / 256)), dim3(256), 0, s, part, y,
