@@ -197,7 +197,8 @@ int yule_hip_quantized_gemm(yule_hip_backend *be, yule_buffer weights, yule_buff
 
 /* The same product for f32 X [M][n_cols] (no counterpart in the reference):
  * each row is split into f16 hi + lo after its power-of-two scale
- * (x = hi + lo to ~2^-22) and Y = X_hi W + X_lo W, two MFMA products, so
+ * (x = hi + lo to ~2^-22) and Y = X_hi W + X_lo W, both products swept
+ * into the same accumulators in one launch, so
  * each row matches the f32 matvec of the same row to the matvec bar at f32
  * accuracy (the batched prefill of the runner, whose KV cache must equal
  * token-by-token decode's).  Same formats, shapes, aliasing rules and
