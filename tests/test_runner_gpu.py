@@ -217,6 +217,41 @@ def test_runner_prefill_batched_matches_oracle(hip, tiny, which):
     run.close()
 
 
+@pytest.mark.parametrize("scheme,dim,hd", [("Q6_K", 512, 64), ("Q8_0", 512, 128), ("Q4_0", 256, 32),
+                                            ("Q5_K", 512, 64), ("Q8_K", 512, 128)])
+def test_runner_prefill_batched_formats(hip, scheme, dim, hd):
+    """Batched prefill on every GEMM format and head sizes 32 to 128: a
+    one-token batch, a 33-token batch (ragged against the GEMM's 64-row
+    tiles), then decode steps over the cache they wrote; logits vs the
+    oracle (Q8_K, which Yule's CPU runner cannot run: the float64 forward).
+    An empty batch and one past the context length are refused."""
+    from yule_amd.model import LlamaConfig
+    cfg = LlamaConfig(n_layers=2, dim=dim, n_heads=dim // hd, n_kv_heads=2, ff_dim=512, vocab=512, max_seq=96)
+    m = SyntheticModel.generate(cfg, seed=23, scheme=scheme)
+    say(f"[runner] batched prefill, {scheme} dim {dim} hd {hd}")
+    ref = NpForward(m) if scheme == "Q8_K" else oracle.Runner(m, n_threads=4)
+    toks = synth.uniform_tokens(42, 44, cfg.vocab)
+    run = HipRunner(hip, m)
+    try:
+        got, want = run.prefill_batched(toks[:1]), ref.forward(int(toks[0]))
+        assert np.max(np.abs(got - want)) <= tolerance_bar(want)
+        got = run.prefill_batched(toks[1:34])
+        for t in toks[1:34]:
+            want = ref.forward(int(t))
+        assert run.pos == 34
+        assert np.max(np.abs(got - want)) <= tolerance_bar(want)
+        for i, t in enumerate(toks[34:]):
+            got, want = run.decode_step(int(t)), ref.forward(int(t))
+            assert np.max(np.abs(got - want)) <= tolerance_bar(want), f"decode step {i}"
+        with pytest.raises(YuleGpuError):
+            run.prefill_batched(np.zeros(0, np.uint32))
+        with pytest.raises(YuleGpuError, match="context"):
+            run.prefill_batched(synth.uniform_tokens(43, cfg.max_seq - run.pos + 1, cfg.vocab))
+        assert run.pos == 44
+    finally:
+        run.close()
+
+
 def test_runner_greedy_token_prefill_path(hip, tiny, monkeypatch):
     """generate_greedy with the token-by-token prompt pass (the runner's
     fallback when a projection has no batched path) gives the oracle's tokens,

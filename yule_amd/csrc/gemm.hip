@@ -235,6 +235,15 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
     __shared__ __align__(16) _Float16 sx[2][BM * GLD];
     __shared__ __align__(16) _Float16 sw[2][BN * GLD];
     __shared__ float sd[2][B32 ? 2 : 1][BN];   // d per weight row: super-block slot, or the stage's two blocks
+    // Q6_K with f32 X: the weight tile holds q - 32 and each row's four
+    // sub-block scales of the stage sit here as f16 pairs (16 * (sc >> 4),
+    // sc & 15); the MFMA B operand is then both halves of sc * (q - 32), each
+    // exact in f16 (|16 * (sc >> 4) * (q - 32)| <= 4096 in steps of 16,
+    // |(sc & 15) * (q - 32)| <= 480), accumulated by two MFMAs.  The single
+    // product sc * (q - 32) reaches 4096 and rounds above 2048; that rounding
+    // (<= 4.9e-4 relative on those weights) is kept for bf16 X.
+    constexpr bool X6 = DT == YULE_DTYPE_Q6_K && SWEEPS == 2;
+    __shared__ uint32_t ssc[X6 ? 2 : 1][X6 ? BN : 1][4];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t wm = wave / WNN, wn = wave % WNN;
     // Tile of this workgroup.  The grid is one-dimensional over
@@ -452,9 +461,17 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
             align_raw<4>(R.sc, R.msc, scw);
             align_raw<4>(R.d, R.md, dw);
             const uint32_t g = 2u * (st & 1u) + part, nib = 4u * (st & 1u), qsh = 2u * g;
-            const _Float16 sc0 = (_Float16)(float)(int8_t)(scw[0] & 0xFFu);
-            const _Float16 sc1 = (_Float16)(float)(int8_t)((scw[0] >> 8) & 0xFFu);
+            const int isc0 = (int8_t)(scw[0] & 0xFFu), isc1 = (int8_t)((scw[0] >> 8) & 0xFFu);
+            const _Float16 sc0 = (_Float16)(float)isc0, sc1 = (_Float16)(float)isc1;
             const h2v S0 = {sc0, sc0}, S1 = {sc1, sc1};
+            if constexpr (X6) {   // the stage's sub-blocks 2 part and 2 part + 1 of this row
+                auto pack = [](int sc) {
+                    const h2v v = {(_Float16)(float)(sc - (sc & 15)), (_Float16)(float)(sc & 15)};
+                    return __builtin_bit_cast(uint32_t, v);
+                };
+                ssc[b][wr][2u * part] = pack(isc0);
+                ssc[b][wr][2u * part + 1u] = pack(isc1);
+            }
             uint32_t outw[16];
             // four weights per dword: the 6-bit values q (byte lanes), paired
             // (q0, q2), (q1, q3) in the X order {0,2,1,3}, as f16 q - 32
@@ -464,8 +481,10 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
             for (int i = 0; i < 8; i++) {
                 const uint32_t q6 = ((ql[i] >> nib) & 0x0F0F0F0Fu) | (((qh[i] >> qsh) & 0x03030303u) << 4);
                 const h2v sc = i < 4 ? S0 : S1;   // weights 0-15 / 16-31 of the quarter
-                outw[2 * i] = pk_scale(u8pair_to_f16(q6 & 0x00FF00FFu, (_Float16)32.0f), sc);
-                outw[2 * i + 1] = pk_scale(u8pair_to_f16((q6 >> 8) & 0x00FF00FFu, (_Float16)32.0f), sc);
+                const uint32_t e = u8pair_to_f16(q6 & 0x00FF00FFu, (_Float16)32.0f);
+                const uint32_t o = u8pair_to_f16((q6 >> 8) & 0x00FF00FFu, (_Float16)32.0f);
+                outw[2 * i] = X6 ? e : pk_scale(e, sc);
+                outw[2 * i + 1] = X6 ? o : pk_scale(o, sc);
             }
 #pragma unroll
             for (int c = 0; c < 4; c++) {
@@ -502,6 +521,27 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
                     const float dr = sd[b][ks][wn * 64 + j * 16 + (lane & 15u)];
 #pragma unroll
                     for (int i = 0; i < TM; i++) acc[i][j] += dr * tmp[i][j];
+                }
+            } else if constexpr (X6) {
+                // this lane's 8 k lie in sub-block 2 ks + lane / 32 of the stage
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const uint32_t sp = ssc[b][wn * 64 + j * 16 + (lane & 15u)][2 * ks + (lane >> 5)];
+                    const h2v sh = {__builtin_bit_cast(h2v, sp).x, __builtin_bit_cast(h2v, sp).x};
+                    const h2v sl = {__builtin_bit_cast(h2v, sp).y, __builtin_bit_cast(h2v, sp).y};
+                    half8 b1, b2;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const h2v q = {bw[j][2 * e], bw[j][2 * e + 1]};
+                        const h2v p1 = q * sh, p2 = q * sl;
+                        b1[2 * e] = p1.x; b1[2 * e + 1] = p1.y;
+                        b2[2 * e] = p2.x; b2[2 * e + 1] = p2.y;
+                    }
+#pragma unroll
+                    for (int i = 0; i < TM; i++) {
+                        tmp[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b1, tmp[i][j], 0, 0, 0);
+                        tmp[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b2, tmp[i][j], 0, 0, 0);
+                    }
                 }
             } else {
 #pragma unroll
