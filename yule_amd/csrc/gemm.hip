@@ -764,8 +764,8 @@ using namespace yule;
 namespace {
 
 // Split count: none once the tiles alone fill every CU; below that, as many
-// splits as fit in one round of resident workgroups (two per CU), so that
-// small-M launches keep all CUs busy without a partial second round.
+// splits as fit in one round of resident workgroups (gemm_wgs_per_cu), so
+// that small-M launches keep all CUs busy without a partial second round.
 // Tile width along the weight rows: 256 (eight waves) halves the X bytes
 // each weight tile is multiplied against and measured 5-30% faster once M
 // fills the CUs with wide tiles (M >= 1024; Q6_K, whose dequant is dearer,
@@ -785,13 +785,19 @@ uint32_t gemm_bm(uint32_t m, bool f32x) {
     return m <= 64 || (f32x && m <= (uint32_t)env) ? 64u : 128u;
 }
 
-uint32_t gemm_splits(uint32_t m, uint32_t n, uint32_t k, uint32_t bn, uint32_t bm) {
+// Workgroups resident per CU: one for the 256-wide tiles and for Q6_K's
+// 128-row and two-sweep kernels (their registers), two otherwise.
+uint32_t gemm_wgs_per_cu(uint32_t dtype, uint32_t bm, uint32_t bn, bool f32x) {
+    return bn == 256 || (dtype == YULE_DTYPE_Q6_K && (bm == 128 || f32x)) ? 1u : 2u;
+}
+
+uint32_t gemm_splits(uint32_t m, uint32_t n, uint32_t k, uint32_t bn, uint32_t bm, uint32_t per_cu) {
     static const int env = env_int("YULE_GEMM_SPLITS", 0);
     if (env > 0) return (uint32_t)env < k / 256 ? (uint32_t)env : k / 256;
     const uint32_t tiles = ((n + bn - 1) / bn) * ((m + bm - 1) / bm);
     const uint32_t cus = (uint32_t)device_cus();
     if (tiles >= cus) return 1;
-    uint32_t ks = 2 * cus / tiles;
+    uint32_t ks = per_cu * cus / tiles;
     const uint32_t bpr = k / 256;
     return ks < 1 ? 1 : ks > bpr ? bpr : ks;
 }
@@ -889,7 +895,7 @@ static GemmWork gemm_work(uint32_t m, uint32_t n_rows, uint32_t n_cols, uint32_t
     g.q4 = dtype == YULE_DTYPE_Q4_K || dtype == YULE_DTYPE_Q5_K;   // min term: X sub-block sums
     g.bn = gemm_bn(m, dtype);
     g.bm = gemm_bm(m, f32x);
-    g.ks = gemm_splits(m, n_rows, n_cols, g.bn, g.bm);
+    g.ks = gemm_splits(m, n_rows, n_cols, g.bn, g.bm, gemm_wgs_per_cu(dtype, g.bm, g.bn, f32x));
     g.tail = gemm_tail(m, n_rows, n_cols, g.bn, g.bm, g.ks);
     g.n_x = (size_t)m * n_cols;
     g.n_sub = (size_t)m * (n_cols / 32);
