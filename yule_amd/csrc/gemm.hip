@@ -207,6 +207,12 @@ __device__ __forceinline__ uint32_t u8pair_to_f16(uint32_t v, _Float16 bias) {
     return __builtin_bit_cast(uint32_t, h);
 }
 
+// Weight matrices of one launch, stacked along Y's rows (one matrix: s1 = s2 = N)
+struct GemmW {
+    const uint8_t *w[3];
+    uint32_t s1, s2;
+};
+
 // Split-K: split z of `splits` takes super-blocks [kb_lo, kb_hi) and,
 // when splits > 1, writes its partial tile to y + z*M*N (summed in a
 // fixed order by gemm_reduce_kernel, so results do not depend on timing).
@@ -214,8 +220,7 @@ __device__ __forceinline__ uint32_t u8pair_to_f16(uint32_t v, _Float16 bias) {
 // with a few spilled bytes); Q6_K's larger dequant state keeps it at one.
 template <uint32_t DT, int BM, int BN, int SWEEPS>
 __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YULE_DTYPE_Q6_K ? 1 : 2))) void gemm_kernel(
-    const uint8_t *__restrict__ w, const _Float16 *__restrict__ xh, const _Float16 *__restrict__ xl,
-    float *__restrict__ y, const _Float16 *__restrict__ xs_hi, const _Float16 *__restrict__ xs_lo,
+    const GemmW wm_, const _Float16 *__restrict__ xh, const _Float16 *__restrict__ xl, float *__restrict__ y, const _Float16 *__restrict__ xs_hi, const _Float16 *__restrict__ xs_lo,
     const float *__restrict__ rowscale, uint32_t M, uint32_t N, uint32_t K, uint32_t xcd_remap, uint32_t tail) {
     constexpr bool Q5 = DT == YULE_DTYPE_Q5_K;
     constexpr bool Q4 = DT == YULE_DTYPE_Q4_K || Q5;   // Q5_K: Q4_K plus a fifth bit per weight from qh
@@ -296,7 +301,12 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
     // rows to row 0) and are used as they are: a row of the product depends
     // only on its own X row and a column only on its own weight row, and the
     // epilogue stores neither, so no masking is needed.
-    const uint8_t *wrow = w + (size_t)(r0 + wr < N ? r0 + wr : 0) * row_bytes;
+    // the tile's weight matrix: rows [0, s1) of Y come from w[0], [s1, s2)
+    // from w[1], [s2, N) from w[2] (a tile never straddles two), addressed
+    // here by the tile's row in Y
+    const uint32_t seg = r0 >= wm_.s2 ? 2u : r0 >= wm_.s1 ? 1u : 0u;
+    const uint8_t *w = wm_.w[seg] - (size_t)(seg == 2 ? wm_.s2 : seg == 1 ? wm_.s1 : 0u) * row_bytes;
+    const uint8_t *wrow = w + (size_t)(r0 + wr < N ? r0 + wr : r0) * row_bytes;
 
     // stc: std::integral_constant<int, ST>, the stage's index in its
     // super-block when the caller knows it at compile time (ST >= 0), else -1
@@ -660,7 +670,7 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
             for (uint32_t it = 0; it < (uint32_t)(BN * 4) / NTH; it++) {
                 const uint32_t idx = tid + NTH * it, row = idx >> 2, sbq = idx & 3u, sb = kk + sbq;
                 const bool ok = r0 + row < N && sb < kb_hi;
-                const uint32_t rc = r0 + row < N ? r0 + row : N - 1u, sbc = sb < kb_hi ? sb : kb_hi - 1u;
+                const uint32_t rc = r0 + row < N ? r0 + row : r0, sbc = sb < kb_hi ? sb : kb_hi - 1u;
                 const uint4 h4 = *reinterpret_cast<const uint4 *>(w + (size_t)rc * row_bytes + (size_t)sbc * BB);
                 const float dmin = f16_bits(h4.x >> 16);
                 const uint32_t hd[3] = {h4.y, h4.z, h4.w};
@@ -823,7 +833,7 @@ uint32_t gemm_tail(uint32_t m, uint32_t n, uint32_t k, uint32_t bn, uint32_t bm,
 // halves (xh, xl) swept in turn into the same accumulators.  Y rows are
 // scaled by rowscale.
 struct GemmPass {
-    const uint8_t *w;
+    GemmW w;
     const _Float16 *xh, *xl, *xs_hi, *xs_lo;
     const float *rowscale;
     float *y;
@@ -907,7 +917,9 @@ static GemmWork gemm_work(uint32_t m, uint32_t n_rows, uint32_t n_cols, uint32_t
 }
 
 // Enqueue the pre-pass and the product(s) of one call into workspace ws.
-static int gemm_enqueue(hipStream_t s, const uint8_t *w, const void *x, bool f32x, float *y, uint32_t m,
+static GemmW one_matrix(const uint8_t *w, uint32_t n_rows) { return GemmW{{w, w, w}, n_rows, n_rows}; }
+
+static int gemm_enqueue(hipStream_t s, const GemmW &w, const void *x, bool f32x, float *y, uint32_t m,
                         uint32_t n_rows, uint32_t n_cols, uint32_t dtype, const GemmWork &g, void *ws) {
     uint8_t *b = static_cast<uint8_t *>(ws);
     float *part = g.ks > 1 ? reinterpret_cast<float *>(b) : nullptr;
@@ -990,11 +1002,13 @@ static int gemm_entry(yule_hip_backend *be, yule_buffer weights, yule_buffer x, 
                                                    std::to_string(kStaticWorkspaceBytes) + "-byte one");
         void *ws = static_workspace(be->device);
         if (!ws) return set_error(YULE_ERR_HIP, std::string(what) + ": static workspace not set up for this device");
-        return gemm_enqueue(be->stream, (const uint8_t *)pw, px, f32x, (float *)py, m, n_rows, n_cols, dtype, g, ws);
+        return gemm_enqueue(be->stream, one_matrix((const uint8_t *)pw, n_rows), px, f32x, (float *)py, m, n_rows,
+                            n_cols, dtype, g, ws);
     }
     ScratchLease lease;   // held until every launch below is enqueued
     if ((rc = get_scratch(be, g.total, &lease))) return rc;
-    return gemm_enqueue(be->stream, (const uint8_t *)pw, px, f32x, (float *)py, m, n_rows, n_cols, dtype, g, lease.ptr);
+    return gemm_enqueue(be->stream, one_matrix((const uint8_t *)pw, n_rows), px, f32x, (float *)py, m, n_rows, n_cols,
+                        dtype, g, lease.ptr);
 }
 
 // the f32-X product for library callers that own their workspace (the
@@ -1009,7 +1023,37 @@ int yule::launch_gemm_f32(hipStream_t s, const uint8_t *w, const float *x, float
                           uint32_t n_cols, uint32_t dtype, void *ws) {
     if (!gemm_dtype_ok(dtype) || n_cols % 256) return set_error(YULE_ERR_UNSUPPORTED, "gemm: format or shape");
     if (!m || !n_rows) return YULE_OK;
-    return gemm_enqueue(s, w, x, true, y, m, n_rows, n_cols, dtype, gemm_work(m, n_rows, n_cols, dtype, true), ws);
+    return gemm_enqueue(s, one_matrix(w, n_rows), x, true, y, m, n_rows, n_cols, dtype,
+                        gemm_work(m, n_rows, n_cols, dtype, true), ws);
+}
+
+// Several matrices of one format and width that share X, as one product
+// (Y = [M][sum of their rows], each matrix's rows a block of columns): one
+// pre-pass, one launch, one split-K reduction.  Each matrix's row count must
+// be a multiple of 256, so that no tile of either width straddles two.
+bool yule::gemm_multi_ok(uint32_t dtype, uint32_t n_cols, const uint32_t *rows, uint32_t n_mat) {
+    if (!gemm_supports(dtype, n_cols) || n_mat == 0 || n_mat > 3) return false;
+    for (uint32_t i = 0; i < n_mat; i++)
+        if (rows[i] == 0 || rows[i] % 256) return false;
+    return true;
+}
+
+size_t yule::gemm_f32_multi_workspace_bytes(uint32_t m, const uint32_t *rows, uint32_t n_mat, uint32_t n_cols,
+                                            uint32_t dtype) {
+    uint32_t total = 0;
+    for (uint32_t i = 0; i < n_mat; i++) total += rows[i];
+    return gemm_work(m, total, n_cols, dtype, true).total;
+}
+
+int yule::launch_gemm_f32_multi(hipStream_t s, const uint8_t *const *w, const uint32_t *rows, uint32_t n_mat,
+                                const float *x, float *y, uint32_t m, uint32_t n_cols, uint32_t dtype, void *ws) {
+    if (!gemm_multi_ok(dtype, n_cols, rows, n_mat)) return set_error(YULE_ERR_UNSUPPORTED, "gemm: format or shape");
+    if (!m) return YULE_OK;
+    GemmW g{{w[0], n_mat > 1 ? w[1] : w[0], n_mat > 2 ? w[2] : w[0]}, 0, 0};
+    const uint32_t total = rows[0] + (n_mat > 1 ? rows[1] : 0) + (n_mat > 2 ? rows[2] : 0);
+    g.s1 = n_mat > 1 ? rows[0] : total;
+    g.s2 = n_mat > 2 ? rows[0] + rows[1] : total;
+    return gemm_enqueue(s, g, x, true, y, m, total, n_cols, dtype, gemm_work(m, total, n_cols, dtype, true), ws);
 }
 
 extern "C" int yule_hip_quantized_gemm(yule_hip_backend *be, yule_buffer weights, yule_buffer x_bf16, yule_buffer y,

@@ -136,18 +136,28 @@ int launch_attn_chunks(hipStream_t stream, const float *q, const float *kc, cons
 // f32-X prefill GEMM into a caller-owned workspace (gemm.hip)
 bool gemm_supports(uint32_t dtype, uint32_t n_cols);
 size_t gemm_f32_workspace_bytes(uint32_t m, uint32_t n_rows, uint32_t n_cols, uint32_t dtype);
+// up to three matrices of one format sharing X as one f32-X product into
+// Y [m][sum of rows] (each row count a multiple of 256)
+bool gemm_multi_ok(uint32_t dtype, uint32_t n_cols, const uint32_t *rows, uint32_t n_mat);
+size_t gemm_f32_multi_workspace_bytes(uint32_t m, const uint32_t *rows, uint32_t n_mat, uint32_t n_cols,
+                                      uint32_t dtype);
+int launch_gemm_f32_multi(hipStream_t stream, const uint8_t *const *w, const uint32_t *rows, uint32_t n_mat,
+                          const float *x, float *y, uint32_t m, uint32_t n_cols, uint32_t dtype, void *ws);
 int launch_gemm_f32(hipStream_t stream, const uint8_t *w, const float *x, float *y, uint32_t m, uint32_t n_rows,
                     uint32_t n_cols, uint32_t dtype, void *ws);
 // batched prompt pass (prefill.hip)
 int launch_embed_rows_batch(hipStream_t stream, uint32_t dtype, const uint8_t *table, const uint32_t *tokens,
                             uint32_t vocab, float *out, uint32_t dim, uint32_t n);
 int launch_rms_rows(hipStream_t stream, const float *x, const float *w, float *out, uint32_t n, uint32_t rows, float eps);
+// rows of q ldq floats apart, rows of k and v ldkv
 int launch_rope_rows(hipStream_t stream, float *q, const float *k, const float *v, float *kc, float *vc,
                      const float *cos_t, const float *sin_t, uint32_t pos0, uint32_t n, uint32_t qd, uint32_t kvd,
-                     uint32_t hd);
+                     uint32_t hd, uint32_t ldq, uint32_t ldkv);
 bool attn_prefill_supported(uint32_t hd);
 int launch_attn_prefill(hipStream_t stream, const float *q, const float *kc, const float *vc, float *out, uint32_t pos0,
-                        uint32_t n, uint32_t n_heads, uint32_t n_kv, uint32_t hd);
+                        uint32_t n, uint32_t n_heads, uint32_t n_kv, uint32_t hd, uint32_t ldq);
+// out [n][ff] = SwiGLU of rows held as [gate | up] ([n][2 ff])
+int launch_swiglu_rows(hipStream_t stream, const float *gu, float *out, uint32_t ff, uint32_t n);
 // one launch of an empty kernel (launch-overhead probe)
 int launch_empty(hipStream_t stream);
 // out[i] = value for i < n

@@ -92,39 +92,42 @@ int launch_rms_rows(hipStream_t s, const float *x, const float *w, float *out, u
 
 // ---- RoPE of row p's q (in place) and k with the table row of position
 // pos0 + p, and k, v into cache row pos0 + p (model_runner.rs:277-293,
-// 654-669; the same arithmetic as the decode step's Q/K/V epilogue)
+// 654-669; the same arithmetic as the decode step's Q/K/V epilogue).  Rows
+// of q are ldq floats apart, rows of k and v ldkv (separate buffers: qd and
+// kvd; one [q | k | v] buffer: qd + 2 kvd for all three).
 __global__ void rope_rows_kernel(float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
                                  float *__restrict__ kc, float *__restrict__ vc, const float *__restrict__ cos_t,
                                  const float *__restrict__ sin_t, uint32_t pos0, uint32_t qd, uint32_t kvd,
-                                 uint32_t hd) {
+                                 uint32_t hd, uint32_t ldq, uint32_t ldkv) {
     const uint32_t p = blockIdx.y, j = blockIdx.x * blockDim.x + threadIdx.x, half = hd / 2;
     const uint32_t pos = pos0 + p, nqp = qd / 2, nkp = kvd / 2;
     if (j < nqp) {   // rotation pair j of q
         const uint32_t i = j % half;
         const float c = cos_t[(size_t)pos * half + i], sn = sin_t[(size_t)pos * half + i];
-        float *qr = q + (size_t)p * qd + 2 * j;
+        float *qr = q + (size_t)p * ldq + 2 * j;
         const float x0 = qr[0], x1 = qr[1];
         qr[0] = x0 * c - x1 * sn;
         qr[1] = x0 * sn + x1 * c;
     } else if (j < nqp + nkp) {   // pair j - nqp of k, and the matching v values
         const uint32_t jk = j - nqp, i = jk % half;
         const float c = cos_t[(size_t)pos * half + i], sn = sin_t[(size_t)pos * half + i];
-        const float *kr = k + (size_t)p * kvd + 2 * jk;
+        const float *kr = k + (size_t)p * ldkv + 2 * jk;
         const float x0 = kr[0], x1 = kr[1];
         float *krow = kc + (size_t)pos * kvd + 2 * jk, *vrow = vc + (size_t)pos * kvd + 2 * jk;
         krow[0] = x0 * c - x1 * sn;
         krow[1] = x0 * sn + x1 * c;
-        const float *vr = v + (size_t)p * kvd + 2 * jk;
+        const float *vr = v + (size_t)p * ldkv + 2 * jk;
         vrow[0] = vr[0];
         vrow[1] = vr[1];
     }
 }
 
 int launch_rope_rows(hipStream_t s, float *q, const float *k, const float *v, float *kc, float *vc, const float *cos_t,
-                     const float *sin_t, uint32_t pos0, uint32_t n, uint32_t qd, uint32_t kvd, uint32_t hd) {
+                     const float *sin_t, uint32_t pos0, uint32_t n, uint32_t qd, uint32_t kvd, uint32_t hd, uint32_t ldq,
+                     uint32_t ldkv) {
     const uint32_t pairs = (qd + kvd) / 2;
     hipLaunchKernelGGL(rope_rows_kernel, dim3((pairs + 255) / 256, n), dim3(256), 0, s, q, k, v, kc, vc, cos_t, sin_t,
-                       pos0, qd, kvd, hd);
+                       pos0, qd, kvd, hd, ldq, ldkv);
     return check_launch("rope rows");
 }
 
@@ -138,8 +141,8 @@ int launch_rope_rows(hipStream_t s, float *q, const float *k, const float *v, fl
 template <uint32_t HD>
 __global__ __launch_bounds__(256) void attn_prefill_kernel(const float *__restrict__ q, const float *__restrict__ kc,
                                                            const float *__restrict__ vc, float *__restrict__ out,
-                                                           uint32_t pos0, uint32_t qd, uint32_t group,
-                                                           uint32_t n_kv) {
+                                                           uint32_t pos0, uint32_t qd, uint32_t ldq,
+                                                           uint32_t group, uint32_t n_kv) {
     constexpr uint32_t NT = 256, ND4 = HD / 4, LPP = HD / 16, C = NT / LPP, NG = NT / ND4;
     static_assert(C == 4 * NG && LPP >= 2 && LPP <= 16, "geometry");
     __shared__ float ps[C];
@@ -147,7 +150,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float *__restri
     __shared__ float4 ored[NT];
     const uint32_t h = blockIdx.x, p = blockIdx.y, tid = threadIdx.x, lane = tid & 63u, w = tid >> 6;
     const uint32_t kvh = h / group, kvs4 = n_kv * ND4, seq = pos0 + p + 1;
-    const float4 *q4 = reinterpret_cast<const float4 *>(q + (size_t)p * qd) + (size_t)h * ND4;
+    const float4 *q4 = reinterpret_cast<const float4 *>(q + (size_t)p * ldq) + (size_t)h * ND4;
     const float4 *kc4 = reinterpret_cast<const float4 *>(kc) + (size_t)kvh * ND4;
     const float4 *vc4 = reinterpret_cast<const float4 *>(vc) + (size_t)kvh * ND4;
     const uint32_t t = tid / LPP, sub = tid % LPP, d4 = tid % ND4, pg = tid / ND4;
@@ -208,17 +211,31 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float *__restri
     }
 }
 
+// ---- SwiGLU of rows held as [gate | up] (one gate/up product): out[p][i] =
+// gate * sigmoid(gate) * up (model_runner.rs:967-972, the eltwise form)
+__global__ void swiglu_rows_kernel(const float *__restrict__ gu, float *__restrict__ out, uint32_t ff) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x, p = blockIdx.y;
+    if (i >= ff) return;
+    const float g = gu[(size_t)p * 2 * ff + i], u = gu[(size_t)p * 2 * ff + ff + i];
+    out[(size_t)p * ff + i] = g * (1.0f / (1.0f + expf(-g))) * u;
+}
+
+int launch_swiglu_rows(hipStream_t s, const float *gu, float *out, uint32_t ff, uint32_t n) {
+    hipLaunchKernelGGL(swiglu_rows_kernel, dim3((ff + 255) / 256, n), dim3(256), 0, s, gu, out, ff);
+    return check_launch("swiglu rows");
+}
+
 bool attn_prefill_supported(uint32_t hd) { return hd == 32 || hd == 64 || hd == 128 || hd == 256; }
 
 int launch_attn_prefill(hipStream_t s, const float *q, const float *kc, const float *vc, float *out, uint32_t pos0,
-                        uint32_t n, uint32_t n_heads, uint32_t n_kv, uint32_t hd) {
+                        uint32_t n, uint32_t n_heads, uint32_t n_kv, uint32_t hd, uint32_t ldq) {
     const dim3 grid(n_heads, n);
     const uint32_t qd = n_heads * hd, group = n_heads / n_kv;
     switch (hd) {
-    case 32: hipLaunchKernelGGL(attn_prefill_kernel<32>, grid, dim3(256), 0, s, q, kc, vc, out, pos0, qd, group, n_kv); break;
-    case 64: hipLaunchKernelGGL(attn_prefill_kernel<64>, grid, dim3(256), 0, s, q, kc, vc, out, pos0, qd, group, n_kv); break;
-    case 128: hipLaunchKernelGGL(attn_prefill_kernel<128>, grid, dim3(256), 0, s, q, kc, vc, out, pos0, qd, group, n_kv); break;
-    case 256: hipLaunchKernelGGL(attn_prefill_kernel<256>, grid, dim3(256), 0, s, q, kc, vc, out, pos0, qd, group, n_kv); break;
+    case 32: hipLaunchKernelGGL(attn_prefill_kernel<32>, grid, dim3(256), 0, s, q, kc, vc, out, pos0, qd, ldq, group, n_kv); break;
+    case 64: hipLaunchKernelGGL(attn_prefill_kernel<64>, grid, dim3(256), 0, s, q, kc, vc, out, pos0, qd, ldq, group, n_kv); break;
+    case 128: hipLaunchKernelGGL(attn_prefill_kernel<128>, grid, dim3(256), 0, s, q, kc, vc, out, pos0, qd, ldq, group, n_kv); break;
+    case 256: hipLaunchKernelGGL(attn_prefill_kernel<256>, grid, dim3(256), 0, s, q, kc, vc, out, pos0, qd, ldq, group, n_kv); break;
     default: return set_error(YULE_ERR_UNSUPPORTED, "prefill attention: head size");
     }
     return check_launch("prefill attention");

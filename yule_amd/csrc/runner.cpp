@@ -56,6 +56,9 @@ struct yule_hip_runner {
     bool batchable = false;
     float *bx = nullptr, *bn = nullptr, *bq = nullptr, *bk = nullptr, *bv = nullptr, *ba = nullptr, *bp = nullptr,
           *bg = nullptr, *bu = nullptr;
+    // [q | k | v] and [gate | up] rows of the layers whose projections share
+    // a format (one GEMM each)
+    float *bqkv = nullptr, *bgu = nullptr;
     void *bws = nullptr;
     size_t bws_size = 0;
     float last_prefill_ms = 0.f;
@@ -276,6 +279,16 @@ int run_step(yule_hip_runner *r, uint32_t pos) {
     return hip_error(hipGraphLaunch(r->exec[split], r->be->stream), "runner: graph launch");
 }
 
+// Q/K/V (gate/up) of a layer as one GEMM: one format, rows multiples of 256
+bool qkv_one(const yule_hip_runner *r, const yule_hip_runner::Layer &L) {
+    const uint32_t qd = r->n_heads * r->hd, kvd = r->n_kv * r->hd, rows[3] = {qd, kvd, kvd};
+    return L.tq == L.tk && L.tk == L.tv && gemm_multi_ok(L.tq, r->dim, rows, 3);
+}
+bool gu_one(const yule_hip_runner *r, const yule_hip_runner::Layer &L) {
+    const uint32_t rows[2] = {r->ff, r->ff};
+    return L.tg == L.tu && gemm_multi_ok(L.tg, r->dim, rows, 2);
+}
+
 // GEMM workspace the batched pass over n rows needs (the largest of its
 // products)
 size_t batch_workspace(const yule_hip_runner *r, uint32_t n) {
@@ -287,6 +300,9 @@ size_t batch_workspace(const yule_hip_runner *r, uint32_t n) {
                              gemm_f32_workspace_bytes(n, r->ff, r->dim, L.tg), gemm_f32_workspace_bytes(n, r->ff, r->dim, L.tu),
                              gemm_f32_workspace_bytes(n, r->dim, r->ff, L.td)};
         for (size_t v : w) need = std::max(need, v);
+        const uint32_t qkv[3] = {qd, kvd, kvd}, gu[2] = {r->ff, r->ff};
+        if (qkv_one(r, L)) need = std::max(need, gemm_f32_multi_workspace_bytes(n, qkv, 3, r->dim, L.tq));
+        if (gu_one(r, L)) need = std::max(need, gemm_f32_multi_workspace_bytes(n, gu, 2, r->dim, L.tg));
     }
     return need;
 }
@@ -297,7 +313,8 @@ int ensure_batch(yule_hip_runner *r, uint32_t n) {
     if (!r->bx) {
         struct { float **p; size_t n; } bufs[] = {
             {&r->bx, r->dim}, {&r->bn, r->dim}, {&r->bq, qd}, {&r->bk, kvd}, {&r->bv, kvd},
-            {&r->ba, qd}, {&r->bp, r->dim}, {&r->bg, r->ff}, {&r->bu, r->ff}};
+            {&r->ba, qd}, {&r->bp, r->dim}, {&r->bg, r->ff}, {&r->bu, r->ff}, {&r->bqkv, qd + 2 * kvd},
+            {&r->bgu, 2 * r->ff}};
         for (auto &b : bufs)
             if ((rc = dev_alloc(r, (size_t)r->max_seq * b.n * 4, reinterpret_cast<void **>(b.p)))) return rc;
     }
@@ -330,20 +347,43 @@ int prefill_rows(yule_hip_runner *r, uint32_t pos0, uint32_t n, uint32_t prompt_
     if ((rc = set_ctl(r, pos0 + n - 1, 0, prompt_len))) return rc;
     void *ws = r->bws;
     if ((rc = launch_embed_rows_batch(s, r->embd_t, r->embd, r->prompt + pos0, r->vocab, r->bx, r->dim, n))) return rc;
+    const uint32_t qkv_rows[3] = {qd, kvd, kvd}, gu_rows[2] = {r->ff, r->ff};
     for (const auto &L : r->layers) {
-        if ((rc = launch_rms_rows(s, r->bx, L.attn_norm, r->bn, r->dim, n, r->eps)) ||
-            (rc = launch_gemm_f32(s, L.wq, r->bn, r->bq, n, qd, r->dim, L.tq, ws)) ||
-            (rc = launch_gemm_f32(s, L.wk, r->bn, r->bk, n, kvd, r->dim, L.tk, ws)) ||
-            (rc = launch_gemm_f32(s, L.wv, r->bn, r->bv, n, kvd, r->dim, L.tv, ws)) ||
-            (rc = launch_rope_rows(s, r->bq, r->bk, r->bv, L.kc, L.vc, r->cos_t, r->sin_t, pos0, n, qd, kvd, r->hd)) ||
-            (rc = launch_attn_prefill(s, r->bq, L.kc, L.vc, r->ba, pos0, n, r->n_heads, r->n_kv, r->hd)) ||
+        if ((rc = launch_rms_rows(s, r->bx, L.attn_norm, r->bn, r->dim, n, r->eps))) return rc;
+        // q, k, v rows: one [q | k | v] product when the three share a format
+        const float *q = r->bq, *k = r->bk, *v = r->bv;
+        uint32_t ldq = qd, ldkv = kvd;
+        if (qkv_one(r, L)) {
+            const uint8_t *w[3] = {L.wq, L.wk, L.wv};
+            if ((rc = launch_gemm_f32_multi(s, w, qkv_rows, 3, r->bn, r->bqkv, n, r->dim, L.tq, ws))) return rc;
+            q = r->bqkv;
+            k = r->bqkv + qd;
+            v = r->bqkv + qd + kvd;
+            ldq = ldkv = qd + 2 * kvd;
+        } else if ((rc = launch_gemm_f32(s, L.wq, r->bn, r->bq, n, qd, r->dim, L.tq, ws)) ||
+                   (rc = launch_gemm_f32(s, L.wk, r->bn, r->bk, n, kvd, r->dim, L.tk, ws)) ||
+                   (rc = launch_gemm_f32(s, L.wv, r->bn, r->bv, n, kvd, r->dim, L.tv, ws))) {
+            return rc;
+        }
+        if ((rc = launch_rope_rows(s, const_cast<float *>(q), k, v, L.kc, L.vc, r->cos_t, r->sin_t, pos0, n, qd, kvd,
+                                   r->hd, ldq, ldkv)) ||
+            (rc = launch_attn_prefill(s, q, L.kc, L.vc, r->ba, pos0, n, r->n_heads, r->n_kv, r->hd, ldq)) ||
             (rc = launch_gemm_f32(s, L.wo, r->ba, r->bp, n, r->dim, qd, L.to, ws)) ||
             (rc = launch_eltwise(s, 2, r->bx, r->bp, r->bx, n * r->dim)) ||
-            (rc = launch_rms_rows(s, r->bx, L.ffn_norm, r->bn, r->dim, n, r->eps)) ||
-            (rc = launch_gemm_f32(s, L.wg, r->bn, r->bg, n, r->ff, r->dim, L.tg, ws)) ||
-            (rc = launch_gemm_f32(s, L.wu, r->bn, r->bu, n, r->ff, r->dim, L.tu, ws)) ||
-            (rc = launch_eltwise(s, 3, r->bg, r->bu, r->bg, n * r->ff)) ||
-            (rc = launch_gemm_f32(s, L.wd, r->bg, r->bp, n, r->dim, r->ff, L.td, ws)) ||
+            (rc = launch_rms_rows(s, r->bx, L.ffn_norm, r->bn, r->dim, n, r->eps)))
+            return rc;
+        // gate and up: one [gate | up] product when they share a format
+        if (gu_one(r, L)) {
+            const uint8_t *w[2] = {L.wg, L.wu};
+            if ((rc = launch_gemm_f32_multi(s, w, gu_rows, 2, r->bn, r->bgu, n, r->dim, L.tg, ws)) ||
+                (rc = launch_swiglu_rows(s, r->bgu, r->bg, r->ff, n)))
+                return rc;
+        } else if ((rc = launch_gemm_f32(s, L.wg, r->bn, r->bg, n, r->ff, r->dim, L.tg, ws)) ||
+                   (rc = launch_gemm_f32(s, L.wu, r->bn, r->bu, n, r->ff, r->dim, L.tu, ws)) ||
+                   (rc = launch_eltwise(s, 3, r->bg, r->bu, r->bg, n * r->ff))) {
+            return rc;
+        }
+        if ((rc = launch_gemm_f32(s, L.wd, r->bg, r->bp, n, r->dim, r->ff, L.td, ws)) ||
             (rc = launch_eltwise(s, 2, r->bx, r->bp, r->bx, n * r->dim)))
             return rc;
     }
