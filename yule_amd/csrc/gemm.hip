@@ -111,8 +111,8 @@ template <bool F32>
 __global__ __launch_bounds__(256) void gemm_xprep_kernel(const void *__restrict__ xin, _Float16 *__restrict__ xh,
                                                          _Float16 *__restrict__ xl, _Float16 *__restrict__ hi,
                                                          _Float16 *__restrict__ lo, float *__restrict__ rowscale,
-                                                         uint32_t K) {
-    __shared__ float red[4];
+                                                         uint32_t K, const float *__restrict__ nw, float eps) {
+    __shared__ float red[4], red2[4];
     const uint32_t m = blockIdx.x, tid = threadIdx.x, nch = K / 8;
     auto load8 = [&](uint32_t c, float *v) {
         if constexpr (F32) {
@@ -129,18 +129,44 @@ __global__ __launch_bounds__(256) void gemm_xprep_kernel(const void *__restrict_
             }
         }
     };
-    float amax = 0.f;
+    // nw: the row is x * inv * nw, inv = 1 / sqrt(mean(x^2) + eps) (RMSNorm,
+    // model_runner.rs:246-275, fused here so that the projection reads the
+    // residual stream itself)
+    auto loadw8 = [&](uint32_t c, float *v) {
+        const float4 *p = reinterpret_cast<const float4 *>(nw + 8 * c);
+        const float4 a = p[0], b = p[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    };
+    float amax = 0.f, ss = 0.f;
     for (uint32_t c = tid; c < nch; c += 256) {
         float v[8];
         load8(c, v);
+        if (nw) {
+            float wv[8];
+            loadw8(c, wv);
 #pragma unroll
-        for (int t = 0; t < 8; t++) amax = fmaxf(amax, fabsf(v[t]));   // NaN is dropped here, kept below
+            for (int t = 0; t < 8; t++) {
+                ss += v[t] * v[t];
+                amax = fmaxf(amax, fabsf(v[t] * wv[t]));
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < 8; t++) amax = fmaxf(amax, fabsf(v[t]));   // NaN is dropped here, kept below
+        }
     }
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
-    if ((tid & 63) == 0) red[tid >> 6] = amax;
+    for (int off = 32; off >= 1; off >>= 1) {
+        amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+        ss += __shfl_xor(ss, off, 64);
+    }
+    if ((tid & 63) == 0) {
+        red[tid >> 6] = amax;
+        red2[tid >> 6] = ss;
+    }
     __syncthreads();
     amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float inv = nw ? 1.0f / sqrtf(((red2[0] + red2[1]) + (red2[2] + red2[3])) / (float)K + eps) : 1.0f;
+    amax *= inv;   // the normalised row's largest magnitude, to rounding (the scale only needs its exponent)
     int e = 0;
     (void)frexpf(amax, &e);
     const int es = 10 - e < 126 ? 10 - e : 126;   // rows below 2^-116 keep s = 2^126
@@ -152,6 +178,12 @@ __global__ __launch_bounds__(256) void gemm_xprep_kernel(const void *__restrict_
         const bool ok = c < nch;
         float v[8];
         load8(ok ? c : 0u, v);
+        if (nw) {
+            float wv[8];
+            loadw8(ok ? c : 0u, wv);
+#pragma unroll
+            for (int t = 0; t < 8; t++) v[t] = v[t] * inv * wv[t];
+        }
         float s = 0.f;
         uint32_t oh[4], ol[4];
 #pragma unroll
@@ -221,7 +253,8 @@ struct GemmW {
 template <uint32_t DT, int BM, int BN, int SWEEPS>
 __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YULE_DTYPE_Q6_K ? 1 : 2))) void gemm_kernel(
     const GemmW wm_, const _Float16 *__restrict__ xh, const _Float16 *__restrict__ xl, float *__restrict__ y, const _Float16 *__restrict__ xs_hi, const _Float16 *__restrict__ xs_lo,
-    const float *__restrict__ rowscale, uint32_t M, uint32_t N, uint32_t K, uint32_t xcd_remap, uint32_t tail) {
+    const float *__restrict__ rowscale, uint32_t M, uint32_t N, uint32_t K, uint32_t xcd_remap, uint32_t tail,
+    uint32_t accumulate) {
     constexpr bool Q5 = DT == YULE_DTYPE_Q5_K;
     constexpr bool Q4 = DT == YULE_DTYPE_Q4_K || Q5;   // Q5_K: Q4_K plus a fifth bit per weight from qh
     constexpr bool B32 = DT == YULE_DTYPE_Q8_0 || DT == YULE_DTYPE_Q4_0;   // 32-weight blocks, d per block
@@ -738,6 +771,7 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
                 if (m < M && r < N) {
                     const float v = acc[i][j][e] * rowscale[m];   // the row's power of two back out: exact
                     if (halves) unsafeAtomicAdd(y + (size_t)m * N + r, v);
+                    else if (accumulate && splits == 1) y[(size_t)m * N + r] += v;
                     else y[(size_t)m * N + r] = v;
                 }
             }
@@ -758,13 +792,14 @@ __global__ void gemm_zero_tiles_kernel(float *__restrict__ y, uint32_t M, uint32
     }
 }
 
-// y[i] = sum over z of part[z][i], z ascending
-__global__ void gemm_reduce_kernel(const float *__restrict__ part, float *__restrict__ y, uint64_t n, uint32_t ks) {
+// y[i] = sum over z of part[z][i], z ascending (accumulate: y[i] + that sum)
+__global__ void gemm_reduce_kernel(const float *__restrict__ part, float *__restrict__ y, uint64_t n, uint32_t ks,
+                                   uint32_t accumulate) {
     const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
     float s = part[i];
     for (uint32_t z = 1; z < ks; z++) s += part[(uint64_t)z * n + i];
-    y[i] = s;
+    y[i] = accumulate ? y[i] + s : s;
 }
 
 }  // namespace yule
@@ -837,7 +872,7 @@ struct GemmPass {
     const _Float16 *xh, *xl, *xs_hi, *xs_lo;
     const float *rowscale;
     float *y;
-    uint32_t m, n, k, ks, bn, bm, tail;
+    uint32_t m, n, k, ks, bn, bm, tail, accumulate;
 };
 
 template <uint32_t DT, int BN>
@@ -852,16 +887,16 @@ void launch_gemm_bn(hipStream_t s, const GemmPass &p) {
     if (p.xl) {   // f32 X: the hi and lo sweeps
         if (bm == 64)
             hipLaunchKernelGGL((gemm_kernel<DT, 64, BN, 2>), dim3(grid), dim3(2 * BN), 0, s, p.w, p.xh, p.xl, p.y,
-                               p.xs_hi, p.xs_lo, p.rowscale, p.m, p.n, p.k, remap, p.tail);
+                               p.xs_hi, p.xs_lo, p.rowscale, p.m, p.n, p.k, remap, p.tail, p.accumulate);
         else
             hipLaunchKernelGGL((gemm_kernel<DT, 128, BN, 2>), dim3(grid), dim3(2 * BN), 0, s, p.w, p.xh, p.xl, p.y,
-                               p.xs_hi, p.xs_lo, p.rowscale, p.m, p.n, p.k, remap, p.tail);
+                               p.xs_hi, p.xs_lo, p.rowscale, p.m, p.n, p.k, remap, p.tail, p.accumulate);
     } else if (bm == 64) {
         hipLaunchKernelGGL((gemm_kernel<DT, 64, BN, 1>), dim3(grid), dim3(2 * BN), 0, s, p.w, p.xh, p.xl, p.y, p.xs_hi,
-                           p.xs_lo, p.rowscale, p.m, p.n, p.k, remap, p.tail);
+                           p.xs_lo, p.rowscale, p.m, p.n, p.k, remap, p.tail, p.accumulate);
     } else {
         hipLaunchKernelGGL((gemm_kernel<DT, 128, BN, 1>), dim3(grid), dim3(2 * BN), 0, s, p.w, p.xh, p.xl, p.y, p.xs_hi,
-                           p.xs_lo, p.rowscale, p.m, p.n, p.k, remap, p.tail);
+                           p.xs_lo, p.rowscale, p.m, p.n, p.k, remap, p.tail, p.accumulate);
     }
 }
 
@@ -919,8 +954,11 @@ static GemmWork gemm_work(uint32_t m, uint32_t n_rows, uint32_t n_cols, uint32_t
 // Enqueue the pre-pass and the product(s) of one call into workspace ws.
 static GemmW one_matrix(const uint8_t *w, uint32_t n_rows) { return GemmW{{w, w, w}, n_rows, n_rows}; }
 
+// accumulate: Y += the product (no K-half tail then: its atomic adds would
+// add into Y in either order)
 static int gemm_enqueue(hipStream_t s, const GemmW &w, const void *x, bool f32x, float *y, uint32_t m,
-                        uint32_t n_rows, uint32_t n_cols, uint32_t dtype, const GemmWork &g, void *ws) {
+                        uint32_t n_rows, uint32_t n_cols, uint32_t dtype, const GemmWork &g, void *ws,
+                        bool accumulate = false, const float *norm_w = nullptr, float eps = 0.f) {
     uint8_t *b = static_cast<uint8_t *>(ws);
     float *part = g.ks > 1 ? reinterpret_cast<float *>(b) : nullptr;
     _Float16 *xh = reinterpret_cast<_Float16 *>(b + g.part_bytes);
@@ -929,17 +967,19 @@ static int gemm_enqueue(hipStream_t s, const GemmW &w, const void *x, bool f32x,
     float *rowscale = reinterpret_cast<float *>(
         (reinterpret_cast<uintptr_t>(xh + (f32x ? 2 : 1) * g.n_x + (g.q4 ? 2 * g.n_sub : 0)) + 255) & ~(uintptr_t)255);
     if (f32x)
-        hipLaunchKernelGGL(gemm_xprep_kernel<true>, dim3(m), dim3(256), 0, s, x, xh, xl, xs_hi, xs_lo, rowscale, n_cols);
+        hipLaunchKernelGGL(gemm_xprep_kernel<true>, dim3(m), dim3(256), 0, s, x, xh, xl, xs_hi, xs_lo, rowscale, n_cols,
+                           norm_w, eps);
     else
         hipLaunchKernelGGL(gemm_xprep_kernel<false>, dim3(m), dim3(256), 0, s, x, xh, xl, xs_hi, xs_lo, rowscale,
-                           n_cols);
+                           n_cols, norm_w, eps);
     int rc = check_launch("quantized_gemm: x pre-pass");
     if (rc) return rc;
-    const GemmPass p{w, xh, xl, xs_hi, xs_lo, rowscale, g.ks > 1 ? part : y, m, n_rows, n_cols, g.ks, g.bn, g.bm, g.tail};
+    const GemmPass p{w, xh, xl, xs_hi, xs_lo, rowscale, g.ks > 1 ? part : y, m, n_rows, n_cols, g.ks, g.bn, g.bm,
+                     accumulate ? 0u : g.tail, accumulate ? 1u : 0u};
     if ((rc = launch_gemm_dt(s, dtype, p))) return rc;
     if (g.ks > 1) {
         hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)((g.n_y + 255) / 256)), dim3(256), 0, s, part, y,
-                           (uint64_t)g.n_y, g.ks);
+                           (uint64_t)g.n_y, g.ks, accumulate ? 1u : 0u);
         if ((rc = check_launch("quantized_gemm: split-K reduction"))) return rc;
     }
     return YULE_OK;
@@ -1020,11 +1060,11 @@ size_t yule::gemm_f32_workspace_bytes(uint32_t m, uint32_t n_rows, uint32_t n_co
 }
 
 int yule::launch_gemm_f32(hipStream_t s, const uint8_t *w, const float *x, float *y, uint32_t m, uint32_t n_rows,
-                          uint32_t n_cols, uint32_t dtype, void *ws) {
+                          uint32_t n_cols, uint32_t dtype, void *ws, bool accumulate, const float *norm_w, float eps) {
     if (!gemm_dtype_ok(dtype) || n_cols % 256) return set_error(YULE_ERR_UNSUPPORTED, "gemm: format or shape");
     if (!m || !n_rows) return YULE_OK;
     return gemm_enqueue(s, one_matrix(w, n_rows), x, true, y, m, n_rows, n_cols, dtype,
-                        gemm_work(m, n_rows, n_cols, dtype, true), ws);
+                        gemm_work(m, n_rows, n_cols, dtype, true), ws, accumulate, norm_w, eps);
 }
 
 // Several matrices of one format and width that share X, as one product
@@ -1046,14 +1086,16 @@ size_t yule::gemm_f32_multi_workspace_bytes(uint32_t m, const uint32_t *rows, ui
 }
 
 int yule::launch_gemm_f32_multi(hipStream_t s, const uint8_t *const *w, const uint32_t *rows, uint32_t n_mat,
-                                const float *x, float *y, uint32_t m, uint32_t n_cols, uint32_t dtype, void *ws) {
+                                const float *x, float *y, uint32_t m, uint32_t n_cols, uint32_t dtype, void *ws,
+                                const float *norm_w, float eps) {
     if (!gemm_multi_ok(dtype, n_cols, rows, n_mat)) return set_error(YULE_ERR_UNSUPPORTED, "gemm: format or shape");
     if (!m) return YULE_OK;
     GemmW g{{w[0], n_mat > 1 ? w[1] : w[0], n_mat > 2 ? w[2] : w[0]}, 0, 0};
     const uint32_t total = rows[0] + (n_mat > 1 ? rows[1] : 0) + (n_mat > 2 ? rows[2] : 0);
     g.s1 = n_mat > 1 ? rows[0] : total;
     g.s2 = n_mat > 2 ? rows[0] + rows[1] : total;
-    return gemm_enqueue(s, g, x, true, y, m, total, n_cols, dtype, gemm_work(m, total, n_cols, dtype, true), ws);
+    return gemm_enqueue(s, g, x, true, y, m, total, n_cols, dtype, gemm_work(m, total, n_cols, dtype, true), ws,
+                        false, norm_w, eps);
 }
 
 extern "C" int yule_hip_quantized_gemm(yule_hip_backend *be, yule_buffer weights, yule_buffer x_bf16, yule_buffer y,

@@ -142,13 +142,16 @@ bool gemm_multi_ok(uint32_t dtype, uint32_t n_cols, const uint32_t *rows, uint32
 size_t gemm_f32_multi_workspace_bytes(uint32_t m, const uint32_t *rows, uint32_t n_mat, uint32_t n_cols,
                                       uint32_t dtype);
 int launch_gemm_f32_multi(hipStream_t stream, const uint8_t *const *w, const uint32_t *rows, uint32_t n_mat,
-                          const float *x, float *y, uint32_t m, uint32_t n_cols, uint32_t dtype, void *ws);
+                          const float *x, float *y, uint32_t m, uint32_t n_cols, uint32_t dtype, void *ws,
+                          const float *norm_w = nullptr, float eps = 0.f);
+// accumulate: Y += X W (the residual add of the output and down projections);
+// norm_w: X's rows RMS-normalised and scaled by norm_w (eps) on the way in
 int launch_gemm_f32(hipStream_t stream, const uint8_t *w, const float *x, float *y, uint32_t m, uint32_t n_rows,
-                    uint32_t n_cols, uint32_t dtype, void *ws);
+                    uint32_t n_cols, uint32_t dtype, void *ws, bool accumulate = false, const float *norm_w = nullptr,
+                    float eps = 0.f);
 // batched prompt pass (prefill.hip)
 int launch_embed_rows_batch(hipStream_t stream, uint32_t dtype, const uint8_t *table, const uint32_t *tokens,
                             uint32_t vocab, float *out, uint32_t dim, uint32_t n);
-int launch_rms_rows(hipStream_t stream, const float *x, const float *w, float *out, uint32_t n, uint32_t rows, float eps);
 // rows of q ldq floats apart, rows of k and v ldkv
 int launch_rope_rows(hipStream_t stream, float *q, const float *k, const float *v, float *kc, float *vc,
                      const float *cos_t, const float *sin_t, uint32_t pos0, uint32_t n, uint32_t qd, uint32_t kvd,

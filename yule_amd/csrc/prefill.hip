@@ -69,27 +69,6 @@ int launch_embed_rows_batch(hipStream_t s, uint32_t dtype, const uint8_t *table,
     return check_launch("embedding rows");
 }
 
-// ---- RMSNorm of each row (model_runner.rs:246-275): out = x * w / sqrt(mean(x^2) + eps)
-__global__ __launch_bounds__(256) void rms_rows_kernel(const float *__restrict__ x, const float *__restrict__ w,
-                                                       float *__restrict__ out, uint32_t n, float eps) {
-    __shared__ float red[4];
-    const float *xr = x + (size_t)blockIdx.x * n;
-    float *orow = out + (size_t)blockIdx.x * n;
-    float ss = 0.f;
-    for (uint32_t i = threadIdx.x; i < n; i += 256) ss += xr[i] * xr[i];
-    ss = wsum(ss);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
-    __syncthreads();
-    ss = (red[0] + red[1]) + (red[2] + red[3]);
-    const float inv = 1.0f / sqrtf(ss / (float)n + eps);
-    for (uint32_t i = threadIdx.x; i < n; i += 256) orow[i] = xr[i] * inv * w[i];
-}
-
-int launch_rms_rows(hipStream_t s, const float *x, const float *w, float *out, uint32_t n, uint32_t rows, float eps) {
-    hipLaunchKernelGGL(rms_rows_kernel, dim3(rows), dim3(256), 0, s, x, w, out, n, eps);
-    return check_launch("rms_norm rows");
-}
-
 // ---- RoPE of row p's q (in place) and k with the table row of position
 // pos0 + p, and k, v into cache row pos0 + p (model_runner.rs:277-293,
 // 654-669; the same arithmetic as the decode step's Q/K/V epilogue).  Rows

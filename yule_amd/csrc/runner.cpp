@@ -54,8 +54,8 @@ struct yule_hip_runner {
     // batched prefill (prefill_rows): row buffers for max_seq rows and the
     // GEMM workspace, allocated at the first batched prefill
     bool batchable = false;
-    float *bx = nullptr, *bn = nullptr, *bq = nullptr, *bk = nullptr, *bv = nullptr, *ba = nullptr, *bp = nullptr,
-          *bg = nullptr, *bu = nullptr;
+    float *bx = nullptr, *bq = nullptr, *bk = nullptr, *bv = nullptr, *ba = nullptr, *bg = nullptr,
+          *bu = nullptr;
     // [q | k | v] and [gate | up] rows of the layers whose projections share
     // a format (one GEMM each)
     float *bqkv = nullptr, *bgu = nullptr;
@@ -312,8 +312,8 @@ int ensure_batch(yule_hip_runner *r, uint32_t n) {
     int rc;
     if (!r->bx) {
         struct { float **p; size_t n; } bufs[] = {
-            {&r->bx, r->dim}, {&r->bn, r->dim}, {&r->bq, qd}, {&r->bk, kvd}, {&r->bv, kvd},
-            {&r->ba, qd}, {&r->bp, r->dim}, {&r->bg, r->ff}, {&r->bu, r->ff}, {&r->bqkv, qd + 2 * kvd},
+            {&r->bx, r->dim}, {&r->bq, qd}, {&r->bk, kvd}, {&r->bv, kvd},
+            {&r->ba, qd}, {&r->bg, r->ff}, {&r->bu, r->ff}, {&r->bqkv, qd + 2 * kvd},
             {&r->bgu, 2 * r->ff}};
         for (auto &b : bufs)
             if ((rc = dev_alloc(r, (size_t)r->max_seq * b.n * 4, reinterpret_cast<void **>(b.p)))) return rc;
@@ -333,7 +333,9 @@ int ensure_batch(yule_hip_runner *r, uint32_t n) {
 }
 
 // The prompt tokens at r->prompt[pos0, pos0 + n) through every layer as n
-// rows at once (prefill.hip; each projection one f32-X GEMM), writing KV rows
+// rows at once (prefill.hip; projections as f32-X GEMMs: RMSNorm folded into
+// the GEMM's X pre-pass, Q/K/V and gate/up one product each where they share
+// a format, the residual adds in the O and down products), writing KV rows
 // pos0.. pos0 + n - 1; then the head over the last row, as the decode step
 // for position pos0 + n - 1 would run it, with ctl = {pos0 + n - 1, -,
 // prompt_len}: the argmax lands in tokens[pos0 + n - 1] and ctl[1], and ctl[0]
@@ -349,42 +351,40 @@ int prefill_rows(yule_hip_runner *r, uint32_t pos0, uint32_t n, uint32_t prompt_
     if ((rc = launch_embed_rows_batch(s, r->embd_t, r->embd, r->prompt + pos0, r->vocab, r->bx, r->dim, n))) return rc;
     const uint32_t qkv_rows[3] = {qd, kvd, kvd}, gu_rows[2] = {r->ff, r->ff};
     for (const auto &L : r->layers) {
-        if ((rc = launch_rms_rows(s, r->bx, L.attn_norm, r->bn, r->dim, n, r->eps))) return rc;
         // q, k, v rows: one [q | k | v] product when the three share a format
         const float *q = r->bq, *k = r->bk, *v = r->bv;
         uint32_t ldq = qd, ldkv = kvd;
         if (qkv_one(r, L)) {
             const uint8_t *w[3] = {L.wq, L.wk, L.wv};
-            if ((rc = launch_gemm_f32_multi(s, w, qkv_rows, 3, r->bn, r->bqkv, n, r->dim, L.tq, ws))) return rc;
+            if ((rc = launch_gemm_f32_multi(s, w, qkv_rows, 3, r->bx, r->bqkv, n, r->dim, L.tq, ws, L.attn_norm,
+                                            r->eps)))
+                return rc;
             q = r->bqkv;
             k = r->bqkv + qd;
             v = r->bqkv + qd + kvd;
             ldq = ldkv = qd + 2 * kvd;
-        } else if ((rc = launch_gemm_f32(s, L.wq, r->bn, r->bq, n, qd, r->dim, L.tq, ws)) ||
-                   (rc = launch_gemm_f32(s, L.wk, r->bn, r->bk, n, kvd, r->dim, L.tk, ws)) ||
-                   (rc = launch_gemm_f32(s, L.wv, r->bn, r->bv, n, kvd, r->dim, L.tv, ws))) {
+        } else if ((rc = launch_gemm_f32(s, L.wq, r->bx, r->bq, n, qd, r->dim, L.tq, ws, false, L.attn_norm, r->eps)) ||
+                   (rc = launch_gemm_f32(s, L.wk, r->bx, r->bk, n, kvd, r->dim, L.tk, ws, false, L.attn_norm, r->eps)) ||
+                   (rc = launch_gemm_f32(s, L.wv, r->bx, r->bv, n, kvd, r->dim, L.tv, ws, false, L.attn_norm, r->eps))) {
             return rc;
         }
         if ((rc = launch_rope_rows(s, const_cast<float *>(q), k, v, L.kc, L.vc, r->cos_t, r->sin_t, pos0, n, qd, kvd,
                                    r->hd, ldq, ldkv)) ||
             (rc = launch_attn_prefill(s, q, L.kc, L.vc, r->ba, pos0, n, r->n_heads, r->n_kv, r->hd, ldq)) ||
-            (rc = launch_gemm_f32(s, L.wo, r->ba, r->bp, n, r->dim, qd, L.to, ws)) ||
-            (rc = launch_eltwise(s, 2, r->bx, r->bp, r->bx, n * r->dim)) ||
-            (rc = launch_rms_rows(s, r->bx, L.ffn_norm, r->bn, r->dim, n, r->eps)))
+            (rc = launch_gemm_f32(s, L.wo, r->ba, r->bx, n, r->dim, qd, L.to, ws, true)))   // residual += O
             return rc;
         // gate and up: one [gate | up] product when they share a format
         if (gu_one(r, L)) {
             const uint8_t *w[2] = {L.wg, L.wu};
-            if ((rc = launch_gemm_f32_multi(s, w, gu_rows, 2, r->bn, r->bgu, n, r->dim, L.tg, ws)) ||
+            if ((rc = launch_gemm_f32_multi(s, w, gu_rows, 2, r->bx, r->bgu, n, r->dim, L.tg, ws, L.ffn_norm, r->eps)) ||
                 (rc = launch_swiglu_rows(s, r->bgu, r->bg, r->ff, n)))
                 return rc;
-        } else if ((rc = launch_gemm_f32(s, L.wg, r->bn, r->bg, n, r->ff, r->dim, L.tg, ws)) ||
-                   (rc = launch_gemm_f32(s, L.wu, r->bn, r->bu, n, r->ff, r->dim, L.tu, ws)) ||
+        } else if ((rc = launch_gemm_f32(s, L.wg, r->bx, r->bg, n, r->ff, r->dim, L.tg, ws, false, L.ffn_norm, r->eps)) ||
+                   (rc = launch_gemm_f32(s, L.wu, r->bx, r->bu, n, r->ff, r->dim, L.tu, ws, false, L.ffn_norm, r->eps)) ||
                    (rc = launch_eltwise(s, 3, r->bg, r->bu, r->bg, n * r->ff))) {
             return rc;
         }
-        if ((rc = launch_gemm_f32(s, L.wd, r->bg, r->bp, n, r->dim, r->ff, L.td, ws)) ||
-            (rc = launch_eltwise(s, 2, r->bx, r->bp, r->bx, n * r->dim)))
+        if ((rc = launch_gemm_f32(s, L.wd, r->bg, r->bx, n, r->dim, r->ff, L.td, ws, true)))   // residual += down
             return rc;
     }
     if ((rc = hip_error(hipMemcpyAsync(r->hidden, r->bx + (size_t)(n - 1) * r->dim, (size_t)r->dim * 4,
