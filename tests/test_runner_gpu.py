@@ -293,6 +293,23 @@ def test_runner_wide_rows_fused_variants(hip, threads_w64):
     say(f"[runner] {r.stdout.strip()}")
 
 
+@pytest.mark.parametrize("splits", ["1", "3"])
+def test_runner_prefill_batched_forced_splits(hip, splits):
+    """The batched prefill with the GEMM's K split forced to 1 (every tile
+    stored by the epilogue, which adds the O and down products into the
+    residual rows) and to 3 (the split-K reduction does it), against the
+    oracle (tests/prefill_splits_check.py, in a child process because the
+    split count is read once per process)."""
+    import os
+    import subprocess
+    say(f"[runner] batched prefill with {splits} K splits")
+    env = dict(os.environ, YULE_GEMM_SPLITS=splits)
+    r = subprocess.run([sys.executable, str(Path(__file__).with_name("prefill_splits_check.py"))], env=env,
+                       capture_output=True, text=True, timeout=110)
+    assert r.returncode == 0 and r.stdout.startswith("ok"), r.stdout[-2000:] + r.stderr[-4000:]
+    say(f"[runner] {r.stdout.strip()}")
+
+
 def test_runner_prefill_determinism_reset_and_limits(hip, tiny):
     say("[runner] prefill determinism / reset / context limit")
     run = HipRunner(hip, tiny)
