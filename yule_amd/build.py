@@ -36,6 +36,7 @@ HIP_FLAGS = [
     "-Wno-unused-result",
     # packed FP32 VALU ops are kept out of every kernel of this library
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
 ]
 
 

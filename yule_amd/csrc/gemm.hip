@@ -252,9 +252,12 @@ struct GemmW {
 // with a few spilled bytes); Q6_K's larger dequant state keeps it at one.
 template <uint32_t DT, int BM, int BN, int SWEEPS>
 __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YULE_DTYPE_Q6_K ? 1 : 2))) void gemm_kernel(
-    const GemmW wm_, const _Float16 *__restrict__ xh, const _Float16 *__restrict__ xl, float *__restrict__ y, const _Float16 *__restrict__ xs_hi, const _Float16 *__restrict__ xs_lo,
-    const float *__restrict__ rowscale, uint32_t M, uint32_t N, uint32_t K, uint32_t xcd_remap, uint32_t tail,
-    uint32_t accumulate) {
+    // the first 14 dwords (what the first loads need) arrive preloaded in
+    // SGPRs: no kernel-argument load delays them
+    const _Float16 *__restrict__ xh, const uint8_t *w0, const uint8_t *w1, const uint8_t *w2, uint32_t s1,
+    uint32_t s2, uint32_t M, uint32_t N, uint32_t K, uint32_t tail, const _Float16 *__restrict__ xl,
+    float *__restrict__ y, const _Float16 *__restrict__ xs_hi, const _Float16 *__restrict__ xs_lo,
+    const float *__restrict__ rowscale, uint32_t xcd_remap, uint32_t accumulate) {
     constexpr bool Q5 = DT == YULE_DTYPE_Q5_K;
     constexpr bool Q4 = DT == YULE_DTYPE_Q4_K || Q5;   // Q5_K: Q4_K plus a fifth bit per weight from qh
     constexpr bool B32 = DT == YULE_DTYPE_Q8_0 || DT == YULE_DTYPE_Q4_0;   // 32-weight blocks, d per block
@@ -337,8 +340,8 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
     // the tile's weight matrix: rows [0, s1) of Y come from w[0], [s1, s2)
     // from w[1], [s2, N) from w[2] (a tile never straddles two), addressed
     // here by the tile's row in Y
-    const uint32_t seg = r0 >= wm_.s2 ? 2u : r0 >= wm_.s1 ? 1u : 0u;
-    const uint8_t *w = wm_.w[seg] - (size_t)(seg == 2 ? wm_.s2 : seg == 1 ? wm_.s1 : 0u) * row_bytes;
+    const uint32_t seg = r0 >= s2 ? 2u : r0 >= s1 ? 1u : 0u;
+    const uint8_t *w = (seg == 2 ? w2 : seg == 1 ? w1 : w0) - (size_t)(seg == 2 ? s2 : seg == 1 ? s1 : 0u) * row_bytes;
     const uint8_t *wrow = w + (size_t)(r0 + wr < N ? r0 + wr : r0) * row_bytes;
 
     // stc: std::integral_constant<int, ST>, the stage's index in its
@@ -884,20 +887,19 @@ void launch_gemm_bn(hipStream_t s, const GemmPass &p) {
     if (p.tail)
         hipLaunchKernelGGL(gemm_zero_tiles_kernel, dim3(p.tail * (bm / 8)), dim3(256), 0, s, p.y, p.m, p.n,
                            tiles - p.tail, nt, bm, (uint32_t)BN);
+#define YULE_GEMM_ARGS p.xh, p.w.w[0], p.w.w[1], p.w.w[2], p.w.s1, p.w.s2, p.m, p.n, p.k, p.tail, p.xl, p.y, p.xs_hi, \
+        p.xs_lo, p.rowscale, remap, p.accumulate
     if (p.xl) {   // f32 X: the hi and lo sweeps
         if (bm == 64)
-            hipLaunchKernelGGL((gemm_kernel<DT, 64, BN, 2>), dim3(grid), dim3(2 * BN), 0, s, p.w, p.xh, p.xl, p.y,
-                               p.xs_hi, p.xs_lo, p.rowscale, p.m, p.n, p.k, remap, p.tail, p.accumulate);
+            hipLaunchKernelGGL((gemm_kernel<DT, 64, BN, 2>), dim3(grid), dim3(2 * BN), 0, s, YULE_GEMM_ARGS);
         else
-            hipLaunchKernelGGL((gemm_kernel<DT, 128, BN, 2>), dim3(grid), dim3(2 * BN), 0, s, p.w, p.xh, p.xl, p.y,
-                               p.xs_hi, p.xs_lo, p.rowscale, p.m, p.n, p.k, remap, p.tail, p.accumulate);
+            hipLaunchKernelGGL((gemm_kernel<DT, 128, BN, 2>), dim3(grid), dim3(2 * BN), 0, s, YULE_GEMM_ARGS);
     } else if (bm == 64) {
-        hipLaunchKernelGGL((gemm_kernel<DT, 64, BN, 1>), dim3(grid), dim3(2 * BN), 0, s, p.w, p.xh, p.xl, p.y, p.xs_hi,
-                           p.xs_lo, p.rowscale, p.m, p.n, p.k, remap, p.tail, p.accumulate);
+        hipLaunchKernelGGL((gemm_kernel<DT, 64, BN, 1>), dim3(grid), dim3(2 * BN), 0, s, YULE_GEMM_ARGS);
     } else {
-        hipLaunchKernelGGL((gemm_kernel<DT, 128, BN, 1>), dim3(grid), dim3(2 * BN), 0, s, p.w, p.xh, p.xl, p.y, p.xs_hi,
-                           p.xs_lo, p.rowscale, p.m, p.n, p.k, remap, p.tail, p.accumulate);
+        hipLaunchKernelGGL((gemm_kernel<DT, 128, BN, 1>), dim3(grid), dim3(2 * BN), 0, s, YULE_GEMM_ARGS);
     }
+#undef YULE_GEMM_ARGS
 }
 
 template <uint32_t DT>

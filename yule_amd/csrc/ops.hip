@@ -986,9 +986,10 @@ constexpr uint32_t kChunkMaxCombine = 1024;   // chunks per head (the runner use
 
 template <uint32_t HD>
 __global__ __launch_bounds__(kChunkThreads) void attn_chunk_kernel(
+    // the leading 14 dwords arrive preloaded in SGPRs
     const float *__restrict__ q, const float *__restrict__ kc, const float *__restrict__ vc,
-    const uint32_t *__restrict__ ctl, float *__restrict__ out, float *__restrict__ part, float2 *__restrict__ ml,
-    uint32_t *__restrict__ ticket, uint32_t group, uint32_t n_kv, uint32_t seq_host, uint32_t max_rows,
+    const uint32_t *__restrict__ ctl, uint32_t group, uint32_t n_kv, uint32_t seq_host, uint32_t max_rows,
+    float *__restrict__ out, float *__restrict__ part, float2 *__restrict__ ml, uint32_t *__restrict__ ticket,
     uint32_t max_chunks) {
     constexpr uint32_t NT = kChunkThreads, ND4 = HD / 4;
     constexpr uint32_t LPP = HD / 16;          // lanes per position in the scores, four float4 each
@@ -1164,11 +1165,11 @@ int launch_attn_chunks(hipStream_t s, const float *q, const float *kc, const flo
     uint32_t *ticket = reinterpret_cast<uint32_t *>(ml + (size_t)n_heads * mc);
     const dim3 grid(n_heads, mc);
     if (hd == 64)
-        hipLaunchKernelGGL(attn_chunk_kernel<64>, grid, dim3(kChunkThreads), 0, s, q, kc, vc, ctl, out, part, ml,
-                           ticket, n_heads / n_kv, n_kv, seq_host, max_rows, mc);
+        hipLaunchKernelGGL(attn_chunk_kernel<64>, grid, dim3(kChunkThreads), 0, s, q, kc, vc, ctl, n_heads / n_kv,
+                           n_kv, seq_host, max_rows, out, part, ml, ticket, mc);
     else
-        hipLaunchKernelGGL(attn_chunk_kernel<128>, grid, dim3(kChunkThreads), 0, s, q, kc, vc, ctl, out, part, ml,
-                           ticket, n_heads / n_kv, n_kv, seq_host, max_rows, mc);
+        hipLaunchKernelGGL(attn_chunk_kernel<128>, grid, dim3(kChunkThreads), 0, s, q, kc, vc, ctl, n_heads / n_kv,
+                           n_kv, seq_host, max_rows, out, part, ml, ticket, mc);
     return check_launch("attn_chunks");
 }
 

@@ -128,7 +128,9 @@ struct RawPair {
 // a team computes row r of both and stores silu(g)*u into segment 0's
 // output (model_runner.rs:963-972), so SwiGLU costs nothing extra.
 template <class F, int W, int D, int NT, bool PAIR, bool TWO>
-__global__ __launch_bounds__(NT) void qmv_stream_kernel(const Segs sg, const float *__restrict__ x, uint32_t bpr,
+__global__ __launch_bounds__(NT) void qmv_stream_kernel(const uint8_t *vb0, const uint8_t *vb1, const uint8_t *vb2,
+                                                        const float *__restrict__ x, uint32_t st1, uint32_t st2,
+                                                        uint32_t n_rows, uint32_t bpr, const Segs sg,
                                                         const QmvXf xf) {
     static_assert(!PAIR || W <= 64, "paired rows need single-wave teams");
     constexpr uint32_t RI = NT / W;                   // rows per workgroup iteration
@@ -138,7 +140,15 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const Segs sg, const flo
     extern __shared__ float xl[];
     __shared__ float part[NWV];
     const uint32_t tid = threadIdx.x, team = tid / W, t = tid % W;
-    const uint32_t units = bpr * F::UPB, n_rows = PAIR ? sg.start[1] : sg.total;
+    // The leading scalar arguments (segment bases, x, row starts, row count,
+    // bpr: 12 dwords) arrive preloaded in SGPRs (-amdgpu-kernarg-preload-
+    // count), so the first weight and x loads issue without waiting for a
+    // kernel-argument load.  vbI = segment I's weights moved back by its
+    // first row (PAIR: the gate and up weights themselves); stI = first
+    // concatenated row of segment I.  At most kStreamSegs segments.
+    const uint8_t *const vbv[kStreamSegs] = {vb0, vb1, vb2};
+    const uint32_t stv[kStreamSegs] = {0u, st1, st2};
+    const uint32_t units = bpr * F::UPB;
     const size_t row_bytes = (size_t)bpr * F::BB;
     const bool active = t < units;
     const uint32_t k = active ? t / F::UPB : 0, sub = t % F::UPB;
@@ -154,7 +164,7 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const Segs sg, const flo
     auto seg_of = [&](uint32_t row) {
         uint32_t s = 0;
 #pragma unroll
-        for (int i = 1; i < kMaxSegs; i++) s += row >= sg.start[i];
+        for (int i = 1; i < kStreamSegs; i++) s += row >= stv[i];
         return s;
     };
     auto fetch = [&](uint32_t rbase) -> Buf {
@@ -162,13 +172,12 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const Segs sg, const flo
         row = uni(row < n_rows ? row : n_rows - 1);
         if constexpr (PAIR) {
             const size_t off = (size_t)row * row_bytes + (size_t)k * F::BB;
-            return {F::load(sg.w[0] + off, sub), F::load(sg.w[1] + off, sub)};
+            return {F::load(vb0 + off, sub), F::load(vb1 + off, sub)};
         } else {
             const uint32_t s = seg_of(row);
-            const uint8_t *wb = sg.w[0] - (size_t)sg.start[0] * row_bytes;
+            const uint8_t *wb = vb0;
 #pragma unroll
-            for (int i = 1; i < kMaxSegs; i++)
-                wb = s == (uint32_t)i ? sg.w[i] - (size_t)sg.start[i] * row_bytes : wb;
+            for (int i = 1; i < kStreamSegs; i++) wb = s == (uint32_t)i ? vbv[i] : wb;
             return F::load(wb + (size_t)row * row_bytes + (size_t)k * F::BB, sub);
         }
     };
@@ -177,9 +186,9 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const Segs sg, const flo
     // with a wave-uniform row pass it through uni() first
     auto store = [&](uint32_t row, float v) {
         const uint32_t s = seg_of(row);
-        float *yb = sg.y[0] - sg.start[0];
+        float *yb = sg.y[0];
 #pragma unroll
-        for (int i = 1; i < kMaxSegs; i++) yb = s == (uint32_t)i ? sg.y[i] - sg.start[i] : yb;
+        for (int i = 1; i < kStreamSegs; i++) yb = s == (uint32_t)i ? sg.y[i] - stv[i] : yb;
         if (xf.epi == kEpiAdd) v = yb[row] + v;   // residual + projection (model_runner.rs:782-784)
         yb[row] = v;
         if (xf.epi == kEpiArgmax) {
@@ -279,7 +288,7 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const Segs sg, const flo
             // (row bases are even): the pair meets across lane W
             const float other = __shfl_xor(acc, W, 64);
             const uint32_t row = rbase + team;
-            const uint32_t s = seg_of(row < n_rows ? row : n_rows - 1), loc = row - sg.start[s < kMaxSegs ? s : 0];
+            const uint32_t s = seg_of(row < n_rows ? row : n_rows - 1), loc = row - stv[s < kStreamSegs ? s : 0];
             const uint32_t i = (loc % xf.hd) / 2;
             const float c = __shfl(rcos, (int)i, 64), sn = __shfl(rsin, (int)i, 64);
             const bool even = (loc & 1u) == 0;
@@ -287,7 +296,7 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const Segs sg, const flo
             float v = acc;
             if (s < 2) v = even ? x0 * c - x1 * sn : x0 * sn + x1 * c;
             if (t == 0 && row < n_rows) {
-                const size_t kvd = (size_t)(sg.start[2] - sg.start[1]);
+                const size_t kvd = (size_t)(st2 - st1);
                 if (s == 0) sg.y[0][loc] = v;
                 else (s == 1 ? xf.kc : xf.vc)[(size_t)rpos * kvd + loc] = v;
             }
@@ -356,19 +365,25 @@ template <class F, int W, int D, int NT>
 static void launch_stream_d(hipStream_t s, const Segs &sg, const float *x, uint32_t bpr, uint32_t blocks,
                             const QmvXf &xf) {
     const size_t lds = (size_t)lds_pad(bpr * F::BS) * sizeof(float);
+    const size_t row_bytes = (size_t)bpr * F::BB;
+    const uint8_t *vb[kStreamSegs];
+    for (int i = 0; i < kStreamSegs; i++) vb[i] = xf.pair ? sg.w[i] : sg.w[i] - (size_t)sg.start[i] * row_bytes;
+    const uint32_t n_rows = xf.pair ? sg.start[1] : sg.total;
+#define YULE_QMV_ARGS vb[0], vb[1], vb[2], x, sg.start[1], sg.start[2], n_rows, bpr, sg, xf
     if constexpr (W <= 64) {
         if (xf.pair) {   // always with a transform (checked by launch_qmv_fused)
-            hipLaunchKernelGGL((qmv_stream_kernel<F, W, D, NT, true, true>), dim3(blocks), dim3(NT), lds, s, sg, x,
-                               bpr, xf);
+            hipLaunchKernelGGL((qmv_stream_kernel<F, W, D, NT, true, true>), dim3(blocks), dim3(NT), lds, s,
+                               YULE_QMV_ARGS);
             return;
         }
     }
     if (xf.mode != kXfNone)
-        hipLaunchKernelGGL((qmv_stream_kernel<F, W, D, NT, false, true>), dim3(blocks), dim3(NT), lds, s, sg, x, bpr,
-                           xf);
+        hipLaunchKernelGGL((qmv_stream_kernel<F, W, D, NT, false, true>), dim3(blocks), dim3(NT), lds, s,
+                           YULE_QMV_ARGS);
     else
-        hipLaunchKernelGGL((qmv_stream_kernel<F, W, D, NT, false, false>), dim3(blocks), dim3(NT), lds, s, sg, x,
-                           bpr, xf);
+        hipLaunchKernelGGL((qmv_stream_kernel<F, W, D, NT, false, false>), dim3(blocks), dim3(NT), lds, s,
+                           YULE_QMV_ARGS);
+#undef YULE_QMV_ARGS
 }
 
 // Workgroup shape: NT threads (RI = NT / W teams) share one LDS copy of the
@@ -428,6 +443,10 @@ static int launch_fmt(hipStream_t s, const QmvSeg *segs, uint32_t n_seg, const f
         }
         for (uint32_t i = n_seg; i < kMaxSegs; i++) sg.start[i] = total;
         sg.total = total;
+        if (n_seg > (uint32_t)kStreamSegs) {   // as two launches (no fused epilogue spans matrices here)
+            const int rc = launch_fmt<F>(s, segs, kStreamSegs, x, n_cols, xf);
+            return rc ? rc : launch_fmt<F>(s, segs + kStreamSegs, n_seg - kStreamSegs, x, n_cols, xf);
+        }
         if (units <= 16) return launch_stream<F, 16>(s, sg, x, bpr, xf), YULE_OK;
         if (units <= 32) return launch_stream<F, 32>(s, sg, x, bpr, xf), YULE_OK;
         if (units <= 64) return launch_stream<F, 64>(s, sg, x, bpr, xf), YULE_OK;

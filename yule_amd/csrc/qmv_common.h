@@ -40,6 +40,8 @@ __device__ __forceinline__ uint32_t argmax_row(unsigned long long key) {
 
 // Up to kMaxSegs matrices sharing one activation vector (same n_cols and
 // format) run as one launch over their concatenated rows: Q/K/V, gate/up.
+// matrices per streaming-kernel launch (larger requests take two launches)
+constexpr int kStreamSegs = 3;
 struct Segs {
     const uint8_t *w[kMaxSegs];
     float *y[kMaxSegs];
