@@ -108,10 +108,11 @@ __device__ __forceinline__ void align_raw(const uint32_t *raw, uint32_t mis, uin
 // {0,2,1,3} order; for f32 input also xl = f16(x * s - xh); the Q4_K min
 // term's sub-block sums of x * s as f16 hi + lo; rowscale[m] = 1 / s.
 template <bool F32>
-__global__ __launch_bounds__(256) void gemm_xprep_kernel(const void *__restrict__ xin, _Float16 *__restrict__ xh,
+// (inputs first: the leading 14 dwords arrive preloaded in SGPRs)
+__global__ __launch_bounds__(256) void gemm_xprep_kernel(const void *__restrict__ xin, const float *__restrict__ nw,
+                                                         uint32_t K, float eps, _Float16 *__restrict__ xh,
                                                          _Float16 *__restrict__ xl, _Float16 *__restrict__ hi,
-                                                         _Float16 *__restrict__ lo, float *__restrict__ rowscale,
-                                                         uint32_t K, const float *__restrict__ nw, float eps) {
+                                                         _Float16 *__restrict__ lo, float *__restrict__ rowscale) {
     __shared__ float red[4], red2[4];
     const uint32_t m = blockIdx.x, tid = threadIdx.x, nch = K / 8;
     auto load8 = [&](uint32_t c, float *v) {
@@ -969,11 +970,11 @@ static int gemm_enqueue(hipStream_t s, const GemmW &w, const void *x, bool f32x,
     float *rowscale = reinterpret_cast<float *>(
         (reinterpret_cast<uintptr_t>(xh + (f32x ? 2 : 1) * g.n_x + (g.q4 ? 2 * g.n_sub : 0)) + 255) & ~(uintptr_t)255);
     if (f32x)
-        hipLaunchKernelGGL(gemm_xprep_kernel<true>, dim3(m), dim3(256), 0, s, x, xh, xl, xs_hi, xs_lo, rowscale, n_cols,
-                           norm_w, eps);
+        hipLaunchKernelGGL(gemm_xprep_kernel<true>, dim3(m), dim3(256), 0, s, x, norm_w, n_cols, eps, xh, xl, xs_hi,
+                           xs_lo, rowscale);
     else
-        hipLaunchKernelGGL(gemm_xprep_kernel<false>, dim3(m), dim3(256), 0, s, x, xh, xl, xs_hi, xs_lo, rowscale,
-                           n_cols, norm_w, eps);
+        hipLaunchKernelGGL(gemm_xprep_kernel<false>, dim3(m), dim3(256), 0, s, x, norm_w, n_cols, eps, xh, xl, xs_hi,
+                           xs_lo, rowscale);
     int rc = check_launch("quantized_gemm: x pre-pass");
     if (rc) return rc;
     const GemmPass p{w, xh, xl, xs_hi, xs_lo, rowscale, g.ks > 1 ? part : y, m, n_rows, n_cols, g.ks, g.bn, g.bm,
