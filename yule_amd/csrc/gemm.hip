@@ -110,13 +110,26 @@ __device__ __forceinline__ void align_raw(const uint32_t *raw, uint32_t mis, uin
 template <bool F32>
 // (inputs first: the leading 14 dwords arrive preloaded in SGPRs)
 __global__ __launch_bounds__(256) void gemm_xprep_kernel(const void *__restrict__ xin, const float *__restrict__ nw,
-                                                         uint32_t K, float eps, _Float16 *__restrict__ xh,
-                                                         _Float16 *__restrict__ xl, _Float16 *__restrict__ hi,
-                                                         _Float16 *__restrict__ lo, float *__restrict__ rowscale) {
+                                                         uint32_t K, float eps, uint32_t glu,
+                                                         _Float16 *__restrict__ xh, _Float16 *__restrict__ xl,
+                                                         _Float16 *__restrict__ hi, _Float16 *__restrict__ lo,
+                                                         float *__restrict__ rowscale) {
     __shared__ float red[4], red2[4];
     const uint32_t m = blockIdx.x, tid = threadIdx.x, nch = K / 8;
     auto load8 = [&](uint32_t c, float *v) {
         if constexpr (F32) {
+            if (glu) {
+                // rows held as [gate | up] (2K wide): x = gate * sigmoid(gate) * up
+                // (SwiGLU, model_runner.rs:967-972, as the eltwise form computes it)
+                const float *g = static_cast<const float *>(xin) + (size_t)m * 2 * K + 8 * c;
+                const float4 a = reinterpret_cast<const float4 *>(g)[0], b = reinterpret_cast<const float4 *>(g)[1];
+                const float4 ua = reinterpret_cast<const float4 *>(g + K)[0], ub = reinterpret_cast<const float4 *>(g + K)[1];
+                const float gv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+                const float uv[8] = {ua.x, ua.y, ua.z, ua.w, ub.x, ub.y, ub.z, ub.w};
+#pragma unroll
+                for (int t = 0; t < 8; t++) v[t] = gv[t] * (1.0f / (1.0f + expf(-gv[t]))) * uv[t];
+                return;
+            }
             const float4 *p = reinterpret_cast<const float4 *>(static_cast<const float *>(xin) + (size_t)m * K + 8 * c);
             const float4 a = p[0], b = p[1];
             v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
@@ -961,7 +974,7 @@ static GemmW one_matrix(const uint8_t *w, uint32_t n_rows) { return GemmW{{w, w,
 // add into Y in either order)
 static int gemm_enqueue(hipStream_t s, const GemmW &w, const void *x, bool f32x, float *y, uint32_t m,
                         uint32_t n_rows, uint32_t n_cols, uint32_t dtype, const GemmWork &g, void *ws,
-                        bool accumulate = false, const float *norm_w = nullptr, float eps = 0.f) {
+                        bool accumulate = false, const float *norm_w = nullptr, float eps = 0.f, bool glu = false) {
     uint8_t *b = static_cast<uint8_t *>(ws);
     float *part = g.ks > 1 ? reinterpret_cast<float *>(b) : nullptr;
     _Float16 *xh = reinterpret_cast<_Float16 *>(b + g.part_bytes);
@@ -970,11 +983,11 @@ static int gemm_enqueue(hipStream_t s, const GemmW &w, const void *x, bool f32x,
     float *rowscale = reinterpret_cast<float *>(
         (reinterpret_cast<uintptr_t>(xh + (f32x ? 2 : 1) * g.n_x + (g.q4 ? 2 * g.n_sub : 0)) + 255) & ~(uintptr_t)255);
     if (f32x)
-        hipLaunchKernelGGL(gemm_xprep_kernel<true>, dim3(m), dim3(256), 0, s, x, norm_w, n_cols, eps, xh, xl, xs_hi,
-                           xs_lo, rowscale);
+        hipLaunchKernelGGL(gemm_xprep_kernel<true>, dim3(m), dim3(256), 0, s, x, norm_w, n_cols, eps, glu ? 1u : 0u,
+                           xh, xl, xs_hi, xs_lo, rowscale);
     else
-        hipLaunchKernelGGL(gemm_xprep_kernel<false>, dim3(m), dim3(256), 0, s, x, norm_w, n_cols, eps, xh, xl, xs_hi,
-                           xs_lo, rowscale);
+        hipLaunchKernelGGL(gemm_xprep_kernel<false>, dim3(m), dim3(256), 0, s, x, norm_w, n_cols, eps, 0u, xh, xl,
+                           xs_hi, xs_lo, rowscale);
     int rc = check_launch("quantized_gemm: x pre-pass");
     if (rc) return rc;
     const GemmPass p{w, xh, xl, xs_hi, xs_lo, rowscale, g.ks > 1 ? part : y, m, n_rows, n_cols, g.ks, g.bn, g.bm,
@@ -1063,11 +1076,13 @@ size_t yule::gemm_f32_workspace_bytes(uint32_t m, uint32_t n_rows, uint32_t n_co
 }
 
 int yule::launch_gemm_f32(hipStream_t s, const uint8_t *w, const float *x, float *y, uint32_t m, uint32_t n_rows,
-                          uint32_t n_cols, uint32_t dtype, void *ws, bool accumulate, const float *norm_w, float eps) {
+                          uint32_t n_cols, uint32_t dtype, void *ws, bool accumulate, const float *norm_w, float eps,
+                          bool glu) {
     if (!gemm_dtype_ok(dtype) || n_cols % 256) return set_error(YULE_ERR_UNSUPPORTED, "gemm: format or shape");
+    if (glu && norm_w) return set_error(YULE_ERR_INVALID, "gemm: SwiGLU input and RMSNorm together");
     if (!m || !n_rows) return YULE_OK;
     return gemm_enqueue(s, one_matrix(w, n_rows), x, true, y, m, n_rows, n_cols, dtype,
-                        gemm_work(m, n_rows, n_cols, dtype, true), ws, accumulate, norm_w, eps);
+                        gemm_work(m, n_rows, n_cols, dtype, true), ws, accumulate, norm_w, eps, glu);
 }
 
 // Several matrices of one format and width that share X, as one product

@@ -145,10 +145,12 @@ int launch_gemm_f32_multi(hipStream_t stream, const uint8_t *const *w, const uin
                           const float *x, float *y, uint32_t m, uint32_t n_cols, uint32_t dtype, void *ws,
                           const float *norm_w = nullptr, float eps = 0.f);
 // accumulate: Y += X W (the residual add of the output and down projections);
-// norm_w: X's rows RMS-normalised and scaled by norm_w (eps) on the way in
+// norm_w: X's rows RMS-normalised and scaled by norm_w (eps) on the way in;
+// glu: x holds [gate | up] rows (2 n_cols wide) and X = gate * sigmoid(gate)
+// * up, formed on the way in (the down projection after a gate|up product)
 int launch_gemm_f32(hipStream_t stream, const uint8_t *w, const float *x, float *y, uint32_t m, uint32_t n_rows,
                     uint32_t n_cols, uint32_t dtype, void *ws, bool accumulate = false, const float *norm_w = nullptr,
-                    float eps = 0.f);
+                    float eps = 0.f, bool glu = false);
 // batched prompt pass (prefill.hip)
 int launch_embed_rows_batch(hipStream_t stream, uint32_t dtype, const uint8_t *table, const uint32_t *tokens,
                             uint32_t vocab, float *out, uint32_t dim, uint32_t n);
@@ -159,8 +161,6 @@ int launch_rope_rows(hipStream_t stream, float *q, const float *k, const float *
 bool attn_prefill_supported(uint32_t hd);
 int launch_attn_prefill(hipStream_t stream, const float *q, const float *kc, const float *vc, float *out, uint32_t pos0,
                         uint32_t n, uint32_t n_heads, uint32_t n_kv, uint32_t hd, uint32_t ldq);
-// out [n][ff] = SwiGLU of rows held as [gate | up] ([n][2 ff])
-int launch_swiglu_rows(hipStream_t stream, const float *gu, float *out, uint32_t ff, uint32_t n);
 // one launch of an empty kernel (launch-overhead probe)
 int launch_empty(hipStream_t stream);
 // out[i] = value for i < n

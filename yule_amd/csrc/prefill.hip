@@ -190,20 +190,6 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float *__restri
     }
 }
 
-// ---- SwiGLU of rows held as [gate | up] (one gate/up product): out[p][i] =
-// gate * sigmoid(gate) * up (model_runner.rs:967-972, the eltwise form)
-__global__ void swiglu_rows_kernel(const float *__restrict__ gu, float *__restrict__ out, uint32_t ff) {
-    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x, p = blockIdx.y;
-    if (i >= ff) return;
-    const float g = gu[(size_t)p * 2 * ff + i], u = gu[(size_t)p * 2 * ff + ff + i];
-    out[(size_t)p * ff + i] = g * (1.0f / (1.0f + expf(-g))) * u;
-}
-
-int launch_swiglu_rows(hipStream_t s, const float *gu, float *out, uint32_t ff, uint32_t n) {
-    hipLaunchKernelGGL(swiglu_rows_kernel, dim3((ff + 255) / 256, n), dim3(256), 0, s, gu, out, ff);
-    return check_launch("swiglu rows");
-}
-
 bool attn_prefill_supported(uint32_t hd) { return hd == 32 || hd == 64 || hd == 128 || hd == 256; }
 
 int launch_attn_prefill(hipStream_t s, const float *q, const float *kc, const float *vc, float *out, uint32_t pos0,

@@ -374,17 +374,20 @@ int prefill_rows(yule_hip_runner *r, uint32_t pos0, uint32_t n, uint32_t prompt_
             (rc = launch_gemm_f32(s, L.wo, r->ba, r->bx, n, r->dim, qd, L.to, ws, true)))   // residual += O
             return rc;
         // gate and up: one [gate | up] product when they share a format
-        if (gu_one(r, L)) {
+        // (one [gate | up] product: SwiGLU is formed in the down product's X
+        // pre-pass)
+        const bool gu = gu_one(r, L);
+        if (gu) {
             const uint8_t *w[2] = {L.wg, L.wu};
-            if ((rc = launch_gemm_f32_multi(s, w, gu_rows, 2, r->bx, r->bgu, n, r->dim, L.tg, ws, L.ffn_norm, r->eps)) ||
-                (rc = launch_swiglu_rows(s, r->bgu, r->bg, r->ff, n)))
+            if ((rc = launch_gemm_f32_multi(s, w, gu_rows, 2, r->bx, r->bgu, n, r->dim, L.tg, ws, L.ffn_norm, r->eps)))
                 return rc;
         } else if ((rc = launch_gemm_f32(s, L.wg, r->bx, r->bg, n, r->ff, r->dim, L.tg, ws, false, L.ffn_norm, r->eps)) ||
                    (rc = launch_gemm_f32(s, L.wu, r->bx, r->bu, n, r->ff, r->dim, L.tu, ws, false, L.ffn_norm, r->eps)) ||
                    (rc = launch_eltwise(s, 3, r->bg, r->bu, r->bg, n * r->ff))) {
             return rc;
         }
-        if ((rc = launch_gemm_f32(s, L.wd, r->bg, r->bx, n, r->dim, r->ff, L.td, ws, true)))   // residual += down
+        if ((rc = launch_gemm_f32(s, L.wd, gu ? r->bgu : r->bg, r->bx, n, r->dim, r->ff, L.td, ws, true, nullptr, 0.f,
+                                  gu)))   // residual += down
             return rc;
     }
     if ((rc = hip_error(hipMemcpyAsync(r->hidden, r->bx + (size_t)(n - 1) * r->dim, (size_t)r->dim * 4,
