@@ -699,6 +699,17 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
         sweep();
     }
 
+    // the row scales of this lane's output rows, loaded now so that the
+    // stores below wait on nothing (a load issued after stores would wait
+    // for them too: loads and stores share one counter)
+    float rs[TM][4];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const uint32_t m = m0 + wm * (BM / 2) + i * 16 + 4 * (lane >> 4) + e;
+            rs[i][e] = rowscale[m < M ? m : M - 1u];
+        }
     if (Q4 && xs_hi) {   // (no sums: the second, lo, product of an f32 X)
         // min term: acc -= sum_j xsum[m][j] * (dmin*mn)[r][j] over the K/32
         // sub-blocks.  In chunks of four super-blocks the workgroup stages
@@ -786,7 +797,7 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
             for (int e = 0; e < 4; e++) {
                 const uint32_t m = m0 + wm * (BM / 2) + i * 16 + 4 * (lane >> 4) + e;
                 if (m < M && r < N) {
-                    const float v = acc[i][j][e] * rowscale[m];   // the row's power of two back out: exact
+                    const float v = acc[i][j][e] * rs[i][e];   // the row's power of two back out: exact
                     if (halves) unsafeAtomicAdd(y + (size_t)m * N + r, v);
                     else if (accumulate && splits == 1) y[(size_t)m * N + r] += v;
                     else y[(size_t)m * N + r] = v;
