@@ -187,16 +187,25 @@ __global__ __launch_bounds__(256) void gemm_xprep_kernel(const void *__restrict_
     const bool scaled = amax > 0.f && amax <= 3.402823466e38f;
     const float sc = scaled ? ldexpf(1.0f, es) : 1.0f;
     const int perm[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+    // The next chunk's loads are issued before this chunk's stores: a load
+    // issued after stores would wait for them (one counter for both).
+    float nv[8], nwv[8];
+    load8(tid < nch ? tid : 0u, nv);
+    if (nw) loadw8(tid < nch ? tid : 0u, nwv);
     for (uint32_t c0 = 0; c0 < nch; c0 += 256) {   // uniform trip count: the quad sums below need every lane
         const uint32_t c = c0 + tid;
         const bool ok = c < nch;
         float v[8];
-        load8(ok ? c : 0u, v);
-        if (nw) {
-            float wv[8];
-            loadw8(ok ? c : 0u, wv);
 #pragma unroll
-            for (int t = 0; t < 8; t++) v[t] = v[t] * inv * wv[t];
+        for (int t = 0; t < 8; t++) v[t] = nv[t];
+        if (nw) {
+#pragma unroll
+            for (int t = 0; t < 8; t++) v[t] = v[t] * inv * nwv[t];
+        }
+        if (c0 + 256 < nch) {
+            const uint32_t cn = c + 256 < nch ? c + 256 : 0u;
+            load8(cn, nv);
+            if (nw) loadw8(cn, nwv);
         }
         float s = 0.f;
         uint32_t oh[4], ol[4];
