@@ -130,7 +130,8 @@ struct RawPair {
 template <class F, int W, int D, int NT, bool PAIR, bool TWO>
 __global__ __launch_bounds__(NT) void qmv_stream_kernel(const uint8_t *vb0, const uint8_t *vb1, const uint8_t *vb2,
                                                         const float *__restrict__ x, uint32_t st1, uint32_t st2,
-                                                        uint32_t n_rows, uint32_t bpr, const Segs sg,
+                                                        uint32_t n_rows, uint32_t bpr,
+                                                        const uint32_t *__restrict__ rope_ctl, const Segs sg,
                                                         const QmvXf xf) {
     static_assert(!PAIR || W <= 64, "paired rows need single-wave teams");
     constexpr uint32_t RI = NT / W;                   // rows per workgroup iteration
@@ -141,9 +142,9 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const uint8_t *vb0, cons
     __shared__ float part[NWV];
     const uint32_t tid = threadIdx.x, team = tid / W, t = tid % W;
     // The leading scalar arguments (segment bases, x, row starts, row count,
-    // bpr: 12 dwords) arrive preloaded in SGPRs (-amdgpu-kernarg-preload-
-    // count), so the first weight and x loads issue without waiting for a
-    // kernel-argument load.  vbI = segment I's weights moved back by its
+    // bpr, the RoPE control block: 14 dwords) arrive preloaded in SGPRs
+    // (-amdgpu-kernarg-preload-count), so the first weight and x loads issue
+    // without waiting for a kernel-argument load.  vbI = segment I's weights moved back by its
     // first row (PAIR: the gate and up weights themselves); stI = first
     // concatenated row of segment I.  At most kStreamSegs segments.
     const uint8_t *const vbv[kStreamSegs] = {vb0, vb1, vb2};
@@ -212,6 +213,11 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const uint8_t *vb0, cons
     // TWO: a fused input transform is on (its operand is loaded with x); a
     // template parameter, so the plain kernels carry none of its code
     {
+        // kEpiRope: the position first of all, so that the table loads below,
+        // which need it, wait for it alone and not for the x and weight loads
+        // behind it (loads complete in issue order)
+        uint32_t pos_early = 0;
+        if (W < 64 && rope_ctl) pos_early = rope_ctl[0];
         const uint32_t n = bpr * F::BS, n4 = n / 4;
         const float4 *x4 = reinterpret_cast<const float4 *>(x), *a4 = reinterpret_cast<const float4 *>(xf.a);
         float4 xv[kXPer], av[kXPer];
@@ -230,7 +236,7 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const uint8_t *vb0, cons
             // RoPE epilogue: lane l keeps cos / sin of pair l of the position's
             // table row (unconditional loads from a valid address either way)
             const bool rope = xf.epi == kEpiRope;
-            rpos = rope ? xf.ctl[0] : 0u;
+            rpos = rope ? pos_early : 0u;
             const uint32_t half = rope ? xf.hd / 2 : 1u, li = (tid & 63u) % half;
             rcos = (rope ? xf.cos_t : x)[(size_t)rpos * half + li];
             rsin = (rope ? xf.sin_t : x)[(size_t)rpos * half + li];
@@ -369,7 +375,8 @@ static void launch_stream_d(hipStream_t s, const Segs &sg, const float *x, uint3
     const uint8_t *vb[kStreamSegs];
     for (int i = 0; i < kStreamSegs; i++) vb[i] = xf.pair ? sg.w[i] : sg.w[i] - (size_t)sg.start[i] * row_bytes;
     const uint32_t n_rows = xf.pair ? sg.start[1] : sg.total;
-#define YULE_QMV_ARGS vb[0], vb[1], vb[2], x, sg.start[1], sg.start[2], n_rows, bpr, sg, xf
+    const uint32_t *rope_ctl = xf.epi == kEpiRope ? xf.ctl : nullptr;
+#define YULE_QMV_ARGS vb[0], vb[1], vb[2], x, sg.start[1], sg.start[2], n_rows, bpr, rope_ctl, sg, xf
     if constexpr (W <= 64) {
         if (xf.pair) {   // always with a transform (checked by launch_qmv_fused)
             hipLaunchKernelGGL((qmv_stream_kernel<F, W, D, NT, true, true>), dim3(blocks), dim3(NT), lds, s,
