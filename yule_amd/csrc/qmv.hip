@@ -144,9 +144,10 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const uint8_t *vb0, cons
     // The leading scalar arguments (segment bases, x, row starts, row count,
     // bpr, the RoPE control block: 14 dwords) arrive preloaded in SGPRs
     // (-amdgpu-kernarg-preload-count), so the first weight and x loads issue
-    // without waiting for a kernel-argument load.  vbI = segment I's weights moved back by its
-    // first row (PAIR: the gate and up weights themselves); stI = first
-    // concatenated row of segment I.  At most kStreamSegs segments.
+    // without waiting for a kernel-argument load.  vbI = segment I's weights
+    // moved back by its first row (PAIR: the gate and up weights themselves);
+    // stI = first concatenated row of segment I.  At most kStreamSegs
+    // segments.  rope_ctl: the control block of a kEpiRope launch, else null.
     const uint8_t *const vbv[kStreamSegs] = {vb0, vb1, vb2};
     const uint32_t stv[kStreamSegs] = {0u, st1, st2};
     const uint32_t units = bpr * F::UPB;
@@ -157,10 +158,9 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const uint8_t *vb0, cons
     const uint32_t r0 = blockIdx.x * RI;
     if (r0 >= n_rows) return;   // uniform per workgroup
 
-    // concatenated row -> weight row pointer / output slot.  vbase[i] is
-    // segment i's weight base moved back by start[i] rows, so a row's
-    // address is vbase[seg] + row * row_bytes.  With whole-wave teams the
-    // row is wave-uniform and all of this runs on the scalar unit.
+    // concatenated row -> weight row pointer / output slot: a row's address
+    // is vbv[seg] + row * row_bytes.  With whole-wave teams the row is
+    // wave-uniform and all of this runs on the scalar unit.
     auto uni = [&](uint32_t v) { return W >= 64 ? __builtin_amdgcn_readfirstlane(v) : v; };
     auto seg_of = [&](uint32_t row) {
         uint32_t s = 0;
