@@ -38,9 +38,10 @@ __device__ __forceinline__ uint32_t argmax_row(unsigned long long key) {
     return k == kKeyPosInf || k == kKeyNegInf ? ~lo : lo;
 }
 
-// Up to kMaxSegs matrices sharing one activation vector (same n_cols and
-// format) run as one launch over their concatenated rows: Q/K/V, gate/up.
-// matrices per streaming-kernel launch (larger requests take two launches)
+// Matrices sharing one activation vector (same n_cols and format) run as
+// one launch over their concatenated rows (Q/K/V, gate/up): up to
+// kStreamSegs per streaming-kernel launch; the up to kMaxSegs of a request
+// take two launches beyond that.
 constexpr int kStreamSegs = 3;
 struct Segs {
     const uint8_t *w[kMaxSegs];
