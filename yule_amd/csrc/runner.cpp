@@ -64,10 +64,17 @@ struct yule_hip_runner {
     float last_prefill_ms = 0.f;
     hipGraph_t graph[2] = {nullptr, nullptr};
     hipGraphExec_t exec[2] = {nullptr, nullptr};
+    // multi_steps of the same step per graph: generate_greedy replays these
+    // over runs of decode steps of one variant (one graph launch per
+    // multi_steps tokens: each launch of a graph costs ~7 us of idle GPU)
+    uint32_t multi_steps = 8;
+    hipGraph_t graph_n[2] = {nullptr, nullptr};
+    hipGraphExec_t exec_n[2] = {nullptr, nullptr};
     uint32_t pos = 0;  // host mirror of ctl[0]
 };
 
 namespace {
+
 
 int set_ctl(yule_hip_runner *r, uint32_t pos, uint32_t token, uint32_t prompt_len);
 int enqueue_head(yule_hip_runner *r);
@@ -264,6 +271,28 @@ int ensure_graph(yule_hip_runner *r, bool split) {
     if (erc) return erc;
     if (rc) return rc;
     return hip_error(hipGraphInstantiate(&r->exec[split], r->graph[split], nullptr, nullptr, 0),
+                     "runner: graph instantiate");
+}
+
+// generate_greedy's runs of decode steps replay multi-step graphs (not with
+// YULE_RUNNER_NO_GRAPH, and not when the runner's multi_steps is 1)
+bool multi_ok(const yule_hip_runner *r) {
+    static const bool direct = getenv("YULE_RUNNER_NO_GRAPH") != nullptr;
+    return !direct && r->multi_steps > 1;
+}
+
+int ensure_graph_n(yule_hip_runner *r, bool split) {
+    const uint32_t n = r->multi_steps;
+    if (r->exec_n[split]) return YULE_OK;
+    hipStream_t s = r->be->stream;
+    int rc = hip_error(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "runner: begin capture");
+    if (rc) return rc;
+    int erc = YULE_OK;
+    for (uint32_t i = 0; i < n && !erc; i++) erc = enqueue_step(r, split);
+    rc = hip_error(hipStreamEndCapture(s, &r->graph_n[split]), "runner: end capture");
+    if (erc) return erc;
+    if (rc) return rc;
+    return hip_error(hipGraphInstantiate(&r->exec_n[split], r->graph_n[split], nullptr, nullptr, 0),
                      "runner: graph instantiate");
 }
 
@@ -495,6 +524,8 @@ int yule_hip_runner_create(yule_hip_backend *be, const yule_model_desc *d, yule_
         (rc = dev_alloc(r, split_scratch_bytes(r->n_heads, hd, r->max_seq), &r->attn_ws)))
         return fail(rc);
     r->fused = getenv("YULE_RUNNER_UNFUSED") == nullptr && qmv_fusable(r->out_t, r->dim);
+    // decode steps per replayed graph in generate_greedy (1: one per step)
+    if (const char *e = getenv("YULE_RUNNER_GRAPH_STEPS")) r->multi_steps = std::max(1, atoi(e));
     for (const auto &L : r->layers)
         r->fused = r->fused && qmv_fusable(L.tq, r->dim) && qmv_fusable(L.tk, r->dim) && qmv_fusable(L.tv, r->dim) &&
                    qmv_fusable(L.to, qd) && qmv_fusable(L.tg, r->dim) && qmv_fusable(L.tu, r->dim) &&
@@ -518,6 +549,8 @@ int yule_hip_runner_destroy(yule_hip_runner *r) {
     if (r->be) hipStreamSynchronize(r->be->stream);
     for (int i = 0; i < 2; i++) {
         if (r->exec[i]) hipGraphExecDestroy(r->exec[i]);
+        if (r->exec_n[i]) hipGraphExecDestroy(r->exec_n[i]);
+        if (r->graph_n[i]) hipGraphDestroy(r->graph_n[i]);
         if (r->graph[i]) hipGraphDestroy(r->graph[i]);
     }
     for (void *p : r->allocs) hipFree(p);
@@ -574,9 +607,13 @@ int yule_hip_runner_generate_greedy(yule_hip_runner *r, const uint32_t *prompt, 
         if (prompt[i] >= r->vocab) return set_error(YULE_ERR_INVALID, "runner_generate: token id out of range");
     hipStream_t s = r->be->stream;
     int rc;
-    // both graph variants the run needs are captured before the timed loop
+    // every graph the run needs is captured before the timed loop
     if ((rc = ensure_graph(r, false))) return rc;
     if (n_prompt + n_decode >= r->split_min && (rc = ensure_graph(r, true))) return rc;
+    if (multi_ok(r) && n_decode >= r->multi_steps) {
+        if (n_prompt + r->multi_steps < r->split_min && (rc = ensure_graph_n(r, false))) return rc;
+        if (n_prompt + n_decode >= r->split_min && (rc = ensure_graph_n(r, true))) return rc;
+    }
     if ((rc = hip_error(hipMemcpyAsync(r->prompt, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice, s),
                         "runner: prompt upload")))
         return rc;
@@ -594,7 +631,17 @@ int yule_hip_runner_generate_greedy(yule_hip_runner *r, const uint32_t *prompt, 
         if (rc) goto done;
     }
     if ((rc = hip_error(hipEventRecord(e0, s), "hipEventRecord"))) goto done;
-    for (uint32_t i = 0; i < n_decode && !rc; i++) rc = run_step(r, n_prompt + i);
+    for (uint32_t i = 0; i < n_decode && !rc;) {
+        const uint32_t pos = n_prompt + i, K = r->multi_steps;
+        const bool split = pos + 1 >= r->split_min;
+        if (multi_ok(r) && i + K <= n_decode && (pos + K >= r->split_min) == split) {
+            rc = hip_error(hipGraphLaunch(r->exec_n[split], r->be->stream), "runner: graph launch");
+            i += K;
+        } else {
+            rc = run_step(r, pos);
+            i++;
+        }
+    }
     if (rc || (rc = hip_error(hipEventRecord(e1, s), "hipEventRecord"))) goto done;
     if ((rc = hip_error(hipEventSynchronize(e1), "hipEventSynchronize"))) goto done;
     if (ms_per_decode_step) {
