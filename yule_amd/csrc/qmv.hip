@@ -399,7 +399,12 @@ static void launch_stream_d(hipStream_t s, const Segs &sg, const float *x, uint3
 template <class F, int W, int NT>
 static void launch_stream_nt(hipStream_t s, const Segs &sg, const float *x, uint32_t bpr, const QmvXf &xf) {
     constexpr uint32_t RI = NT / W;
-    static const int waves_env = env_int("YULE_QMV_WAVES_PER_CU", 16);
+    // paired gate/up launches are sized for 8 waves per CU: TinyLlama's 5632
+    // gate/up row pairs as 512 workgroups (two rounds for some) decode
+    // 1663 -> 1684 tok/s against 704 (4 or 6 waves: 1618)
+    static const int waves_all = env_int("YULE_QMV_WAVES_PER_CU", 16);
+    static const int waves_pair = env_int("YULE_QMV_PAIR_WAVES", 8);
+    const int waves_env = xf.pair ? waves_pair : waves_all;
     const size_t lds = (size_t)lds_pad(bpr * F::BS) * sizeof(float) + 512;
     const int wg_lds = (int)(kLdsPerCu / lds);
     const int wg_waves = waves_env / (NT / 64) > 0 ? waves_env / (NT / 64) : 1;
