@@ -115,7 +115,7 @@ def test_qmv_reference_generator_rows(hip, dt):
 
 
 SHAPES = [(1, 256), (3, 512), (7, 1024), (33, 2048), (255, 2048), (257, 4096), (300, 5632), (64, 14336),
-          (1000, 768), (4099, 256), (20, 20480), (9, 36864)]
+          (1000, 768), (4099, 256), (20, 20480), (9, 36864), (65, 11008)]
 
 
 @pytest.mark.parametrize("dt", FMTS, ids=lambda d: d.name)

@@ -111,7 +111,8 @@ static uint32_t pick_team(uint32_t units) {
 }
 
 // ---------------------------------------------------------------- streaming kernel
-// Rows stream through persistent workgroups.  A team of W lanes (16..512)
+// Rows stream through persistent workgroups.  A team of W lanes (16..512;
+// 192 = three waves, so rows of 129-192 units leave no wave idle)
 // covers a whole row, one unit per lane, so each lane's activation slice is
 // loaded into registers once for the life of the workgroup; the team then
 // walks rows row0, row0 + stride, ... with the next row's blocks already in
@@ -423,12 +424,15 @@ static void launch_stream(hipStream_t s, const Segs &sg, const float *x, uint32_
     // 512-thread workgroups; narrower teams (2048 columns) 6% slower there
     static const int nt_narrow = env_int("YULE_QMV_THREADS", 256), nt_wide = env_int("YULE_QMV_THREADS_WIDE", 1024);
     static const int nt_w64 = env_int("YULE_QMV_THREADS_W64", 512);
+    if constexpr (W == 192) return launch_stream_nt<F, W, 768>(s, sg, x, bpr, xf);   // four three-wave teams
+    else {
     const int nt = W >= 512 ? 1024 : W >= 128 ? nt_wide : W == 64 ? nt_w64 : nt_narrow;
     if (nt >= 1024) return launch_stream_nt<F, W, 1024>(s, sg, x, bpr, xf);
     if constexpr (W >= 512) return;   // unreachable: 512-lane teams only run in 1024-thread workgroups
     else
     if (nt >= 512) return launch_stream_nt<F, W, 512>(s, sg, x, bpr, xf);
     else launch_stream_nt<F, W, 256>(s, sg, x, bpr, xf);
+    }
 }
 
 // Largest activation vector staged in LDS by the streaming kernel (floats).
@@ -463,6 +467,7 @@ static int launch_fmt(hipStream_t s, const QmvSeg *segs, uint32_t n_seg, const f
         if (units <= 32) return launch_stream<F, 32>(s, sg, x, bpr, xf), YULE_OK;
         if (units <= 64) return launch_stream<F, 64>(s, sg, x, bpr, xf), YULE_OK;
         if (units <= 128) return launch_stream<F, 128>(s, sg, x, bpr, xf), YULE_OK;
+        if (units <= 192) return launch_stream<F, 192>(s, sg, x, bpr, xf), YULE_OK;
         if (units <= 256) return launch_stream<F, 256>(s, sg, x, bpr, xf), YULE_OK;
         return launch_stream<F, 512>(s, sg, x, bpr, xf), YULE_OK;
     }
