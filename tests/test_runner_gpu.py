@@ -187,6 +187,39 @@ def test_runner_attention_formats_and_head_sizes(hip, scheme, dim, hd):
     assert [int(t) for t in out] == want
 
 
+def test_runner_three_wave_team_rows(hip):
+    """Rows of 176 units (Q8_0, 5632 columns) run on three-wave teams in
+    every matvec of the step: RMSNorm staging into Q/K/V, gate and up
+    (unpaired: paired rows need one-wave teams) and the lm_head argmax, the
+    SwiGLU staging into down, the residual add on O and down.  Logits of 10
+    steps vs the oracle, then greedy tokens vs the oracle."""
+    from yule_amd.model import LlamaConfig
+    cfg = LlamaConfig(n_layers=1, dim=5632, n_heads=44, n_kv_heads=4, ff_dim=5632, vocab=512, max_seq=64)
+    m = SyntheticModel.generate(cfg, seed=23, scheme="Q8_0")
+    say("[runner] three-wave teams, Q8_0 dim 5632")
+    run = HipRunner(hip, m)
+    ref = oracle.Runner(m, n_threads=4)
+    try:
+        for i, t in enumerate(synth.uniform_tokens(35, 10, cfg.vocab)):
+            got, want = run.decode_step(int(t)), ref.forward(int(t))
+            assert np.max(np.abs(got - want)) <= tolerance_bar(want), f"step {i}"
+    finally:
+        run.close()
+    prompt = synth.uniform_tokens(36, 6, cfg.vocab)
+    run = HipRunner(hip, m)
+    out, _ = run.generate_greedy(prompt, 12)
+    run.close()
+    ref = oracle.Runner(m, n_threads=4)
+    for t in prompt:
+        logits = ref.forward(int(t))
+    want = []
+    for i in range(13):
+        want.append(oracle.argmax(logits))
+        if i < 12:
+            logits = ref.forward(want[-1])
+    assert [int(t) for t in out] == want
+
+
 @pytest.mark.parametrize("which", ["tiny", "hd64"])
 def test_runner_prefill_batched_matches_oracle(hip, tiny, which):
     """The prompt as one batched pass (GEMM projections, causal attention
