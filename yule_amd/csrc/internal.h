@@ -98,6 +98,14 @@ struct QmvXf {
     const float *cos_t = nullptr, *sin_t = nullptr;   // [max_seq][hd / 2]
     float *kc = nullptr, *vc = nullptr;               // [max_seq][n_kv * hd]
     uint32_t hd = 0;
+    // prefetch: pf_wgs extra workgroups (a multiple of 8, after the compute
+    // grid) read the following launch's matrix pf_w[0] (and pf_w[1], the up
+    // half of a gate/up pair, same rows) into the L2 of the XCD whose
+    // workgroups will read them: that launch's row group g (pf_gbytes bytes
+    // of each matrix, pf_total bytes in all) belongs to XCD g % 8
+    const uint8_t *pf_w[2] = {nullptr, nullptr};
+    uint32_t pf_wgs = 0, pf_gbytes = 0, pf_groups = 0, pf_delay = 0;
+    size_t pf_total = 0;
 };
 
 // Kernel launchers (device code in qmv.hip / ops.hip / attn.hip / gemm.hip).
@@ -110,6 +118,10 @@ int launch_qmv_multi(hipStream_t stream, uint32_t dtype, const QmvSeg *segs, uin
 bool qmv_fusable(uint32_t dtype, uint32_t n_cols);
 // true when gate/up of this shape can run as one paired launch (xf.pair)
 bool qmv_pairable(uint32_t dtype, uint32_t n_cols);
+// row-group size (bytes) and group count of a streaming launch of this shape
+// whose group g runs on XCD g % 8; false when its grid gives no such mapping
+bool qmv_group_plan(uint32_t dtype, uint32_t n_rows, uint32_t n_cols, bool pair, uint32_t *group_bytes,
+                    uint32_t *groups, uint32_t *rows_per_group);
 // lanes per row of the streaming matvec for this shape
 uint32_t qmv_team_width(uint32_t dtype, uint32_t n_cols);
 // true when the Q/K/V launch can apply RoPE and write the KV cache (kEpiRope)

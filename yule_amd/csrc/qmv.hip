@@ -131,7 +131,7 @@ struct RawPair {
 template <class F, int W, int D, int NT, bool PAIR, bool TWO>
 __global__ __launch_bounds__(NT) void qmv_stream_kernel(const uint8_t *vb0, const uint8_t *vb1, const uint8_t *vb2,
                                                         const float *__restrict__ x, uint32_t st1, uint32_t st2,
-                                                        uint32_t n_rows, uint32_t bpr,
+                                                        uint32_t n_rows, uint32_t bpr_pf,
                                                         const uint32_t *__restrict__ rope_ctl, const Segs sg,
                                                         const QmvXf xf) {
     static_assert(!PAIR || W <= 64, "paired rows need single-wave teams");
@@ -151,11 +151,31 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const uint8_t *vb0, cons
     // segments.  rope_ctl: the control block of a kEpiRope launch, else null.
     const uint8_t *const vbv[kStreamSegs] = {vb0, vb1, vb2};
     const uint32_t stv[kStreamSegs] = {0u, st1, st2};
+    // bpr_pf: blocks per row | compute workgroups << 16 (any further
+    // workgroups prefetch)
+    const uint32_t bpr = bpr_pf & 0xffffu, nblk = bpr_pf >> 16;
+    if (blockIdx.x >= nblk) {
+        const uint32_t pfw = gridDim.x - nblk;
+        // prefetch workgroup: one dword of every 128-byte line of the row
+        // groups that the next launch runs on this workgroup's XCD
+        for (uint32_t i = 0; i < xf.pf_delay; i++) __builtin_amdgcn_s_sleep(8);
+        const uint32_t xcd = blockIdx.x & 7u, rank = (blockIdx.x - nblk) >> 3, nr = pfw >> 3;
+        const uint32_t lpg = (xf.pf_gbytes + 127) / 128, nseg = xf.pf_w[1] ? 2u : 1u;
+        const uint32_t mine = xf.pf_groups > xcd + 8 * rank ? (xf.pf_groups - xcd - 8 * rank + 8 * nr - 1) / (8 * nr) : 0;
+        uint32_t acc = 0;
+        for (uint32_t j = tid; j < mine * lpg * nseg; j += NT) {
+            const uint32_t gi = j / (lpg * nseg), rem = j % (lpg * nseg), sgi = rem / lpg, line = rem % lpg;
+            const size_t off = (size_t)(xcd + 8 * (rank + gi * nr)) * xf.pf_gbytes + (size_t)line * 128;
+            if (off < xf.pf_total) acc ^= *reinterpret_cast<const uint32_t *>((sgi ? xf.pf_w[1] : xf.pf_w[0]) + off);
+        }
+        if (acc == 0x9E3779B9u && n_rows == 0) sg.y[0][0] = 0.f;   // keeps the loads; never true
+        return;
+    }
     const uint32_t units = bpr * F::UPB;
     const size_t row_bytes = (size_t)bpr * F::BB;
     const bool active = t < units;
     const uint32_t k = active ? t / F::UPB : 0, sub = t % F::UPB;
-    const uint32_t stride = gridDim.x * RI;
+    const uint32_t stride = nblk * RI;
     const uint32_t r0 = blockIdx.x * RI;
     if (r0 >= n_rows) return;   // uniform per workgroup
 
@@ -377,7 +397,9 @@ static void launch_stream_d(hipStream_t s, const Segs &sg, const float *x, uint3
     for (int i = 0; i < kStreamSegs; i++) vb[i] = xf.pair ? sg.w[i] : sg.w[i] - (size_t)sg.start[i] * row_bytes;
     const uint32_t n_rows = xf.pair ? sg.start[1] : sg.total;
     const uint32_t *rope_ctl = xf.epi == kEpiRope ? xf.ctl : nullptr;
-#define YULE_QMV_ARGS vb[0], vb[1], vb[2], x, sg.start[1], sg.start[2], n_rows, bpr, rope_ctl, sg, xf
+    const uint32_t bpr_pf = bpr | blocks << 16;
+    blocks += xf.pf_wgs;
+#define YULE_QMV_ARGS vb[0], vb[1], vb[2], x, sg.start[1], sg.start[2], n_rows, bpr_pf, rope_ctl, sg, xf
     if constexpr (W <= 64) {
         if (xf.pair) {   // always with a transform (checked by launch_qmv_fused)
             hipLaunchKernelGGL((qmv_stream_kernel<F, W, D, NT, true, true>), dim3(blocks), dim3(NT), lds, s,
@@ -394,27 +416,35 @@ static void launch_stream_d(hipStream_t s, const Segs &sg, const float *x, uint3
 #undef YULE_QMV_ARGS
 }
 
+// Compute workgroups of a streaming launch: about waves_env waves per CU, no
+// more than the LDS copies of x allow, no more than the row iterations.
+static uint32_t stream_blocks(uint32_t W, uint32_t NT, uint32_t bs, uint32_t bpr, uint32_t rows, bool pair,
+                              bool argmax) {
+    const uint32_t RI = NT / W;
+    static const int waves_all = env_int("YULE_QMV_WAVES_PER_CU", 16);
+    static const int waves_pair = env_int("YULE_QMV_PAIR_WAVES", 8);
+    const int waves_env = pair ? waves_pair : waves_all;
+    const size_t lds = (size_t)lds_pad(bpr * bs) * sizeof(float) + 512;
+    const int wg_lds = (int)(kLdsPerCu / lds);
+    const int wg_waves = waves_env / (int)(NT / 64) > 0 ? waves_env / (int)(NT / 64) : 1;
+    const int wg = wg_waves < wg_lds ? wg_waves : (wg_lds > 0 ? wg_lds : 1);
+    const uint32_t iters = (rows + RI - 1) / RI;
+    const uint32_t cap = (uint32_t)(device_cus() * wg);
+    uint32_t blocks = iters < cap ? iters : cap;
+    if (argmax && blocks > kArgmaxSlots) blocks = kArgmaxSlots;   // one slot per workgroup
+    return blocks;
+}
+
 // Workgroup shape: NT threads (RI = NT / W teams) share one LDS copy of the
 // activation vector; about 16 waves per CU are resident (4 per SIMD, the
 // VGPR limit), as NT-thread workgroups up to the LDS each copy takes.
 template <class F, int W, int NT>
 static void launch_stream_nt(hipStream_t s, const Segs &sg, const float *x, uint32_t bpr, const QmvXf &xf) {
-    constexpr uint32_t RI = NT / W;
     // paired gate/up launches are sized for 8 waves per CU: TinyLlama's 5632
     // gate/up row pairs as 512 workgroups (two rounds for some) decode
     // 1663 -> 1684 tok/s against 704 (4 or 6 waves: 1618)
-    static const int waves_all = env_int("YULE_QMV_WAVES_PER_CU", 16);
-    static const int waves_pair = env_int("YULE_QMV_PAIR_WAVES", 8);
-    const int waves_env = xf.pair ? waves_pair : waves_all;
-    const size_t lds = (size_t)lds_pad(bpr * F::BS) * sizeof(float) + 512;
-    const int wg_lds = (int)(kLdsPerCu / lds);
-    const int wg_waves = waves_env / (NT / 64) > 0 ? waves_env / (NT / 64) : 1;
-    const int wg = wg_waves < wg_lds ? wg_waves : (wg_lds > 0 ? wg_lds : 1);
     const uint32_t rows = xf.pair ? sg.start[1] : sg.total;
-    const uint32_t iters = (rows + RI - 1) / RI;
-    const uint32_t cap = (uint32_t)(device_cus() * wg);
-    uint32_t blocks = iters < cap ? iters : cap;
-    if (xf.epi == kEpiArgmax && blocks > kArgmaxSlots) blocks = kArgmaxSlots;   // one slot per workgroup
+    const uint32_t blocks = stream_blocks(W, NT, F::BS, bpr, rows, xf.pair, xf.epi == kEpiArgmax);
     launch_stream_d<F, W, 2, NT>(s, sg, x, bpr, blocks, xf);
 }
 
@@ -442,6 +472,45 @@ template <class F>
 static bool stream_ok(uint32_t n_cols) {
     static const bool v1 = getenv("YULE_QMV_V1") != nullptr;
     return !v1 && (n_cols / F::BS) * F::UPB <= 512 && n_cols <= kMaxStageCols;
+}
+
+// team width and workgroup size launch_fmt / launch_stream pick for a row of `units`
+static uint32_t stream_team(uint32_t units) {
+    return units <= 16 ? 16 : units <= 32 ? 32 : units <= 64 ? 64 : units <= 128 ? 128 : units <= 192 ? 192
+         : units <= 256 ? 256 : 512;
+}
+static uint32_t stream_threads(uint32_t W) {
+    static const int nt_narrow = env_int("YULE_QMV_THREADS", 256), nt_wide = env_int("YULE_QMV_THREADS_WIDE", 1024);
+    static const int nt_w64 = env_int("YULE_QMV_THREADS_W64", 512);
+    if (W == 192) return 768;
+    const int nt = W >= 512 ? 1024 : W >= 128 ? nt_wide : W == 64 ? nt_w64 : nt_narrow;
+    return nt >= 1024 ? 1024 : nt >= 512 ? 512 : 256;
+}
+
+template <class F>
+static bool group_plan(uint32_t n_rows, uint32_t n_cols, bool pair, uint32_t *gb, uint32_t *groups, uint32_t *rpg) {
+    if (!stream_ok<F>(n_cols) || n_cols % F::BS) return false;
+    const uint32_t bpr = n_cols / F::BS, W = stream_team(bpr * F::UPB), NT = stream_threads(W), RI = NT / W;
+    if (pair && W > 64) return false;
+    const uint32_t blocks = stream_blocks(W, NT, F::BS, bpr, n_rows, pair, false);
+    if (blocks % 8) return false;   // then group g would not map to XCD g % 8
+    *gb = RI * bpr * F::BB;
+    *groups = (n_rows + RI - 1) / RI;
+    *rpg = RI;
+    return true;
+}
+
+bool qmv_group_plan(uint32_t dtype, uint32_t n_rows, uint32_t n_cols, bool pair, uint32_t *gb, uint32_t *groups,
+                    uint32_t *rpg) {
+    switch (dtype) {
+    case YULE_DTYPE_Q4_K: return group_plan<Q4K>(n_rows, n_cols, pair, gb, groups, rpg);
+    case YULE_DTYPE_Q5_K: return group_plan<Q5K>(n_rows, n_cols, pair, gb, groups, rpg);
+    case YULE_DTYPE_Q6_K: return group_plan<Q6K>(n_rows, n_cols, pair, gb, groups, rpg);
+    case YULE_DTYPE_Q8_K: return group_plan<Q8K>(n_rows, n_cols, pair, gb, groups, rpg);
+    case YULE_DTYPE_Q8_0: return group_plan<Q80>(n_rows, n_cols, pair, gb, groups, rpg);
+    case YULE_DTYPE_Q4_0: return group_plan<Q40>(n_rows, n_cols, pair, gb, groups, rpg);
+    default: return false;
+    }
 }
 
 template <class F>

@@ -68,6 +68,10 @@ struct yule_hip_runner {
     // over runs of decode steps of one variant (one graph launch per
     // multi_steps tokens: each launch of a graph costs ~7 us of idle GPU)
     uint32_t multi_steps = 8;
+    // experimental: launches carry extra workgroups that read the next
+    // launch's weights into its XCDs' L2 (bit 1: O -> gate/up, 2: gate/up ->
+    // down, 4: Q/K/V -> O)
+    uint32_t pf_mask = 4, pf_wgs = 256, pf_delay = 0;
     hipGraph_t graph_n[2] = {nullptr, nullptr};
     hipGraphExec_t exec_n[2] = {nullptr, nullptr};
     uint32_t pos = 0;  // host mirror of ctl[0]
@@ -162,6 +166,24 @@ int enqueue_head(yule_hip_runner *r) {
 // (SwiGLU moves into the down launch's staging when gate/up cannot pair)
 // and at the end [rms_norm + lm_head + argmax] [advance]; otherwise the
 // same operations as separate kernels.
+// Point xf's prefetch workgroups at the weights of a following launch: one
+// matrix of n_rows x n_cols, or a gate/up pair (w1 = up) of that shape;
+// nothing when that launch's grid gives no group-to-XCD mapping.
+static void plan_prefetch(const yule_hip_runner *r, QmvXf &xf, uint32_t dtype, const uint8_t *w0, const uint8_t *w1,
+                          uint32_t n_rows, uint32_t n_cols) {
+    uint32_t gb = 0, groups = 0, rpg = 0, bs = 0, bb = 0;
+    if (!r->pf_wgs || !qmv_group_plan(dtype, n_rows, n_cols, w1 != nullptr, &gb, &groups, &rpg) ||
+        !quant_geometry(dtype, &bs, &bb))
+        return;
+    xf.pf_w[0] = w0;
+    xf.pf_w[1] = w1;
+    xf.pf_wgs = r->pf_wgs;
+    xf.pf_gbytes = gb;
+    xf.pf_groups = groups;
+    xf.pf_delay = r->pf_delay;
+    xf.pf_total = (size_t)n_rows * (n_cols / bs) * bb;
+}
+
 int enqueue_step(yule_hip_runner *r, bool split) {
     hipStream_t s = r->be->stream;
     const uint32_t qd = r->n_heads * r->hd, kvd = r->n_kv * r->hd;
@@ -193,6 +215,7 @@ int enqueue_step(yule_hip_runner *r, bool split) {
             norm.vc = L.vc;
             norm.hd = r->hd;
         }
+        if ((r->pf_mask & 4) && fuse) plan_prefetch(r, norm, L.to, L.wo, nullptr, r->dim, qd);
         if (L.tq == L.tk && L.tk == L.tv) {
             const QmvSeg segs[3] = {{L.wq, r->q, qd}, {L.wk, r->k, kvd}, {L.wv, r->v, kvd}};
             if ((rc = launch_qmv_fused(s, L.tq, segs, 3, xin, r->dim, norm))) return rc;
@@ -216,6 +239,8 @@ int enqueue_step(yule_hip_runner *r, bool split) {
         if (fuse) {
             QmvXf add;
             add.epi = kEpiAdd;
+            if ((r->pf_mask & 1) && L.tg == L.tu && qmv_pairable(L.tg, r->dim))
+                plan_prefetch(r, add, L.tg, L.wg, L.wu, r->ff, r->dim);
             const QmvSeg so{L.wo, r->hidden, r->dim};
             if ((rc = launch_qmv_fused(s, L.to, &so, 1, r->attn, qd, add))) return rc;
         } else {
@@ -234,6 +259,7 @@ int enqueue_step(yule_hip_runner *r, bool split) {
         const bool pair = fuse && L.tg == L.tu && qmv_pairable(L.tg, r->dim);
         if (pair) {   // gate/up + SwiGLU in one launch; act lands in r->gate
             norm.pair = true;
+            if (r->pf_mask & 2) plan_prefetch(r, norm, L.td, L.wd, nullptr, r->dim, r->ff);
             const QmvSeg segs[2] = {{L.wg, r->gate, r->ff}, {L.wu, r->up, r->ff}};
             if ((rc = launch_qmv_fused(s, L.tg, segs, 2, xin, r->dim, norm))) return rc;
         } else if (L.tg == L.tu) {
@@ -526,6 +552,9 @@ int yule_hip_runner_create(yule_hip_backend *be, const yule_model_desc *d, yule_
     r->fused = getenv("YULE_RUNNER_UNFUSED") == nullptr && qmv_fusable(r->out_t, r->dim);
     // decode steps per replayed graph in generate_greedy (1: one per step)
     if (const char *e = getenv("YULE_RUNNER_GRAPH_STEPS")) r->multi_steps = std::max(1, atoi(e));
+    if (const char *e = getenv("YULE_RUNNER_PREFETCH")) r->pf_mask = (uint32_t)atoi(e);
+    if (const char *e = getenv("YULE_RUNNER_PREFETCH_WGS")) r->pf_wgs = (uint32_t)atoi(e) & ~7u;
+    if (const char *e = getenv("YULE_RUNNER_PREFETCH_DELAY")) r->pf_delay = (uint32_t)atoi(e);
     for (const auto &L : r->layers)
         r->fused = r->fused && qmv_fusable(L.tq, r->dim) && qmv_fusable(L.tk, r->dim) && qmv_fusable(L.tv, r->dim) &&
                    qmv_fusable(L.to, qd) && qmv_fusable(L.tg, r->dim) && qmv_fusable(L.tu, r->dim) &&
