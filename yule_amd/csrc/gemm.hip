@@ -278,7 +278,7 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
     // the first 14 dwords (what the first loads need) arrive preloaded in
     // SGPRs: no kernel-argument load delays them
     const _Float16 *__restrict__ xh, const uint8_t *w0, const uint8_t *w1, const uint8_t *w2, uint32_t s1,
-    uint32_t s2, uint32_t M, uint32_t N, uint32_t K, uint32_t tail, const _Float16 *__restrict__ xl,
+    uint32_t s2, uint32_t M, uint32_t N, uint32_t K, uint32_t tail_ks, const _Float16 *__restrict__ xl,
     float *__restrict__ y, const _Float16 *__restrict__ xs_hi, const _Float16 *__restrict__ xs_lo,
     const float *__restrict__ rowscale, uint32_t xcd_remap, uint32_t accumulate) {
     constexpr bool Q5 = DT == YULE_DTYPE_Q5_K;
@@ -323,10 +323,13 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
     // last round of resident workgroups then runs half as long.  Both
     // halves add into y, which the host zeroed: 0 + a + b is exact in
     // either order.
+    // tail_ks = tail | K splits << 16 (the grid size comes from arguments,
+    // not from the dispatch packet, whose load would delay the first loads)
+    const uint32_t tail = tail_ks & 0xffffu, ks = tail_ks >> 16;
     const uint32_t whole = tiles - tail;
     const bool halves = tail && blockIdx.x >= whole;
-    const uint32_t splits = tail ? (halves ? 2u : 1u) : gridDim.x / tiles;
-    const uint32_t span = tail ? whole : gridDim.x;
+    const uint32_t splits = tail ? (halves ? 2u : 1u) : ks;
+    const uint32_t span = tail ? whole : ks * tiles;
     uint32_t t = blockIdx.x, zs;
     if (halves) {
         zs = (t - whole) & 1u;
@@ -921,7 +924,7 @@ void launch_gemm_bn(hipStream_t s, const GemmPass &p) {
     if (p.tail)
         hipLaunchKernelGGL(gemm_zero_tiles_kernel, dim3(p.tail * (bm / 8)), dim3(256), 0, s, p.y, p.m, p.n,
                            tiles - p.tail, nt, bm, (uint32_t)BN);
-#define YULE_GEMM_ARGS p.xh, p.w.w[0], p.w.w[1], p.w.w[2], p.w.s1, p.w.s2, p.m, p.n, p.k, p.tail, p.xl, p.y, p.xs_hi, \
+#define YULE_GEMM_ARGS p.xh, p.w.w[0], p.w.w[1], p.w.w[2], p.w.s1, p.w.s2, p.m, p.n, p.k, p.tail | p.ks << 16, p.xl, p.y, p.xs_hi, \
         p.xs_lo, p.rowscale, remap, p.accumulate
     if (p.xl) {   // f32 X: the hi and lo sweeps
         if (bm == 64)

@@ -279,9 +279,9 @@ using namespace yule;
 // writes one XOR of every word each workgroup read to part[blockIdx.x], so
 // that the reads are observable and the host can check them.
 __global__ __launch_bounds__(256) void read_probe_kernel(const uint4 *__restrict__ src, uint64_t n16,
-                                                         uint32_t *__restrict__ part) {
+                                                         uint32_t *__restrict__ part, uint32_t grid) {
     __shared__ uint32_t red[4];
-    const uint64_t T = (uint64_t)gridDim.x * 256;
+    const uint64_t T = (uint64_t)grid * 256;   // grid size as an argument: no dispatch-packet load
     uint32_t acc = 0;
     for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += T) {
         const uint4 v = src[i];
@@ -472,7 +472,7 @@ int yule_hip_read_probe(yule_hip_backend *be, yule_buffer src, uint64_t bytes, y
         (rc = get_buffer(be, partials, (size_t)n_partials * 4, &pp, "read_probe (partials)")))
         return rc;
     hipLaunchKernelGGL(read_probe_kernel, dim3(n_partials), dim3(256), 0, be->stream, (const uint4 *)ps, bytes / 16,
-                       (uint32_t *)pp);
+                       (uint32_t *)pp, n_partials);
     return check_launch("read_probe");
 }
 
