@@ -238,7 +238,7 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const uint8_t *vb0, cons
         // which need it, wait for it alone and not for the x and weight loads
         // behind it (loads complete in issue order)
         uint32_t pos_early = 0;
-        if (W < 64 && rope_ctl) pos_early = rope_ctl[0];
+        if (TWO && W < 64 && rope_ctl) pos_early = rope_ctl[0];
         const uint32_t n = bpr * F::BS, n4 = n / 4;
         const float4 *x4 = reinterpret_cast<const float4 *>(x), *a4 = reinterpret_cast<const float4 *>(xf.a);
         float4 xv[kXPer], av[kXPer];
@@ -253,7 +253,10 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const uint8_t *vb0, cons
 #pragma unroll
         for (int j = 0; j < D - 1; j++)
             if (r0 + j * stride < n_rows) buf[j] = fetch(r0 + j * stride);
-        if (W < 64) {
+        // nothing below (the RoPE block's argument loads and their wait)
+        // is scheduled ahead of the first rows' weight loads
+        __builtin_amdgcn_sched_barrier(0);
+        if (TWO && W < 64) {   // kEpiRope comes with an input transform (checked on the host)
             // RoPE epilogue: lane l keeps cos / sin of pair l of the position's
             // table row (unconditional loads from a valid address either way)
             const bool rope = xf.epi == kEpiRope;
@@ -310,7 +313,7 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const uint8_t *vb0, cons
     __shared__ float ring[16][NWV];
     auto finish = [&](float acc, uint32_t rbase, uint32_t it, bool last) {
         acc = team_sum<(W < 64 ? W : 64)>(active ? acc : 0.f);
-        if (W < 64 && xf.epi == kEpiRope) {
+        if (TWO && W < 64 && xf.epi == kEpiRope) {
             // rows 2i and 2i + 1 of a head are teams 2j and 2j + 1 of one wave
             // (row bases are even): the pair meets across lane W
             const float other = __shfl_xor(acc, W, 64);
@@ -598,8 +601,9 @@ int launch_qmv_fused(hipStream_t s, uint32_t dtype, const QmvSeg *segs, uint32_t
     if (xf.epi == kEpiArgmax && n_seg != 1)
         return set_error(YULE_ERR_INVALID, "quantized_matmul: argmax epilogue needs a single matrix");
     if (xf.epi == kEpiRope && (n_seg != 3 || !qmv_rope_ok(dtype, n_cols, xf.hd) || segs[1].n_rows != segs[2].n_rows ||
-                               segs[0].n_rows % xf.hd || segs[1].n_rows % xf.hd || xf.pair))
-        return set_error(YULE_ERR_INVALID, "quantized_matmul: RoPE epilogue needs q, k, v of whole heads on narrow teams");
+                               segs[0].n_rows % xf.hd || segs[1].n_rows % xf.hd || xf.pair || xf.mode == kXfNone))
+        return set_error(YULE_ERR_INVALID,
+                         "quantized_matmul: RoPE epilogue needs q, k, v of whole heads on narrow teams and an input transform");
     if (xf.pair && (n_seg != 2 || segs[0].n_rows != segs[1].n_rows || !qmv_pairable(dtype, n_cols) ||
                     xf.mode == kXfNone))
         return set_error(YULE_ERR_INVALID, "quantized_matmul: paired gate/up needs two equal single-wave matrices and an input transform");
