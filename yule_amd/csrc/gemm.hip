@@ -280,7 +280,7 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
     const _Float16 *__restrict__ xh, const uint8_t *w0, const uint8_t *w1, const uint8_t *w2, uint32_t s1,
     uint32_t s2, uint32_t M, uint32_t N, uint32_t K, uint32_t tail_ks, const _Float16 *__restrict__ xl,
     float *__restrict__ y, const _Float16 *__restrict__ xs_hi, const _Float16 *__restrict__ xs_lo,
-    const float *__restrict__ rowscale, uint32_t xcd_remap, uint32_t accumulate) {
+    const float *__restrict__ rowscale, uint32_t accumulate) {
     constexpr bool Q5 = DT == YULE_DTYPE_Q5_K;
     constexpr bool Q4 = DT == YULE_DTYPE_Q4_K || Q5;   // Q5_K: Q4_K plus a fifth bit per weight from qh
     constexpr bool B32 = DT == YULE_DTYPE_Q8_0 || DT == YULE_DTYPE_Q4_0;   // 32-weight blocks, d per block
@@ -325,7 +325,8 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
     // either order.
     // tail_ks = tail | K splits << 16 (the grid size comes from arguments,
     // not from the dispatch packet, whose load would delay the first loads)
-    const uint32_t tail = tail_ks & 0xffffu, ks = tail_ks >> 16;
+    // bit 31: XCD-contiguous tile order (see below)
+    const uint32_t tail = tail_ks & 0xffffu, ks = (tail_ks >> 16) & 0x7fffu, xcd_remap = tail_ks >> 31;
     const uint32_t whole = tiles - tail;
     const bool halves = tail && blockIdx.x >= whole;
     const uint32_t splits = tail ? (halves ? 2u : 1u) : ks;
@@ -348,7 +349,9 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
     const uint32_t kb_hi = (uint32_t)((uint64_t)bpr * (zs + 1) / splits);
     const uint32_t S = 4 * (kb_hi - kb_lo);     // stages of this split (>= 4)
     const size_t row_bytes = B32 ? (size_t)(K / 32) * BB : (size_t)bpr * BB;
-    if (splits > 1 && !tail) y += (size_t)zs * M * N;
+    // this split's partial product (offset applied at the stores, so that
+    // the load of y is not waited for ahead of the first stage's loads)
+    const size_t y_off = splits > 1 && !tail ? (size_t)zs * M * N : 0;
 
     floatx4 acc[TM][4], tmp[TM][4];
 #pragma unroll
@@ -646,6 +649,9 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
     GemmRegs<DT, XCH> R0, R1;
     load_stage(0, R0, std::integral_constant<int, 0>{});
     load_stage(1, R1, std::integral_constant<int, 1>{});
+    // argument loads the epilogue needs (y, ...) and their waits stay behind
+    // the first two stages' loads
+    __builtin_amdgcn_sched_barrier(0);
     dequant_stage(0, R0, 0, std::integral_constant<int, 0>{});
     load_stage(2, R0, std::integral_constant<int, 2>{});   // S >= 4
     __syncthreads();
@@ -800,6 +806,7 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
     }
 
     // ---- store: lane holds rows 4*(lane/16)+e of column lane%16 of each tile
+    float *const ysplit = y + y_off;
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -809,6 +816,7 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
             for (int e = 0; e < 4; e++) {
                 const uint32_t m = m0 + wm * (BM / 2) + i * 16 + 4 * (lane >> 4) + e;
                 if (m < M && r < N) {
+                    float *const y = ysplit;
                     const float v = acc[i][j][e] * rs[i][e];   // the row's power of two back out: exact
                     if (halves) unsafeAtomicAdd(y + (size_t)m * N + r, v);
                     else if (accumulate && splits == 1) y[(size_t)m * N + r] += v;
@@ -924,8 +932,8 @@ void launch_gemm_bn(hipStream_t s, const GemmPass &p) {
     if (p.tail)
         hipLaunchKernelGGL(gemm_zero_tiles_kernel, dim3(p.tail * (bm / 8)), dim3(256), 0, s, p.y, p.m, p.n,
                            tiles - p.tail, nt, bm, (uint32_t)BN);
-#define YULE_GEMM_ARGS p.xh, p.w.w[0], p.w.w[1], p.w.w[2], p.w.s1, p.w.s2, p.m, p.n, p.k, p.tail | p.ks << 16, p.xl, p.y, p.xs_hi, \
-        p.xs_lo, p.rowscale, remap, p.accumulate
+#define YULE_GEMM_ARGS p.xh, p.w.w[0], p.w.w[1], p.w.w[2], p.w.s1, p.w.s2, p.m, p.n, p.k, p.tail | p.ks << 16 | remap << 31, p.xl, p.y, p.xs_hi, \
+        p.xs_lo, p.rowscale, p.accumulate
     if (p.xl) {   // f32 X: the hi and lo sweeps
         if (bm == 64)
             hipLaunchKernelGGL((gemm_kernel<DT, 64, BN, 2>), dim3(grid), dim3(2 * BN), 0, s, YULE_GEMM_ARGS);
