@@ -109,13 +109,57 @@ __device__ __forceinline__ void align_raw(const uint32_t *raw, uint32_t mis, uin
 // term's sub-block sums of x * s as f16 hi + lo; rowscale[m] = 1 / s.
 template <bool F32>
 // (inputs first: the leading 14 dwords arrive preloaded in SGPRs)
-__global__ __launch_bounds__(256) void gemm_xprep_kernel(const void *__restrict__ xin, const float *__restrict__ nw,
+__global__ __launch_bounds__(256) void gemm_xprep_kernel(const void *xin, const float *__restrict__ nw,
                                                          uint32_t K, float eps, uint32_t glu,
                                                          _Float16 *__restrict__ xh, _Float16 *__restrict__ xl,
                                                          _Float16 *__restrict__ hi, _Float16 *__restrict__ lo,
-                                                         float *__restrict__ rowscale) {
+                                                         float *__restrict__ rowscale, const float *__restrict__ part,
+                                                         uint32_t ks, uint32_t ny, uint32_t rows, uint32_t accumulate) {
     __shared__ float red[4], red2[4];
     const uint32_t m = blockIdx.x, tid = threadIdx.x, nch = K / 8;
+    if (part) {
+        // the previous product's split-K reduction of this row first (its
+        // partials part[z][rows][ny] summed z ascending into xin's row, plus
+        // the row itself with accumulate: the same operations, in the same
+        // order, as gemm_reduce_kernel), then the row is this product's X
+        // (xin is written here, so it carries no __restrict__)
+        float *yrow = const_cast<float *>(static_cast<const float *>(xin)) + (size_t)m * ny;
+        const size_t stride = (size_t)rows * ny;
+        const float *prow = part + (size_t)m * ny;
+        // float4 columns, four at a time per thread: every partial of them
+        // loaded before the sums (per element the same order as above)
+        const uint32_t n4 = ny / 4;
+        float4 *y4 = reinterpret_cast<float4 *>(yrow);
+        const float4 *p4 = reinterpret_cast<const float4 *>(prow);
+        const size_t st4 = stride / 4;
+        for (uint32_t i0 = tid; i0 < n4; i0 += 4 * 256) {
+            float4 sum[4], base[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const uint32_t i = i0 + 256 * u < n4 ? i0 + 256 * u : i0;
+                sum[u] = p4[i];
+                base[u] = accumulate ? y4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+            for (uint32_t z = 1; z < ks; z++) {
+                float4 v[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++) v[u] = p4[(size_t)z * st4 + (i0 + 256 * u < n4 ? i0 + 256 * u : i0)];
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    sum[u].x += v[u].x; sum[u].y += v[u].y; sum[u].z += v[u].z; sum[u].w += v[u].w;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                if (i0 + 256 * u >= n4) break;
+                float4 r = sum[u];
+                if (accumulate) { r.x = base[u].x + r.x; r.y = base[u].y + r.y; r.z = base[u].z + r.z; r.w = base[u].w + r.w; }
+                y4[i0 + 256 * u] = r;
+            }
+        }
+        __threadfence_block();
+        __syncthreads();
+    }
     auto load8 = [&](uint32_t c, float *v) {
         if constexpr (F32) {
             if (glu) {
@@ -1005,7 +1049,8 @@ static GemmW one_matrix(const uint8_t *w, uint32_t n_rows) { return GemmW{{w, w,
 // add into Y in either order)
 static int gemm_enqueue(hipStream_t s, const GemmW &w, const void *x, bool f32x, float *y, uint32_t m,
                         uint32_t n_rows, uint32_t n_cols, uint32_t dtype, const GemmWork &g, void *ws,
-                        bool accumulate = false, const float *norm_w = nullptr, float eps = 0.f, bool glu = false) {
+                        bool accumulate = false, const float *norm_w = nullptr, float eps = 0.f, bool glu = false,
+                        GemmRed *defer = nullptr, const GemmRed *pending = nullptr) {
     uint8_t *b = static_cast<uint8_t *>(ws);
     float *part = g.ks > 1 ? reinterpret_cast<float *>(b) : nullptr;
     _Float16 *xh = reinterpret_cast<_Float16 *>(b + g.part_bytes);
@@ -1013,17 +1058,23 @@ static int gemm_enqueue(hipStream_t s, const GemmW &w, const void *x, bool f32x,
     _Float16 *xs_hi = g.q4 ? xh + (f32x ? 2 : 1) * g.n_x : nullptr, *xs_lo = g.q4 ? xs_hi + g.n_sub : nullptr;
     float *rowscale = reinterpret_cast<float *>(
         (reinterpret_cast<uintptr_t>(xh + (f32x ? 2 : 1) * g.n_x + (g.q4 ? 2 * g.n_sub : 0)) + 255) & ~(uintptr_t)255);
+    const bool red = pending && pending->ks > 1;
+    if (red && (!f32x || pending->y != x || pending->m != m || pending->ny != (glu ? 2 : 1) * n_cols))
+        return set_error(YULE_ERR_INVALID, "quantized_gemm: pending reduction does not produce this X");
     if (f32x)
         hipLaunchKernelGGL(gemm_xprep_kernel<true>, dim3(m), dim3(256), 0, s, x, norm_w, n_cols, eps, glu ? 1u : 0u,
-                           xh, xl, xs_hi, xs_lo, rowscale);
+                           xh, xl, xs_hi, xs_lo, rowscale, red ? pending->part : nullptr, red ? pending->ks : 0u,
+                           red ? pending->ny : 0u, m, red && pending->accumulate ? 1u : 0u);
     else
         hipLaunchKernelGGL(gemm_xprep_kernel<false>, dim3(m), dim3(256), 0, s, x, norm_w, n_cols, eps, 0u, xh, xl,
-                           xs_hi, xs_lo, rowscale);
+                           xs_hi, xs_lo, rowscale, nullptr, 0u, 0u, m, 0u);
     int rc = check_launch("quantized_gemm: x pre-pass");
     if (rc) return rc;
     const GemmPass p{w, xh, xl, xs_hi, xs_lo, rowscale, g.ks > 1 ? part : y, m, n_rows, n_cols, g.ks, g.bn, g.bm,
                      accumulate ? 0u : g.tail, accumulate ? 1u : 0u};
     if ((rc = launch_gemm_dt(s, dtype, p))) return rc;
+    if (defer) *defer = GemmRed{part, y, g.ks > 1 ? g.ks : 0u, n_rows, m, accumulate};
+    if (g.ks > 1 && defer) return YULE_OK;   // summed by the next product's pre-pass
     if (g.ks > 1) {
         hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)((g.n_y + 255) / 256)), dim3(256), 0, s, part, y,
                            (uint64_t)g.n_y, g.ks, accumulate ? 1u : 0u);
@@ -1108,12 +1159,13 @@ size_t yule::gemm_f32_workspace_bytes(uint32_t m, uint32_t n_rows, uint32_t n_co
 
 int yule::launch_gemm_f32(hipStream_t s, const uint8_t *w, const float *x, float *y, uint32_t m, uint32_t n_rows,
                           uint32_t n_cols, uint32_t dtype, void *ws, bool accumulate, const float *norm_w, float eps,
-                          bool glu) {
+                          bool glu, GemmRed *defer, const GemmRed *pending) {
     if (!gemm_dtype_ok(dtype) || n_cols % 256) return set_error(YULE_ERR_UNSUPPORTED, "gemm: format or shape");
     if (glu && norm_w) return set_error(YULE_ERR_INVALID, "gemm: SwiGLU input and RMSNorm together");
+    if (defer) defer->ks = 0;
     if (!m || !n_rows) return YULE_OK;
     return gemm_enqueue(s, one_matrix(w, n_rows), x, true, y, m, n_rows, n_cols, dtype,
-                        gemm_work(m, n_rows, n_cols, dtype, true), ws, accumulate, norm_w, eps, glu);
+                        gemm_work(m, n_rows, n_cols, dtype, true), ws, accumulate, norm_w, eps, glu, defer, pending);
 }
 
 // Several matrices of one format and width that share X, as one product
@@ -1136,15 +1188,16 @@ size_t yule::gemm_f32_multi_workspace_bytes(uint32_t m, const uint32_t *rows, ui
 
 int yule::launch_gemm_f32_multi(hipStream_t s, const uint8_t *const *w, const uint32_t *rows, uint32_t n_mat,
                                 const float *x, float *y, uint32_t m, uint32_t n_cols, uint32_t dtype, void *ws,
-                                const float *norm_w, float eps) {
+                                const float *norm_w, float eps, GemmRed *defer, const GemmRed *pending) {
     if (!gemm_multi_ok(dtype, n_cols, rows, n_mat)) return set_error(YULE_ERR_UNSUPPORTED, "gemm: format or shape");
+    if (defer) defer->ks = 0;
     if (!m) return YULE_OK;
     GemmW g{{w[0], n_mat > 1 ? w[1] : w[0], n_mat > 2 ? w[2] : w[0]}, 0, 0};
     const uint32_t total = rows[0] + (n_mat > 1 ? rows[1] : 0) + (n_mat > 2 ? rows[2] : 0);
     g.s1 = n_mat > 1 ? rows[0] : total;
     g.s2 = n_mat > 2 ? rows[0] + rows[1] : total;
     return gemm_enqueue(s, g, x, true, y, m, total, n_cols, dtype, gemm_work(m, total, n_cols, dtype, true), ws,
-                        false, norm_w, eps);
+                        false, norm_w, eps, false, defer, pending);
 }
 
 extern "C" int yule_hip_quantized_gemm(yule_hip_backend *be, yule_buffer weights, yule_buffer x_bf16, yule_buffer y,

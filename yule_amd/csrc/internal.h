@@ -146,6 +146,17 @@ int launch_attn_chunks(hipStream_t stream, const float *q, const float *kc, cons
                        float *out, void *scratch, uint32_t n_heads, uint32_t n_kv, uint32_t hd, uint32_t max_rows,
                        uint32_t seq_host);
 // f32-X prefill GEMM into a caller-owned workspace (gemm.hip)
+// A split-K reduction left for the next product's X pre-pass (defer): the
+// partials part[ks][m][ny] of y, summed into y (accumulate: added to it) by
+// the pre-pass of the product whose X is y (pending), row by row before it
+// reads the row.  ks = 0: nothing left.  The partials live in the first
+// product's workspace, so the second needs another.
+struct GemmRed {
+    const float *part;
+    float *y;
+    uint32_t ks, ny, m;
+    bool accumulate;
+};
 bool gemm_supports(uint32_t dtype, uint32_t n_cols);
 size_t gemm_f32_workspace_bytes(uint32_t m, uint32_t n_rows, uint32_t n_cols, uint32_t dtype);
 // up to three matrices of one format sharing X as one f32-X product into
@@ -155,14 +166,15 @@ size_t gemm_f32_multi_workspace_bytes(uint32_t m, const uint32_t *rows, uint32_t
                                       uint32_t dtype);
 int launch_gemm_f32_multi(hipStream_t stream, const uint8_t *const *w, const uint32_t *rows, uint32_t n_mat,
                           const float *x, float *y, uint32_t m, uint32_t n_cols, uint32_t dtype, void *ws,
-                          const float *norm_w = nullptr, float eps = 0.f);
+                          const float *norm_w = nullptr, float eps = 0.f, GemmRed *defer = nullptr,
+                          const GemmRed *pending = nullptr);
 // accumulate: Y += X W (the residual add of the output and down projections);
 // norm_w: X's rows RMS-normalised and scaled by norm_w (eps) on the way in;
 // glu: x holds [gate | up] rows (2 n_cols wide) and X = gate * sigmoid(gate)
 // * up, formed on the way in (the down projection after a gate|up product)
 int launch_gemm_f32(hipStream_t stream, const uint8_t *w, const float *x, float *y, uint32_t m, uint32_t n_rows,
                     uint32_t n_cols, uint32_t dtype, void *ws, bool accumulate = false, const float *norm_w = nullptr,
-                    float eps = 0.f, bool glu = false);
+                    float eps = 0.f, bool glu = false, GemmRed *defer = nullptr, const GemmRed *pending = nullptr);
 // batched prompt pass (prefill.hip)
 int launch_embed_rows_batch(hipStream_t stream, uint32_t dtype, const uint8_t *table, const uint32_t *tokens,
                             uint32_t vocab, float *out, uint32_t dim, uint32_t n);

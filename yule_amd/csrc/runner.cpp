@@ -373,7 +373,10 @@ int ensure_batch(yule_hip_runner *r, uint32_t n) {
         for (auto &b : bufs)
             if ((rc = dev_alloc(r, (size_t)r->max_seq * b.n * 4, reinterpret_cast<void **>(b.p)))) return rc;
     }
-    const size_t need = batch_workspace(r, n);
+    // two workspaces: a product whose split-K reduction is left to the next
+    // product's pre-pass keeps its partials in one while the next runs in
+    // the other
+    const size_t need = 2 * ((batch_workspace(r, n) + 255) & ~(size_t)255);
     if (need > r->bws_size) {
         if (r->bws) {
             if ((rc = hip_error(hipStreamSynchronize(r->be->stream), "runner: synchronize"))) return rc;
@@ -402,31 +405,45 @@ int prefill_rows(yule_hip_runner *r, uint32_t pos0, uint32_t n, uint32_t prompt_
     if ((rc = ensure_batch(r, n))) return rc;
     // the control block only feeds the head and advance at the end
     if ((rc = set_ctl(r, pos0 + n - 1, 0, prompt_len))) return rc;
-    void *ws = r->bws;
+    // products alternate between the two workspaces; the O, gate/up and down
+    // products leave their split-K reduction to the next product's pre-pass
+    // (red), which reads their X right after (except the last down: the head
+    // reads its rows)
+    void *wsv[2] = {r->bws, static_cast<uint8_t *>(r->bws) + r->bws_size / 2};
+    uint32_t wi = 0;
+    auto next_ws = [&]() { return wsv[wi ^= 1]; };
+    GemmRed red{}, none{};
     if ((rc = launch_embed_rows_batch(s, r->embd_t, r->embd, r->prompt + pos0, r->vocab, r->bx, r->dim, n))) return rc;
     const uint32_t qkv_rows[3] = {qd, kvd, kvd}, gu_rows[2] = {r->ff, r->ff};
-    for (const auto &L : r->layers) {
+    for (size_t li = 0; li < r->layers.size(); li++) {
+        const auto &L = r->layers[li];
+        const bool last = li + 1 == r->layers.size();
         // q, k, v rows: one [q | k | v] product when the three share a format
         const float *q = r->bq, *k = r->bk, *v = r->bv;
         uint32_t ldq = qd, ldkv = kvd;
         if (qkv_one(r, L)) {
             const uint8_t *w[3] = {L.wq, L.wk, L.wv};
-            if ((rc = launch_gemm_f32_multi(s, w, qkv_rows, 3, r->bx, r->bqkv, n, r->dim, L.tq, ws, L.attn_norm,
-                                            r->eps)))
+            if ((rc = launch_gemm_f32_multi(s, w, qkv_rows, 3, r->bx, r->bqkv, n, r->dim, L.tq, next_ws(), L.attn_norm,
+                                            r->eps, nullptr, &red)))
                 return rc;
             q = r->bqkv;
             k = r->bqkv + qd;
             v = r->bqkv + qd + kvd;
             ldq = ldkv = qd + 2 * kvd;
-        } else if ((rc = launch_gemm_f32(s, L.wq, r->bx, r->bq, n, qd, r->dim, L.tq, ws, false, L.attn_norm, r->eps)) ||
-                   (rc = launch_gemm_f32(s, L.wk, r->bx, r->bk, n, kvd, r->dim, L.tk, ws, false, L.attn_norm, r->eps)) ||
-                   (rc = launch_gemm_f32(s, L.wv, r->bx, r->bv, n, kvd, r->dim, L.tv, ws, false, L.attn_norm, r->eps))) {
+        } else if ((rc = launch_gemm_f32(s, L.wq, r->bx, r->bq, n, qd, r->dim, L.tq, next_ws(), false, L.attn_norm,
+                                         r->eps, false, nullptr, &red)) ||
+                   (rc = launch_gemm_f32(s, L.wk, r->bx, r->bk, n, kvd, r->dim, L.tk, next_ws(), false, L.attn_norm,
+                                         r->eps)) ||
+                   (rc = launch_gemm_f32(s, L.wv, r->bx, r->bv, n, kvd, r->dim, L.tv, next_ws(), false, L.attn_norm,
+                                         r->eps))) {
             return rc;
         }
+        red = none;
         if ((rc = launch_rope_rows(s, const_cast<float *>(q), k, v, L.kc, L.vc, r->cos_t, r->sin_t, pos0, n, qd, kvd,
                                    r->hd, ldq, ldkv)) ||
             (rc = launch_attn_prefill(s, q, L.kc, L.vc, r->ba, pos0, n, r->n_heads, r->n_kv, r->hd, ldq)) ||
-            (rc = launch_gemm_f32(s, L.wo, r->ba, r->bx, n, r->dim, qd, L.to, ws, true)))   // residual += O
+            (rc = launch_gemm_f32(s, L.wo, r->ba, r->bx, n, r->dim, qd, L.to, next_ws(), true, nullptr, 0.f, false,
+                                  &red)))   // residual += O
             return rc;
         // gate and up: one [gate | up] product when they share a format
         // (one [gate | up] product: SwiGLU is formed in the down product's X
@@ -434,16 +451,23 @@ int prefill_rows(yule_hip_runner *r, uint32_t pos0, uint32_t n, uint32_t prompt_
         const bool gu = gu_one(r, L);
         if (gu) {
             const uint8_t *w[2] = {L.wg, L.wu};
-            if ((rc = launch_gemm_f32_multi(s, w, gu_rows, 2, r->bx, r->bgu, n, r->dim, L.tg, ws, L.ffn_norm, r->eps)))
+            const GemmRed in = red;
+            if ((rc = launch_gemm_f32_multi(s, w, gu_rows, 2, r->bx, r->bgu, n, r->dim, L.tg, next_ws(), L.ffn_norm,
+                                            r->eps, &red, &in)))
                 return rc;
-        } else if ((rc = launch_gemm_f32(s, L.wg, r->bx, r->bg, n, r->ff, r->dim, L.tg, ws, false, L.ffn_norm, r->eps)) ||
-                   (rc = launch_gemm_f32(s, L.wu, r->bx, r->bu, n, r->ff, r->dim, L.tu, ws, false, L.ffn_norm, r->eps)) ||
-                   (rc = launch_eltwise(s, 3, r->bg, r->bu, r->bg, n * r->ff))) {
-            return rc;
+        } else {
+            if ((rc = launch_gemm_f32(s, L.wg, r->bx, r->bg, n, r->ff, r->dim, L.tg, next_ws(), false, L.ffn_norm, r->eps,
+                                      false, nullptr, &red)) ||
+                (rc = launch_gemm_f32(s, L.wu, r->bx, r->bu, n, r->ff, r->dim, L.tu, next_ws(), false, L.ffn_norm, r->eps)) ||
+                (rc = launch_eltwise(s, 3, r->bg, r->bu, r->bg, n * r->ff)))
+                return rc;
+            red = none;
         }
-        if ((rc = launch_gemm_f32(s, L.wd, gu ? r->bgu : r->bg, r->bx, n, r->dim, r->ff, L.td, ws, true, nullptr, 0.f,
-                                  gu)))   // residual += down
+        const GemmRed in = red;
+        if ((rc = launch_gemm_f32(s, L.wd, gu ? r->bgu : r->bg, r->bx, n, r->dim, r->ff, L.td, next_ws(), true, nullptr,
+                                  0.f, gu, last ? nullptr : &red, &in)))   // residual += down
             return rc;
+        if (last) red = none;
     }
     if ((rc = hip_error(hipMemcpyAsync(r->hidden, r->bx + (size_t)(n - 1) * r->dim, (size_t)r->dim * 4,
                                        hipMemcpyDeviceToDevice, s),
