@@ -187,6 +187,42 @@ def test_runner_attention_formats_and_head_sizes(hip, scheme, dim, hd):
     assert [int(t) for t in out] == want
 
 
+@pytest.mark.parametrize("mask,wgs", [("7", "64"), ("7", "256"), ("0", "256")])
+def test_runner_prefetch_workgroups(hip, monkeypatch, mask, wgs):
+    """Decode with prefetch workgroups on every pairing the runner offers (O
+    -> gate/up, gate/up -> down, Q/K/V -> O), none, and a small prefetch
+    grid: logits of 6 steps vs the oracle, then greedy tokens vs the
+    oracle.  TinyLlama widths (2048 / 5632) so that every consumer grid maps
+    row groups to XCDs and the prefetch is planned."""
+    from yule_amd.model import LlamaConfig
+    monkeypatch.setenv("YULE_RUNNER_PREFETCH", mask)
+    monkeypatch.setenv("YULE_RUNNER_PREFETCH_WGS", wgs)
+    cfg = LlamaConfig(n_layers=2, dim=2048, n_heads=32, n_kv_heads=4, ff_dim=5632, vocab=512, max_seq=64)
+    m = SyntheticModel.generate(cfg, seed=27, scheme="Q4_K")
+    say(f"[runner] prefetch mask {mask}, {wgs} workgroups")
+    run = HipRunner(hip, m)
+    ref = oracle.Runner(m, n_threads=4)
+    try:
+        for i, t in enumerate(synth.uniform_tokens(37, 6, cfg.vocab)):
+            got, want = run.decode_step(int(t)), ref.forward(int(t))
+            assert np.max(np.abs(got - want)) <= tolerance_bar(want), f"step {i}"
+    finally:
+        run.close()
+    prompt = synth.uniform_tokens(38, 5, cfg.vocab)
+    run = HipRunner(hip, m)
+    out, _ = run.generate_greedy(prompt, 20)
+    run.close()
+    ref = oracle.Runner(m, n_threads=4)
+    for t in prompt:
+        logits = ref.forward(int(t))
+    want = []
+    for i in range(21):
+        want.append(oracle.argmax(logits))
+        if i < 20:
+            logits = ref.forward(want[-1])
+    assert [int(t) for t in out] == want
+
+
 def test_runner_three_wave_team_rows(hip):
     """Rows of 176 units (Q8_0, 5632 columns) run on three-wave teams in
     every matvec of the step: RMSNorm staging into Q/K/V, gate and up
