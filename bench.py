@@ -46,6 +46,9 @@ LLAMA3_LAYER = [("attn_q", 4096, 4096), ("attn_k", 1024, 4096), ("attn_v", 1024,
                 ("ffn_down", 4096, 14336)]
 LLAMA3_LM_HEAD = ("output", 128256, 4096)
 # TinyLlama-1.1B projections
+# TinyLlama-1.1B layer projections (the runner's decode launches, configs[1]'s Q4_K shapes)
+TINY_LAYER = [("attn_q", 2048, 2048), ("attn_k", 256, 2048), ("attn_v", 256, 2048), ("attn_output", 2048, 2048),
+              ("ffn_gate", 5632, 2048), ("ffn_up", 5632, 2048), ("ffn_down", 2048, 5632)]
 TINY_SWEEP = [("q_o", 2048, 2048, DType.Q4_K), ("k_v", 256, 2048, DType.Q4_K), ("gate_up", 5632, 2048, DType.Q4_K),
               ("down", 2048, 5632, DType.Q4_K), ("lm_head", 32000, 2048, DType.Q6_K)]
 
@@ -85,7 +88,7 @@ class Layer:
         """One layer pass.  fused: the HIP runner's launches -- Q/K/V as one
         multi-matrix launch, O, gate/up as one, down; else seven calls."""
         c = s % self.copies
-        if not fused or [n for n, _, _ in self.shapes] != [n for n, _, _ in LLAMA3_LAYER]:
+        if not fused or [n for n, _, _ in self.shapes] != [n for n, _, _ in LLAMA3_LAYER]:   # names, not sizes
             return [(self.w[n][c], self.x[cols], self.y[n][c], r, cols, self.dt) for n, r, cols in self.shapes]
         sh = {n: (r, cols) for n, r, cols in self.shapes}
 
@@ -130,28 +133,53 @@ def matrix_rate(hip, layer, name, launches):
     return us, gbs
 
 
-def read_probe(hip, layer, name, launches, n_wg=2048):
-    """What one launch that only streams the same weight bytes achieves
-    (yule_hip_read_probe, grid-stride 16-byte loads, 2048 workgroups),
-    over the same rotating copies as the matrix it stands beside.  The XOR
-    checksum of the first launch is checked against the host bytes."""
+def read_probe(hip, layer, name, launches, n_wg=2048, pattern=None, loads=1):
+    """What one launch that only streams the same weight bytes achieves, over
+    the same rotating copies as the matrix it stands beside: yule_hip_read_probe
+    (grid-stride 16-byte loads) or, with `pattern`, yule_hip_read_probe_variant.
+    The XOR checksum of the first launch is checked against the host bytes;
+    the median of 5 timed passes is reported."""
     _, r, c = next(s for s in layer.shapes if s[0] == name)
     nbytes = matrix_bytes(layer.dt, r, c)
     part = hip.allocate(4 * n_wg)
-    hip.read_probe(layer.w[name][0], nbytes, part, n_wg)
+
+    def go(w):
+        if pattern is None:
+            hip.read_probe(w, nbytes, part, n_wg)
+        else:
+            hip.read_probe_variant(w, nbytes, part, n_wg, pattern, loads)
+    go(layer.w[name][0])
     got = int(np.bitwise_xor.reduce(hip.download(part, n_wg, np.uint32)))
     want = int(np.bitwise_xor.reduce(np.ascontiguousarray(layer.host[name]).view(np.uint32).ravel()))
     if got != want:
         raise RuntimeError(f"read probe checksum {got:#x} != host {want:#x}")
     for i in range(64):
-        hip.read_probe(layer.w[name][i % layer.copies], nbytes, part, n_wg)
-    hip.timer_start()
-    for i in range(launches):
-        hip.read_probe(layer.w[name][i % layer.copies], nbytes, part, n_wg)
-    us = hip.timer_stop() * 1e3 / launches
+        go(layer.w[name][i % layer.copies])
+    runs = []
+    for _ in range(5):
+        hip.timer_start()
+        for i in range(launches):
+            go(layer.w[name][i % layer.copies])
+        runs.append(hip.timer_stop() * 1e3 / launches)
+    us = float(np.median(runs))
     hip.free(part)
+    what = ("yule_hip_read_probe (grid-stride 16-byte words)" if pattern is None else
+            f"yule_hip_read_probe_variant pattern {pattern}, {loads} words per lane")
     return {"us": round(us, 3), "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1), "bytes": nbytes,
-            "launch": "yule_hip_read_probe, 2048 x 256 threads, back-to-back stream launches"}
+            "launch": f"{what}, {n_wg} x 256 threads, back-to-back stream launches, median of 5 passes"}
+
+
+def dominant_rate(hip, dom, launches=1000, passes=5):
+    """Average launch duration of the dominant matvec (Q4_K 14336x4096): HIP
+    events around `launches` back-to-back launches replayed from one graph,
+    cycling the layer's weight copies; median over `passes` timed passes after
+    one warm-up pass."""
+    _, r, c = dom.shapes[0]
+    ops = dom.ops_for_matrix("ffn_gate", launches)
+    hip.time_qmv_ops(ops[:64], 1, USE_GRAPH)
+    runs = sorted(1e3 * hip.time_qmv_ops(ops, 1, USE_GRAPH) / launches for _ in range(passes))
+    us = runs[len(runs) // 2]
+    return us, algo_bytes(dom.dt, r, c) / (us * 1e-6) / 1e9, runs
 
 
 def _time_qmv_layer(layer, threads, budget_s, max_passes):
@@ -201,7 +229,7 @@ def cpu_baseline(layer, budget_s=12.0, max_passes=2000):
             "port_value": round(port, 3), "host_cpu": host_cpu_record(threads)}
 
 
-def decode_e2e(hip, cpu: bool):
+def decode_e2e(hip, cpu: bool, cpu_steps: int = 256):
     """TinyLlama-shaped Q4_K_M greedy decode, 128-token
     prompt then 256 decode steps, tok/s = 1000 / mean decode-step ms
     (yule-validate/src/performance.rs:303-337)."""
@@ -233,15 +261,17 @@ def decode_e2e(hip, cpu: bool):
             oracle.set_q4k_dot(asm)
         try:
             # the GPU figure's workload: the 128-token prompt (untimed), then
-            # greedy decode steps from position 128 on, as many as fit ~12 s
+            # all 256 greedy decode steps, positions 128..383
             r = oracle.Runner(model, n_threads=threads)
             t0 = time.perf_counter()
             for t in prompt:
                 logits = r.forward(int(t))
             pre_s = time.perf_counter() - t0
             n, t0 = 0, time.perf_counter()
-            while n < 4 or (n < 256 and time.perf_counter() - t0 < 12.0):
-                logits = r.forward(oracle.argmax(logits))
+            cpu_toks = [oracle.argmax(logits)]
+            while n < cpu_steps:
+                logits = r.forward(cpu_toks[-1])
+                cpu_toks.append(oracle.argmax(logits))
                 n += 1
             cms = 1e3 * (time.perf_counter() - t0) / n
         finally:
@@ -255,6 +285,7 @@ def decode_e2e(hip, cpu: bool):
                                        f"greedy decode steps at positions 128..{127 + n} (the GPU run decodes "
                                        f"128..383), through the oracle's restatement of Yule's CPU "
                                        f"TransformerRunner with {what}",
+                             "tokens_match_gpu": [int(t) for t in cpu_toks] == [int(t) for t in toks[:n + 1]],
                              "host_cpu": host_cpu_record(threads)}
         res["decode_speedup_vs_cpu"] = round(cms / ms, 1)
     return res
@@ -360,17 +391,28 @@ def traffic_from_profiles():
     return None
 
 
+def profile_avg_us():
+    """Average duration of the dominant kernel in the committed rocprofv3
+    kernel-trace summary of `bench.py --profile-dominant` (None if absent)."""
+    p = ROOT / "profiles" / "qmv_q4k_14336x4096_traffic.json"
+    try:
+        return json.loads(p.read_text()).get("trace_avg_us")
+    except Exception:
+        return None
+
+
 def profile_dominant(hip, n, copies):
-    """Dominant-kernel-only run for hardware-counter collection: N launches of
-    the Q4_K 14336x4096 matvec (kernel launches, no graph) cycling `copies`
-    weight copies, then one 64 MiB buffer copy whose counters calibrate the
-    bytes-per-KiB scale of FETCH_SIZE / WRITE_SIZE."""
+    """Dominant-kernel-only run for rocprofv3 (kernel trace, or --pmc counters):
+    the bench's own roofline measurement of the Q4_K 14336x4096 matvec (64
+    warm-up launches, then 5 passes of N launches replayed from a graph,
+    cycling the weight copies), then one 64 MiB buffer copy whose counters
+    calibrate the bytes-per-KiB scale of FETCH_SIZE / WRITE_SIZE."""
     L = Layer(hip, DType.Q4_K, [("ffn_gate", 14336, 4096)], max(copies, DOM_COPIES), seed=11)
-    ms = hip.time_qmv_ops(L.ops_for_matrix("ffn_gate", n), 1, use_graph=False)
+    us, _, runs = dominant_rate(hip, L, n)    # exactly the bench's roofline measurement
     src, dst = hip.allocate(64 << 20), hip.allocate(64 << 20)
     hip.copy_buffer(src, dst, 64 << 20)
     hip.synchronize()
-    print(json.dumps({"launches": n, "us_per_launch": round(1e3 * ms / n, 3),
+    print(json.dumps({"launches": n, "us_per_launch": round(us, 3), "passes_us": [round(u, 3) for u in runs],
                       "algo_bytes_per_launch": algo_bytes(DType.Q4_K, 14336, 4096),
                       "calibration_copy_bytes": 64 << 20}), flush=True)
 
@@ -405,6 +447,45 @@ def probe_curve(hip, sizes_mb=(33, 128, 256, 558, 1024), n_wgs=(1024, 2048, 4096
             hip.free(b)
         out[f"{mb}MB"] = row
     print(json.dumps({"read_probe_curve": out, "launch": "yule_hip_read_probe, 256-thread workgroups, "
+                      "back-to-back stream launches over rotating buffers, HIP events"}), flush=True)
+
+
+def probe_variants(hip, sizes_mb=(33, 128), grids=(512, 1024, 2048, 4096)):
+    """Single-launch streaming-read rate by access pattern (yule_hip_read_probe_variant:
+    0 grid-stride words with 1/2/4/8 loads in flight per lane, 1 per-lane runs of
+    16-128 bytes, 2 one contiguous chunk per workgroup) and grid size, over rotating
+    buffers totalling >= 2 GiB; median of 5 timed passes.  Prints one JSON line."""
+    out = {}
+    for mb in sizes_mb:
+        nbytes = (mb * 1000 * 1000) // 4096 * 4096
+        copies = max(2, -(-(2 << 30) // nbytes))
+        bufs = [hip.allocate(nbytes) for _ in range(copies)]
+        launches = max(2 * copies, min(2000, int(4e9 // nbytes)))
+        best = None
+        for pattern in (0, 1, 2):
+            for loads in (1, 2, 4, 8):
+                for n_wg in grids:
+                    part = hip.allocate(4 * n_wg)
+                    for i in range(copies):
+                        hip.read_probe_variant(bufs[i], nbytes, part, n_wg, pattern, loads)
+                    rates = []
+                    for _ in range(5):
+                        hip.timer_start()
+                        for i in range(launches):
+                            hip.read_probe_variant(bufs[i % copies], nbytes, part, n_wg, pattern, loads)
+                        us = hip.timer_stop() * 1e3 / launches
+                        rates.append(nbytes / (us * 1e-6) / 1e9)
+                    hip.free(part)
+                    g = float(np.median(rates))
+                    key = f"{mb}MB p{pattern} u{loads} g{n_wg}"
+                    out[key] = {"us": round(nbytes / (g * 1e9) * 1e6, 3), "GB/s": round(g, 1)}
+                    log(f"read probe variant {key}: {out[key]['us']} us, {g:.1f} GB/s")
+                    if best is None or g > out[best]["GB/s"]:
+                        best = key
+        out[f"{mb}MB best"] = best
+        for b in bufs:
+            hip.free(b)
+    print(json.dumps({"read_probe_variants": out, "launch": "yule_hip_read_probe_variant, 256-thread workgroups, "
                       "back-to-back stream launches over rotating buffers, HIP events"}), flush=True)
 
 
@@ -463,6 +544,8 @@ def main():
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--copies", type=int, default=8)
+    ap.add_argument("--repeats", type=int, default=7,
+                    help="timed K-step runs of the headline; the median is reported")
     ap.add_argument("--quick", action="store_true", help="primary metric and roofline only")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true",
@@ -476,6 +559,8 @@ def main():
                     help="tokens M of the --profile-gemm calls (default 2048)")
     ap.add_argument("--probe-curve", action="store_true",
                     help="only measure the single-launch streaming-read rate against launch size (JSON line)")
+    ap.add_argument("--probe-variants", action="store_true",
+                    help="only measure the single-launch read rate by access pattern and grid (JSON line)")
     ap.add_argument("--profile-decode", type=int, default=0, metavar="N",
                     help="only run N TinyLlama decode steps with kernels launched one by one (for rocprofv3)")
     ap.add_argument("--profile-prefill", type=int, default=0, metavar="N",
@@ -497,6 +582,9 @@ def main():
     if args.probe_curve:
         probe_curve(hip)
         return
+    if args.probe_variants:
+        probe_variants(hip)
+        return
     if args.profile_gemm:
         profile_gemm(hip, args.profile_gemm, args.gemm_m)
         return
@@ -511,12 +599,16 @@ def main():
     log("generating Llama-3-8B Q4_K layer")
     q4k = Layer(hip, DType.Q4_K, LLAMA3_LAYER, args.copies, seed=11)
 
-    # warm-up steps, then exactly K timed steps
+    # warm-up steps, then exactly K timed steps, repeated: the median timing
+    # is the headline, the others its spread
     time_steps(hip, q4k, args.warmup)
-    ms = time_steps(hip, q4k, args.steps)
+    reps = sorted(time_steps(hip, q4k, args.steps) for _ in range(max(1, args.repeats)))
+    ms = reps[len(reps) // 2]
     ms_per_step = ms / args.steps
     value = q4k.step_bytes * args.steps / (ms * 1e-3) / 1e9
-    log(f"Q4_K layer: {ms_per_step * 1e3:.2f} us/step, {value:.1f} GB/s ({100 * value / HBM_PEAK_GBS:.1f}% of peak)")
+    rep_values = [round(q4k.step_bytes * args.steps / (m * 1e-3) / 1e9, 1) for m in reps]
+    log(f"Q4_K layer: {ms_per_step * 1e3:.2f} us/step, {value:.1f} GB/s ({100 * value / HBM_PEAK_GBS:.1f}% of peak); "
+        f"repeats {rep_values}")
     ms7 = time_steps(hip, q4k, args.steps, fused=False)
     value7 = q4k.step_bytes * args.steps / (ms7 * 1e-3) / 1e9
     log(f"Q4_K layer as 7 separate calls: {value7:.1f} GB/s")
@@ -526,19 +618,23 @@ def main():
     # cache, so no launch finds its weights cached)
     n_dom = 1000
     dom = Layer(hip, DType.Q4_K, [("ffn_gate", 14336, 4096)], DOM_COPIES, seed=11)
-    us, gbs = matrix_rate(hip, dom, "ffn_gate", n_dom)
+    us, gbs, dom_runs = dominant_rate(hip, dom, n_dom)
     dom_bytes = algo_bytes(DType.Q4_K, 14336, 4096)
     roofline = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(),
                 "kernel": f"{dominant_kernel_name()} 14336x4096", "avg_launch_us": round(us, 3),
-                "algo_bytes_per_launch": dom_bytes}
+                "avg_launch_us_passes": [round(u, 3) for u in dom_runs],
+                "algo_bytes_per_launch": dom_bytes, "profile_avg_us": profile_avg_us()}
     log(f"dominant kernel Q4_K 14336x4096: {us:.2f} us/launch, {gbs:.1f} GB/s")
     roofline["read_probe"] = read_probe(hip, dom, "ffn_gate", n_dom)
+    # the fastest single-launch read pattern of the variant sweep (bench.py --probe-variants)
+    roofline["read_probe_best"] = read_probe(hip, dom, "ffn_gate", n_dom, n_wg=1024, pattern=1, loads=2)
     roofline["weight_copies"] = DOM_COPIES
     dom.free()
-    roofline["frac_of_read_probe"] = round(gbs / roofline["read_probe"]["GB/s"], 4)
-    log(f"read probe over the same weight copies: {roofline['read_probe']['us']:.2f} us/launch, "
-        f"{roofline['read_probe']['GB/s']:.1f} GB/s")
+    best = max(roofline["read_probe"]["GB/s"], roofline["read_probe_best"]["GB/s"])
+    roofline["frac_of_read_probe"] = round(gbs / best, 4)
+    log(f"read probe over the same weight copies: {roofline['read_probe']['us']:.2f} us/launch "
+        f"(best variant {roofline['read_probe_best']['us']:.2f} us), {best:.1f} GB/s")
 
     # fixed cost of the step's kernel boundaries: the same number of empty
     # kernels per step, replayed from one graph like the timed steps
@@ -546,7 +642,9 @@ def main():
     hip.time_empty_launches(n_launch * min(args.steps, 64), 1, use_graph=USE_GRAPH)        # warm-up
     empty_ms = hip.time_empty_launches(n_launch * args.steps, 1, use_graph=USE_GRAPH)   # one graph, as the steps
     launch_us = 1e3 * empty_ms / args.steps
-    extra = {"layer_as_7_calls_GB/s": round(value7, 1), "per_matrix_q4k": {},
+    extra = {"headline_repeats": {"n": len(reps), "GB/s": rep_values[::-1],
+                                  "spread_pct": round(100 * (rep_values[0] - rep_values[-1]) / value, 2)},
+             "layer_as_7_calls_GB/s": round(value7, 1), "per_matrix_q4k": {},
              "launch_overhead": {"empty_kernels_per_step": n_launch, "us_per_step": round(launch_us, 3),
                                  "value_without_it_GB/s": round(q4k.step_bytes / ((ms_per_step * 1e3 - launch_us) * 1e-6) / 1e9, 1)}}
     log(f"empty-kernel step ({n_launch} launches): {launch_us:.2f} us")
@@ -592,6 +690,20 @@ def main():
             sweep[f"{name} {r}x{c} {dt.name}"] = {"us": round(u, 2), "GB/s": round(g, 1)}
             L.free()
         extra["tinyllama_sweep"] = sweep
+        # configs[1] as the runner issues it: a TinyLlama layer's Q4_K
+        # projections as its four decode launches (Q/K/V multi, O, gate/up,
+        # down), back to back from one graph over 64 rotating layer copies
+        # (1.4 GB), and the lm_head launches back to back
+        L = Layer(hip, DType.Q4_K, TINY_LAYER, 64, seed=51)
+        n = max(256, args.steps)
+        time_steps(hip, L, 64)
+        m = time_steps(hip, L, n)
+        extra["tinyllama_layer_q4k"] = {"us_per_layer": round(1e3 * m / n, 2),
+                                        "GB/s": round(L.step_bytes * n / (m * 1e-3) / 1e9, 1),
+                                        "launches_per_layer": len(L.ops_for_step(0)), "layer_bytes": L.step_bytes}
+        log(f"TinyLlama Q4_K layer (runner launches): {1e3 * m / n:.2f} us, "
+            f"{extra['tinyllama_layer_q4k']['GB/s']} GB/s")
+        L.free()
 
     out = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,

@@ -366,6 +366,16 @@ int yule_hip_time_qmv_ops(yule_hip_backend *be, const yule_qmv_op *ops, uint32_t
 int yule_hip_read_probe(yule_hip_backend *be, yule_buffer src, uint64_t bytes, yule_buffer partials,
                         uint32_t n_partials);
 
+/* Variants of the read probe (same arguments, same partials), to map the
+ * single-launch read rate against the access pattern: pattern 0 =
+ * grid-stride 16-byte words with `loads` (1, 2, 4 or 8) independent loads in
+ * flight per lane; 1 = a run of `loads` consecutive 16-byte words per lane
+ * (16, 32, 64 or 128-byte runs), runs grid-strided; 2 = one contiguous chunk
+ * per workgroup, consecutive words across its lanes, `loads` in flight.
+ * No reference counterpart. */
+int yule_hip_read_probe_variant(yule_hip_backend *be, yule_buffer src, uint64_t bytes, yule_buffer partials,
+                                uint32_t n_partials, uint32_t pattern, uint32_t loads);
+
 /* Launch-overhead probe: n_kernels launches of an empty kernel (one
  * workgroup of 64 threads that returns at once), run `iters` times, captured
  * into one HIP graph when use_graph != 0; writes the elapsed milliseconds
@@ -380,6 +390,18 @@ int yule_hip_time_empty_launches(yule_hip_backend *be, uint32_t n_kernels, uint3
  * for it and writes the elapsed milliseconds. */
 int yule_hip_timer_start(yule_hip_backend *be);
 int yule_hip_timer_stop(yule_hip_backend *be, float *ms);
+
+/* Graph-capture harness (no reference counterpart): capture_begin starts a
+ * HIP stream capture of the backend stream (thread-local mode: only calls
+ * from this thread are captured, and they are recorded, not run);
+ * capture_end ends it and instantiates the graph (replacing any earlier
+ * one); capture_replay launches the instantiated graph on the backend
+ * stream.  Used to check that an entry point enqueues cleanly under
+ * capture (no allocation, no synchronization) and that replays give the
+ * eager result. */
+int yule_hip_capture_begin(yule_hip_backend *be);
+int yule_hip_capture_end(yule_hip_backend *be);
+int yule_hip_capture_replay(yule_hip_backend *be);
 
 #ifdef __cplusplus
 }

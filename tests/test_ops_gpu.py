@@ -239,6 +239,29 @@ def test_argmax_kats(hip):
     hip.free(out)
 
 
+@pytest.mark.parametrize("pattern", [0, 1, 2])
+@pytest.mark.parametrize("loads", [1, 2, 4, 8])
+def test_read_probe_variants_read_every_word_once(hip, pattern, loads):
+    """Each read-probe variant covers every word exactly once, at ragged
+    sizes and grids that leave lanes, runs and chunks partly empty."""
+    say(f"[ops] read_probe_variant pattern {pattern}, {loads} loads in flight")
+    for n_bytes, n_wg in ((16, 1), (16, 64), (4096, 3), (1_000_016, 2048), (33_030_144, 1024)):
+        data = np.random.default_rng(n_bytes + loads).integers(0, 2**32, n_bytes // 4, dtype=np.uint32)
+        src, part = hip.upload(data), hip.allocate(4 * n_wg)
+        hip.read_probe_variant(src, n_bytes, part, n_wg, pattern, loads)
+        got = np.bitwise_xor.reduce(hip.download(part, n_wg, np.uint32))
+        assert int(got) == int(np.bitwise_xor.reduce(data)), (n_bytes, n_wg)
+        hip.free(src)
+        hip.free(part)
+    src, part = hip.allocate(64), hip.allocate(4)
+    with pytest.raises(YuleGpuError):
+        hip.read_probe_variant(src, 64, part, 1, 3, loads)    # no such pattern
+    with pytest.raises(YuleGpuError):
+        hip.read_probe_variant(src, 64, part, 1, pattern, 3)  # loads not a power of two up to 8
+    hip.free(src)
+    hip.free(part)
+
+
 @pytest.mark.parametrize("n_bytes,n_wg", [(16, 1), (16, 64), (4096, 3), (1_000_016, 2048), (33_030_144, 2048)])
 def test_read_probe_reads_every_word_once(hip, n_bytes, n_wg):
     """The roofline probe: the XOR of its per-workgroup partials equals the

@@ -162,24 +162,30 @@ def test_qmv_rows_independent_and_linear(hip):
 
 # BASELINE configs[2] (Llama-3-8B: FFN and the 128256-row lm_head, in each
 # of the layer formats) and configs[1]'s Q6_K lm_head, at full size.
+# configs[2]'s attention projections (Q/O 4096x4096, K/V 1024x4096) in each
+# layer format, and configs[1]'s Q4_K TinyLlama projections as standalone
+# matvecs.
 FULL = [(dt, 14336, 4096) for dt in (DType.Q6_K, DType.Q8_0)] + \
        [(dt, 4096, 14336) for dt in (DType.Q4_K, DType.Q6_K, DType.Q8_0)] + \
-       [(dt, 128256, 4096) for dt in (DType.Q4_K, DType.Q6_K, DType.Q8_0)] + [(DType.Q6_K, 32000, 2048)]
+       [(dt, 128256, 4096) for dt in (DType.Q4_K, DType.Q6_K, DType.Q8_0)] + [(DType.Q6_K, 32000, 2048)] + \
+       [(dt, r, 4096) for dt in (DType.Q4_K, DType.Q6_K, DType.Q8_0) for r in (4096, 1024)] + \
+       [(DType.Q4_K, r, c) for r, c in ((2048, 2048), (256, 2048), (5632, 2048), (2048, 5632))]
 
 
 @pytest.mark.parametrize("dt,n_rows,n_cols", FULL, ids=lambda v: getattr(v, "name", str(v)))
 def test_qmv_config_shapes_full_size(hip, dt, n_rows, n_cols):
-    """The whole matrix on the GPU; 512 seeded rows (first and last included)
-    against the oracle's f64 dot of the same rows; and those rows run alone
-    give bit-identical outputs (each row depends only on its own weights)."""
+    """The whole matrix on the GPU; every row up to 4096 rows, else 512
+    seeded rows (first and last included), against the oracle's f64 dot of
+    the same rows; and those rows run alone give bit-identical outputs (each
+    row depends only on its own weights)."""
     say(f"[qmv] full size {dt.name} {n_rows}x{n_cols}")
     bs, bb = oracle.GEOM[int(dt)]
     row_bytes = n_cols // bs * bb
     w = synth.gen_quant(dt, 300 + int(dt), n_rows, n_cols)
     x = synth.gauss(301, n_cols)
     y = gpu_qmv(hip, dt, w, x, n_rows, n_cols)
-    rows = np.unique(np.concatenate([[0, n_rows - 1],
-                                     np.random.default_rng(n_rows).integers(0, n_rows, 510)]))
+    rows = np.arange(n_rows) if n_rows <= 4096 else np.unique(np.concatenate(
+        [[0, n_rows - 1], np.random.default_rng(n_rows).integers(0, n_rows, 510)]))
     sub = np.concatenate([w[r * row_bytes:(r + 1) * row_bytes] for r in rows])
     ref = oracle.qmv_f64(int(dt), sub, x, len(rows), n_cols)
     assert np.max(np.abs(y[rows] - ref)) <= tolerance_bar(ref)

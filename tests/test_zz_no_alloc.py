@@ -51,3 +51,36 @@ def test_noalloc_gemm_refuses_oversize(hip):
         hip.quantized_gemm_noalloc(hw, hx, hy, M, N, K, DType.Q4_K)
     for h in (hw, hx, hy):
         hip.free(h)
+
+
+def test_noalloc_gemm_under_graph_capture(hip):
+    """The allocation-free entry enqueues cleanly under HIP stream capture
+    (one single-split and one split-K shape in one graph); every replay,
+    with eager work and host synchronizations between replays, gives the
+    allocating entry's Y bit for bit."""
+    print("[noalloc] graph capture: Q4_K 128x2560x2048 and Q6_K 16x1024x1024", flush=True)
+    cases = []
+    for dt, M, N, K, seed in ((DType.Q4_K, 128, 2560, 2048, 141), (DType.Q6_K, 16, 1024, 1024, 143)):
+        w = synth.gen_quant(dt, seed, N, K)
+        xb = bf16_bits(synth.gauss(seed + 1, (M, K)))
+        hw, hx, hy, hz = hip.upload(w), hip.upload(xb), hip.allocate(4 * M * N), hip.allocate(4 * M * N)
+        hip.quantized_gemm(hw, hx, hz, M, N, K, dt)
+        cases.append((dt, M, N, K, hw, hx, hy, hip.download(hz, (M, N)), hz))
+    hip.synchronize()
+    hip.capture_begin()
+    try:
+        for dt, M, N, K, hw, hx, hy, _, _ in cases:
+            hip.quantized_gemm_noalloc(hw, hx, hy, M, N, K, dt)
+    finally:
+        hip.capture_end()
+    for rep in range(3):
+        for dt, M, N, K, hw, hx, hy, want, hz in cases:
+            hip.copy_to_device(np.full(M * N, np.nan, np.float32), hy)   # stale Y must not survive
+            hip.quantized_gemm(hw, hx, hz, M, N, K, dt)                  # eager work between replays
+        hip.capture_replay()
+        hip.synchronize()
+        for dt, M, N, K, hw, hx, hy, want, hz in cases:
+            assert np.array_equal(hip.download(hy, (M, N)), want), f"replay {rep}: {dt.name} M={M} differs"
+    for c in cases:
+        for h in (c[4], c[5], c[6], c[8]):
+            hip.free(h)

@@ -77,9 +77,14 @@ _SIGS: dict[str, tuple] = {
     "yule_hip_gguf_get_array_len": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(C.c_uint64)]),
     "yule_hip_runner_create_from_gguf": (C.c_int, [C.c_void_p, C.c_char_p, C.c_uint32, C.POINTER(C.c_void_p)]),
     "yule_hip_read_probe": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint32]),
+    "yule_hip_read_probe_variant": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint32,
+                                              C.c_uint32, C.c_uint32]),
     "yule_hip_timer_start": (C.c_int, [C.c_void_p]),
     "yule_hip_time_empty_launches": (C.c_int, [C.c_void_p, C.c_uint32, C.c_uint32, C.c_int, C.POINTER(C.c_float)]),
     "yule_hip_timer_stop": (C.c_int, [C.c_void_p, C.POINTER(C.c_float)]),
+    "yule_hip_capture_begin": (C.c_int, [C.c_void_p]),
+    "yule_hip_capture_end": (C.c_int, [C.c_void_p]),
+    "yule_hip_capture_replay": (C.c_int, [C.c_void_p]),
     "yule_hip_time_qmv_ops": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_int,
                                         C.POINTER(C.c_float)]),
 }
@@ -281,6 +286,12 @@ class HipBackend:
         partials[i] = XOR of the words workgroup i read."""
         self._check(self._lib.yule_hip_read_probe(self._be, _h(src), n_bytes, _h(partials), n_partials))
 
+    def read_probe_variant(self, src, n_bytes: int, partials, n_partials: int, pattern: int, loads: int) -> None:
+        """A read-probe variant (pattern 0 grid-stride, 1 per-lane runs, 2 per-workgroup
+        chunks; `loads` 16-byte words in flight per lane); same partials as read_probe."""
+        self._check(self._lib.yule_hip_read_probe_variant(self._be, _h(src), n_bytes, _h(partials), n_partials,
+                                                          pattern, loads))
+
     def argmax(self, inp, n: int, out) -> None:
         self._check(self._lib.yule_hip_argmax(self._be, _h(inp), n, _h(out)))
 
@@ -330,6 +341,18 @@ class HipBackend:
         ms = C.c_float()
         self._check(self._lib.yule_hip_timer_stop(self._be, C.byref(ms)))
         return ms.value
+
+    def capture_begin(self) -> None:
+        """Start capturing this thread's calls on the backend stream into a HIP graph."""
+        self._check(self._lib.yule_hip_capture_begin(self._be))
+
+    def capture_end(self) -> None:
+        """End the capture and instantiate the graph."""
+        self._check(self._lib.yule_hip_capture_end(self._be))
+
+    def capture_replay(self) -> None:
+        """Launch the captured graph on the backend stream."""
+        self._check(self._lib.yule_hip_capture_replay(self._be))
 
     # -- conveniences ----------------------------------------------------------
     def upload(self, data) -> BufferHandle:

@@ -57,6 +57,10 @@ def _compile_hip(src: Path) -> Path:
 def build_hip() -> Path:
     OBJ.mkdir(exist_ok=True)
     srcs = [CSRC / s for s in HIP_SOURCES if (CSRC / s).exists()]
+    keep = {s.name + ".o" for s in srcs}
+    for stale in OBJ.glob("*.o"):   # objects of sources that no longer exist
+        if stale.name not in keep:
+            stale.unlink()
     jobs = min(len(srcs), int(os.environ.get("MAX_JOBS", "8")))
     with cf.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
         objs = list(ex.map(_compile_hip, srcs))

@@ -33,6 +33,9 @@ struct yule_hip_backend {
     std::mutex mu;  // guards `buffers`; ComputeBackend is Send + Sync
     std::unordered_map<uint64_t, yule::Buffer> buffers;
     hipEvent_t timer[2] = {nullptr, nullptr};
+    // harness capture of the calls between capture_begin and capture_end
+    hipGraph_t cap_graph = nullptr;
+    hipGraphExec_t cap_exec = nullptr;
     // device workspace shared by the ops that need one (GEMM staging and
     // split-K partials, split-KV attention partials); grown on demand,
     // freed with the backend

@@ -294,6 +294,56 @@ __global__ __launch_bounds__(256) void read_probe_kernel(const uint4 *__restrict
     if (threadIdx.x == 0) part[blockIdx.x] = red[0] ^ red[1] ^ red[2] ^ red[3];
 }
 
+// Variants of the read probe, to map what a single launch can read:
+//   P = 0  grid-stride 16-byte words, U independent loads in flight per lane
+//          (word i + j*T for j < U, T = threads in the grid);
+//   P = 1  per-lane runs of U consecutive words (a 16*U-byte run per lane),
+//          runs grid-strided;
+//   P = 2  one contiguous chunk of ceil(n16 / grid) words per workgroup,
+//          read with consecutive words across its lanes, U loads in flight
+//          (the layout of a matvec whose workgroups stream whole rows).
+// Every word is read exactly once in each variant, and the per-workgroup
+// XOR is written as in read_probe_kernel.
+template <int P, int U>
+__global__ __launch_bounds__(256) void read_probe_var_kernel(const uint4 *__restrict__ src, uint64_t n16,
+                                                             uint32_t *__restrict__ part, uint32_t grid) {
+    __shared__ uint32_t red[4];
+    uint32_t acc = 0;
+    uint64_t base, step, end = n16;
+    uint32_t lstride;   // distance between a lane's U words
+    if (P == 0) {
+        base = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+        lstride = grid * 256u;
+        step = (uint64_t)lstride * U;
+    } else if (P == 1) {
+        base = ((uint64_t)blockIdx.x * 256 + threadIdx.x) * U;
+        lstride = 1;
+        step = (uint64_t)grid * 256u * U;
+    } else {
+        const uint64_t chunk = (n16 + grid - 1) / grid;
+        const uint64_t c0 = chunk * blockIdx.x;
+        end = c0 + chunk < n16 ? c0 + chunk : n16;
+        base = c0 + threadIdx.x;
+        lstride = 256;
+        step = 256u * U;
+    }
+    for (uint64_t i = base; i < end; i += step) {
+        uint4 v[U];
+#pragma unroll
+        for (int j = 0; j < U; j++) {
+            const uint64_t w = i + (uint64_t)j * lstride;
+            v[j] = w < end ? src[w] : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < U; j++) acc ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) acc ^= __shfl_xor(acc, off, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) part[blockIdx.x] = red[0] ^ red[1] ^ red[2] ^ red[3];
+}
+
 namespace yule {
 __global__ __launch_bounds__(64) void empty_kernel() {}
 
@@ -474,6 +524,29 @@ int yule_hip_read_probe(yule_hip_backend *be, yule_buffer src, uint64_t bytes, y
     hipLaunchKernelGGL(read_probe_kernel, dim3(n_partials), dim3(256), 0, be->stream, (const uint4 *)ps, bytes / 16,
                        (uint32_t *)pp, n_partials);
     return check_launch("read_probe");
+}
+
+int yule_hip_read_probe_variant(yule_hip_backend *be, yule_buffer src, uint64_t bytes, yule_buffer partials,
+                                uint32_t n_partials, uint32_t pattern, uint32_t loads) {
+    BE_OR_FAIL(be);
+    if (bytes % 16 || n_partials == 0 || n_partials > 65536 || pattern > 2 ||
+        (loads != 1 && loads != 2 && loads != 4 && loads != 8))
+        return set_error(YULE_ERR_INVALID, "read_probe_variant: bytes a multiple of 16, n_partials in 1..65536, "
+                                           "pattern 0..2, loads 1, 2, 4 or 8");
+    void *ps, *pp;
+    int rc;
+    if ((rc = get_buffer(be, src, bytes, &ps, "read_probe_variant (src)")) ||
+        (rc = get_buffer(be, partials, (size_t)n_partials * 4, &pp, "read_probe_variant (partials)")))
+        return rc;
+    typedef void (*Kern)(const uint4 *, uint64_t, uint32_t *, uint32_t);
+    static const Kern k[3][4] = {
+        {read_probe_var_kernel<0, 1>, read_probe_var_kernel<0, 2>, read_probe_var_kernel<0, 4>, read_probe_var_kernel<0, 8>},
+        {read_probe_var_kernel<1, 1>, read_probe_var_kernel<1, 2>, read_probe_var_kernel<1, 4>, read_probe_var_kernel<1, 8>},
+        {read_probe_var_kernel<2, 1>, read_probe_var_kernel<2, 2>, read_probe_var_kernel<2, 4>, read_probe_var_kernel<2, 8>}};
+    const int li = loads == 1 ? 0 : loads == 2 ? 1 : loads == 4 ? 2 : 3;
+    hipLaunchKernelGGL(k[pattern][li], dim3(n_partials), dim3(256), 0, be->stream, (const uint4 *)ps, bytes / 16,
+                       (uint32_t *)pp, n_partials);
+    return check_launch("read_probe_variant");
 }
 
 int yule_hip_argmax(yule_hip_backend *be, yule_buffer in, uint32_t n, yule_buffer out) {

@@ -46,7 +46,7 @@ constexpr int kStreamSegs = 3;
 struct Segs {
     const uint8_t *w[kMaxSegs];
     float *y[kMaxSegs];
-    uint32_t start[kMaxSegs];   // first concatenated row of each segment (unused: = total)
+    uint32_t start[kMaxSegs];   // first concatenated row of each segment (slots past the last: total)
     uint32_t total;
 };
 

@@ -1,7 +1,7 @@
 // qmv_formats.h — per-format unit loads and dots of the fused dequant+dot
-// matvec (one lane owns one unit: a slice of one block), shared by the
-// streaming matvec (qmv.hip) and the fused Q/K/V + attention decode launch
-// (qkv_attn.hip).  The nibble arithmetic is described in qmv.hip.
+// matvec (one lane owns one unit: a slice of one block), used by the
+// streaming and column-looping matvec kernels (qmv.hip).  The nibble
+// arithmetic is described in qmv.hip.
 #pragma once
 #include <type_traits>
 

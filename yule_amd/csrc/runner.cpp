@@ -21,6 +21,9 @@
 
 using namespace yule;
 
+// most decode steps captured into one replayed graph
+constexpr long kMaxGraphSteps = 64;
+
 struct yule_hip_runner {
     yule_hip_backend *be = nullptr;
     uint32_t n_layers = 0, dim = 0, n_heads = 0, n_kv = 0, hd = 0, ff = 0, vocab = 0, max_seq = 0;
@@ -67,7 +70,7 @@ struct yule_hip_runner {
     // multi_steps of the same step per graph: generate_greedy replays these
     // over runs of decode steps of one variant (one graph launch per
     // multi_steps tokens: each launch of a graph costs ~7 us of idle GPU)
-    uint32_t multi_steps = 8;
+    uint32_t multi_steps = 8;   // at most kMaxGraphSteps
     // experimental: launches carry extra workgroups that read the next
     // launch's weights into its XCDs' L2 (bit 1: O -> gate/up, 2: gate/up ->
     // down, 4: Q/K/V -> O)
@@ -287,17 +290,34 @@ int enqueue_step(yule_hip_runner *r, bool split) {
     return enqueue_head(r);
 }
 
-int ensure_graph(yule_hip_runner *r, bool split) {
-    if (r->exec[split]) return YULE_OK;
+// Capture `steps` decode steps into *graph and instantiate *exec.  On any
+// failure after the capture began, the graph is destroyed and both slots are
+// left null, so a later call captures afresh without leaking the old graph.
+static int capture_steps(yule_hip_runner *r, bool split, uint32_t steps, hipGraph_t *graph, hipGraphExec_t *exec) {
+    if (*graph) {   // a graph whose instantiation failed earlier
+        (void)hipGraphDestroy(*graph);
+        *graph = nullptr;
+    }
     hipStream_t s = r->be->stream;
     int rc = hip_error(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "runner: begin capture");
     if (rc) return rc;
-    const int erc = enqueue_step(r, split);
-    rc = hip_error(hipStreamEndCapture(s, &r->graph[split]), "runner: end capture");
-    if (erc) return erc;
-    if (rc) return rc;
-    return hip_error(hipGraphInstantiate(&r->exec[split], r->graph[split], nullptr, nullptr, 0),
-                     "runner: graph instantiate");
+    int erc = YULE_OK;
+    for (uint32_t i = 0; i < steps && !erc; i++) erc = enqueue_step(r, split);
+    rc = hip_error(hipStreamEndCapture(s, graph), "runner: end capture");
+    if (!erc && !rc)
+        rc = hip_error(hipGraphInstantiate(exec, *graph, nullptr, nullptr, 0), "runner: graph instantiate");
+    if (erc || rc) {
+        if (*graph) (void)hipGraphDestroy(*graph);
+        *graph = nullptr;
+        *exec = nullptr;
+        return erc ? erc : rc;
+    }
+    return YULE_OK;
+}
+
+int ensure_graph(yule_hip_runner *r, bool split) {
+    if (r->exec[split]) return YULE_OK;
+    return capture_steps(r, split, 1, &r->graph[split], &r->exec[split]);
 }
 
 // generate_greedy's runs of decode steps replay multi-step graphs (not with
@@ -308,18 +328,8 @@ bool multi_ok(const yule_hip_runner *r) {
 }
 
 int ensure_graph_n(yule_hip_runner *r, bool split) {
-    const uint32_t n = r->multi_steps;
     if (r->exec_n[split]) return YULE_OK;
-    hipStream_t s = r->be->stream;
-    int rc = hip_error(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "runner: begin capture");
-    if (rc) return rc;
-    int erc = YULE_OK;
-    for (uint32_t i = 0; i < n && !erc; i++) erc = enqueue_step(r, split);
-    rc = hip_error(hipStreamEndCapture(s, &r->graph_n[split]), "runner: end capture");
-    if (erc) return erc;
-    if (rc) return rc;
-    return hip_error(hipGraphInstantiate(&r->exec_n[split], r->graph_n[split], nullptr, nullptr, 0),
-                     "runner: graph instantiate");
+    return capture_steps(r, split, r->multi_steps, &r->graph_n[split], &r->exec_n[split]);
 }
 
 // Replay the captured step for position `pos`, or (YULE_RUNNER_NO_GRAPH set,
@@ -397,14 +407,15 @@ int ensure_batch(yule_hip_runner *r, uint32_t n) {
 // pos0.. pos0 + n - 1; then the head over the last row, as the decode step
 // for position pos0 + n - 1 would run it, with ctl = {pos0 + n - 1, -,
 // prompt_len}: the argmax lands in tokens[pos0 + n - 1] and ctl[1], and ctl[0]
-// moves to pos0 + n.
-int prefill_rows(yule_hip_runner *r, uint32_t pos0, uint32_t n, uint32_t prompt_len) {
+// moves to pos0 + n.  ctl_ready: the caller has already written that control
+// block (set_ctl synchronizes the stream, so a timed caller does it first).
+int prefill_rows(yule_hip_runner *r, uint32_t pos0, uint32_t n, uint32_t prompt_len, bool ctl_ready = false) {
     hipStream_t s = r->be->stream;
     const uint32_t qd = r->n_heads * r->hd, kvd = r->n_kv * r->hd;
     int rc;
     if ((rc = ensure_batch(r, n))) return rc;
     // the control block only feeds the head and advance at the end
-    if ((rc = set_ctl(r, pos0 + n - 1, 0, prompt_len))) return rc;
+    if (!ctl_ready && (rc = set_ctl(r, pos0 + n - 1, 0, prompt_len))) return rc;
     // products alternate between the two workspaces; the O, gate/up and down
     // products leave their split-K reduction to the next product's pre-pass
     // (red), which reads their X right after (except the last down: the head
@@ -575,10 +586,18 @@ int yule_hip_runner_create(yule_hip_backend *be, const yule_model_desc *d, yule_
         return fail(rc);
     r->fused = getenv("YULE_RUNNER_UNFUSED") == nullptr && qmv_fusable(r->out_t, r->dim);
     // decode steps per replayed graph in generate_greedy (1: one per step)
-    if (const char *e = getenv("YULE_RUNNER_GRAPH_STEPS")) r->multi_steps = std::max(1, atoi(e));
-    if (const char *e = getenv("YULE_RUNNER_PREFETCH")) r->pf_mask = (uint32_t)atoi(e);
-    if (const char *e = getenv("YULE_RUNNER_PREFETCH_WGS")) r->pf_wgs = (uint32_t)atoi(e) & ~7u;
-    if (const char *e = getenv("YULE_RUNNER_PREFETCH_DELAY")) r->pf_delay = (uint32_t)atoi(e);
+    // tuning knobs, each clamped to a documented range: at most 64 decode steps
+    // per captured graph, 2048 prefetch workgroups and 4096 sleep rounds
+    auto knob = [](const char *name, long lo, long hi, long dflt) {
+        const char *e = getenv(name);
+        if (!e) return dflt;
+        const long v = atol(e);
+        return v < lo ? lo : v > hi ? hi : v;
+    };
+    r->multi_steps = (uint32_t)knob("YULE_RUNNER_GRAPH_STEPS", 1, kMaxGraphSteps, r->multi_steps);
+    r->pf_mask = (uint32_t)knob("YULE_RUNNER_PREFETCH", 0, 7, r->pf_mask);
+    r->pf_wgs = (uint32_t)knob("YULE_RUNNER_PREFETCH_WGS", 0, 2048, r->pf_wgs) & ~7u;
+    r->pf_delay = (uint32_t)knob("YULE_RUNNER_PREFETCH_DELAY", 0, 4096, r->pf_delay);
     for (const auto &L : r->layers)
         r->fused = r->fused && qmv_fusable(L.tq, r->dim) && qmv_fusable(L.tk, r->dim) && qmv_fusable(L.tv, r->dim) &&
                    qmv_fusable(L.to, qd) && qmv_fusable(L.tg, r->dim) && qmv_fusable(L.tu, r->dim) &&
@@ -671,15 +690,18 @@ int yule_hip_runner_generate_greedy(yule_hip_runner *r, const uint32_t *prompt, 
                         "runner: prompt upload")))
         return rc;
     hipEvent_t e0 = nullptr, e1 = nullptr, p0 = nullptr;
+    const bool batched = r->batchable && n_prompt >= 2;
     if ((rc = hip_error(hipEventCreate(&e0), "hipEventCreate")) || (rc = hip_error(hipEventCreate(&e1), "hipEventCreate")) ||
         (rc = hip_error(hipEventCreate(&p0), "hipEventCreate")))
         goto done;
     if (r->batchable && n_prompt >= 2 && (rc = ensure_batch(r, n_prompt))) goto done;
+    // the control block is written (a host synchronization) before p0, so the
+    // prefill time holds GPU work only
+    if ((rc = set_ctl(r, batched ? n_prompt - 1 : 0, 0, n_prompt))) goto done;
     if ((rc = hip_error(hipEventRecord(p0, s), "hipEventRecord"))) goto done;
-    if (r->batchable && n_prompt >= 2) {   // the prompt as one batched pass
-        if ((rc = prefill_rows(r, 0, n_prompt, n_prompt))) goto done;
+    if (batched) {   // the prompt as one batched pass
+        if ((rc = prefill_rows(r, 0, n_prompt, n_prompt, true))) goto done;
     } else {
-        if ((rc = set_ctl(r, 0, 0, n_prompt))) goto done;
         for (uint32_t i = 0; i < n_prompt && !rc; i++) rc = run_step(r, i);
         if (rc) goto done;
     }

@@ -149,6 +149,8 @@ int yule_hip_destroy(yule_hip_backend *be) {
     if (be->scratch) hipFree(be->scratch);
     for (hipEvent_t e : be->timer)
         if (e) hipEventDestroy(e);
+    if (be->cap_exec) hipGraphExecDestroy(be->cap_exec);
+    if (be->cap_graph) hipGraphDestroy(be->cap_graph);
     hipStreamDestroy(be->stream);
     delete be;
     return YULE_OK;
@@ -502,6 +504,33 @@ int yule_hip_timer_stop(yule_hip_backend *be, float *ms) {
         (rc = hip_error(hipEventSynchronize(be->timer[1]), "timer: synchronize")))
         return rc;
     return hip_error(hipEventElapsedTime(ms, be->timer[0], be->timer[1]), "timer: elapsed");
+}
+
+static void drop_capture(yule_hip_backend *be) {
+    if (be->cap_exec) (void)hipGraphExecDestroy(be->cap_exec);
+    if (be->cap_graph) (void)hipGraphDestroy(be->cap_graph);
+    be->cap_exec = nullptr;
+    be->cap_graph = nullptr;
+}
+
+int yule_hip_capture_begin(yule_hip_backend *be) {
+    YULE_CHECK_BE(be);
+    drop_capture(be);
+    return hip_error(hipStreamBeginCapture(be->stream, hipStreamCaptureModeThreadLocal), "capture: begin");
+}
+
+int yule_hip_capture_end(yule_hip_backend *be) {
+    YULE_CHECK_BE(be);
+    int rc = hip_error(hipStreamEndCapture(be->stream, &be->cap_graph), "capture: end");
+    if (!rc) rc = hip_error(hipGraphInstantiate(&be->cap_exec, be->cap_graph, nullptr, nullptr, 0), "capture: instantiate");
+    if (rc) drop_capture(be);
+    return rc;
+}
+
+int yule_hip_capture_replay(yule_hip_backend *be) {
+    YULE_CHECK_BE(be);
+    if (!be->cap_exec) return set_error(YULE_ERR_INVALID, "capture_replay: nothing captured");
+    return hip_error(hipGraphLaunch(be->cap_exec, be->stream), "capture: replay");
 }
 
 }  // extern "C"
