@@ -489,6 +489,36 @@ def probe_variants(hip, sizes_mb=(33, 128), grids=(512, 1024, 2048, 4096)):
                       "back-to-back stream launches over rotating buffers, HIP events"}), flush=True)
 
 
+def mfma_probe(hip, iters=4000):
+    """MFMA issue rate with no memory traffic (yule_hip_mfma_probe): both f16
+    shapes, 1-8 independent chains per wave, 1-2 workgroups of four waves per
+    CU (one or two waves per SIMD), median of 3 timed launches after one
+    warm-up.  Prints one JSON line."""
+    info = hip.device_info()
+    inp = hip.upload((np.random.default_rng(5).standard_normal(1024) * 0.01).astype(np.float16))
+    out = {}
+    for shape, flops in ((0, 16384), (1, 32768)):
+        for per_cu in (1, 2):
+            n_wg = info.compute_units * per_cu
+            o = hip.allocate(n_wg * 1024)
+            for chains in (1, 2, 4, 8):
+                hip.mfma_probe(inp, o, shape, chains, n_wg, 64)
+                runs = []
+                for _ in range(3):
+                    hip.timer_start()
+                    hip.mfma_probe(inp, o, shape, chains, n_wg, iters)
+                    runs.append(hip.timer_stop())
+                ms = float(np.median(runs))
+                tf = flops * chains * iters * 4 * n_wg / (ms * 1e-3) / 1e12
+                key = f"{'16x16x32' if shape == 0 else '32x32x16'} {per_cu} wave/SIMD {chains} chains"
+                # each SIMD runs per_cu waves of chains * iters MFMAs
+                out[key] = {"TFLOP/s": round(tf, 1), "mfma_per_us_per_simd": round(per_cu * chains * iters / (ms * 1e3), 2)}
+                log(f"mfma probe {key}: {tf:.1f} TFLOP/s")
+            hip.free(o)
+    hip.free(inp)
+    print(json.dumps({"mfma_probe": out, "iters": iters}), flush=True)
+
+
 def profile_gemm(hip, n, M=2048):
     """N launches of the Q4_K 14336x4096 prefill GEMM at M tokens (BASELINE
     M in {64, 512, 2048}), for rocprofv3 kernel-trace and MFMA
@@ -506,15 +536,16 @@ def profile_gemm(hip, n, M=2048):
 
 
 def profile_decode(hip, n):
-    """N greedy decode steps of the TinyLlama-shaped model after a 16-token
-    prompt, with the runner's kernels launched one by one (tracing profilers
-    do not follow graph replays)."""
+    """N greedy decode steps of the TinyLlama-shaped model after the bench's
+    128-token prompt (positions 128.., as the bench decodes), with the
+    runner's kernels launched one by one (tracing profilers do not follow
+    graph replays)."""
     os.environ["YULE_RUNNER_NO_GRAPH"] = "1"   # read by the runner at its first step
     from yule_amd.backend import HipRunner
     from yule_amd.model import TINYLLAMA, SyntheticModel
     model = SyntheticModel.generate(TINYLLAMA, seed=0)
     run = HipRunner(hip, model)
-    toks, ms = run.generate_greedy(synth.uniform_tokens(1, 16, TINYLLAMA.vocab), n)
+    toks, ms = run.generate_greedy(synth.uniform_tokens(1, 128, TINYLLAMA.vocab), n)
     run.close()
     print(json.dumps({"steps": n, "ms_per_step_ungraphed": round(ms, 4)}), flush=True)
 
@@ -561,6 +592,7 @@ def main():
                     help="only measure the single-launch streaming-read rate against launch size (JSON line)")
     ap.add_argument("--probe-variants", action="store_true",
                     help="only measure the single-launch read rate by access pattern and grid (JSON line)")
+    ap.add_argument("--mfma-probe", action="store_true", help="only measure the MFMA issue rate (JSON line)")
     ap.add_argument("--profile-decode", type=int, default=0, metavar="N",
                     help="only run N TinyLlama decode steps with kernels launched one by one (for rocprofv3)")
     ap.add_argument("--profile-prefill", type=int, default=0, metavar="N",
@@ -581,6 +613,9 @@ def main():
         return
     if args.probe_curve:
         probe_curve(hip)
+        return
+    if args.mfma_probe:
+        mfma_probe(hip)
         return
     if args.probe_variants:
         probe_variants(hip)

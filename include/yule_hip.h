@@ -373,6 +373,16 @@ int yule_hip_read_probe(yule_hip_backend *be, yule_buffer src, uint64_t bytes, y
  * (16, 32, 64 or 128-byte runs), runs grid-strided; 2 = one contiguous chunk
  * per workgroup, consecutive words across its lanes, `loads` in flight.
  * No reference counterpart. */
+/* MFMA issue-rate probe (no reference counterpart): n_wg workgroups of 256
+ * threads (four waves), each wave running `chains` (1, 2, 4 or 8)
+ * independent accumulator chains of `iters` MFMAs with no memory traffic in
+ * the loop: shape 0 = v_mfma_f32_16x16x32_f16 (16384 flops each), 1 =
+ * v_mfma_f32_32x32x16_f16 (32768 flops).  Operands are the 128 16-byte words
+ * of `in` (f16 values); one float per thread goes to `out` (n_wg * 1 KiB).
+ * Time it with timer_start / timer_stop. */
+int yule_hip_mfma_probe(yule_hip_backend *be, yule_buffer in, yule_buffer out, uint32_t shape, uint32_t chains,
+                        uint32_t n_wg, uint32_t iters);
+
 int yule_hip_read_probe_variant(yule_hip_backend *be, yule_buffer src, uint64_t bytes, yule_buffer partials,
                                 uint32_t n_partials, uint32_t pattern, uint32_t loads);
 

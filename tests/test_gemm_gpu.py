@@ -106,10 +106,10 @@ def test_gemm_wide_tiles(hip, dt, M, N, K):
 
 @pytest.mark.parametrize("N,K", [(14336, 4096), (4096, 14336)])
 def test_gemm_config_shapes_m2048(hip, N, K):
-    """BASELINE configs[3] at M=2048: 14336x4096 is 896 tiles of 128 x 256,
-    so its last 128 tiles (m rows 1664-2047, from n 10240 at row 1664 on)
-    run as K halves; 4096x14336 is one whole round.  Rows in both kinds of
-    tile vs the oracle, and a repeat call bit-identical."""
+    """BASELINE configs[3] at M=2048, on the 256 x 256 tiles (128 x 64 per
+    wave, accumulators rescaled per super-block): 14336x4096 is 448 tiles,
+    4096x14336 128 tiles in two K splits.  Rows at tile edges and in the
+    last tiles vs the oracle, and a repeat call bit-identical."""
     dt, M = DType.Q4_K, 2048
     say(f"[gemm] Q4_K {N}x{K} M={M}")
     w = synth.gen_quant(dt, 72, N, K)
@@ -117,7 +117,7 @@ def test_gemm_config_shapes_m2048(hip, N, K):
     y = run_gemm(hip, dt, w, xb, M, N, K)
     assert np.array_equal(y, run_gemm(hip, dt, w, xb, M, N, K)), "second call differs"
     xf = bf16_to_f32(xb).reshape(M, K)
-    for m in (0, 1663, 1664, 1800, 2047):
+    for m in (0, 255, 256, 1663, 1664, 1800, 2047):
         ref = oracle.qmv_f64(int(dt), w, xf[m], N, K)
         assert np.max(np.abs(y[m] - ref)) <= tolerance_bar(ref), f"row {m}"
 

@@ -77,6 +77,8 @@ _SIGS: dict[str, tuple] = {
     "yule_hip_gguf_get_array_len": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(C.c_uint64)]),
     "yule_hip_runner_create_from_gguf": (C.c_int, [C.c_void_p, C.c_char_p, C.c_uint32, C.POINTER(C.c_void_p)]),
     "yule_hip_read_probe": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint32]),
+    "yule_hip_mfma_probe": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint32,
+                                      C.c_uint32]),
     "yule_hip_read_probe_variant": (C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint32,
                                               C.c_uint32, C.c_uint32]),
     "yule_hip_timer_start": (C.c_int, [C.c_void_p]),
@@ -285,6 +287,10 @@ class HipBackend:
         """One streaming-read launch over n_bytes of src (roofline probe);
         partials[i] = XOR of the words workgroup i read."""
         self._check(self._lib.yule_hip_read_probe(self._be, _h(src), n_bytes, _h(partials), n_partials))
+
+    def mfma_probe(self, inp, out, shape: int, chains: int, n_wg: int, iters: int) -> None:
+        """MFMA issue-rate probe (shape 0: 16x16x32 f16, 1: 32x32x16 f16)."""
+        self._check(self._lib.yule_hip_mfma_probe(self._be, _h(inp), _h(out), shape, chains, n_wg, iters))
 
     def read_probe_variant(self, src, n_bytes: int, partials, n_partials: int, pattern: int, loads: int) -> None:
         """A read-probe variant (pattern 0 grid-stride, 1 per-lane runs, 2 per-workgroup

@@ -397,7 +397,17 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
     // the load of y is not waited for ahead of the first stage's loads)
     const size_t y_off = splits > 1 && !tail ? (size_t)zs * M * N : 0;
 
+    // RS (Q4_K, Q5_K): the accumulators are kept in units of the current
+    // super-block's d of their column (u): before each super-block the
+    // column's acc is rescaled by u / d_new, then the block's integer-exact
+    // products accumulate straight into acc, with no second accumulator set
+    // (one f32 rounding per super-block, ~2^-24 of the partial sum).  A
+    // super-block with d = 0 keeps the unit, and its B operand is zero.
+    // Other formats accumulate each super-block (or block) into tmp and add
+    // d * tmp.
+    constexpr bool RS = Q4;
     floatx4 acc[TM][4], tmp[TM][4];
+    float unit[4] = {1.f, 1.f, 1.f, 1.f};
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -537,8 +547,11 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
             const uint32_t scs = ((A >> sh) & mA) | ((hd.y >> (sh + 2)) & mB);
             // high nibbles stay in place (16 q * 2^-24, still a denormal
             // pair) against sc * 2^6, so the product is again sc * q * 2^-14
-            const _Float16 f0 = (_Float16)(float)((scs & 0xFFu) * 1024u);
-            const _Float16 f1 = (_Float16)(float)((scs >> 8) * 64u);
+            // (RS: a super-block with d = 0 contributes through its min term
+            // only, so its B operand is zero)
+            const uint32_t dz = RS && (hd.x & 0x7FFFu) == 0u ? 0u : 1u;
+            const _Float16 f0 = (_Float16)(float)((scs & 0xFFu) * 1024u * dz);
+            const _Float16 f1 = (_Float16)(float)((scs >> 8) * 64u * dz);
             const h2v S0 = {f0, f0}, S1 = {f1, f1};
             const uint32_t q[4] = {R.q.x, R.q.y, R.q.z, R.q.w};
             const uint32_t qb[4] = {R.q5h.x, R.q5h.y, R.q5h.z, R.q5h.w};
@@ -616,8 +629,20 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
 
     // first: this stage opens a super-block, so its first k-step starts
     // each tile's partial from zero (no separate clearing of tmp)
-    auto compute = [&](int b, auto first_t) {
+    auto compute = [&](int b, auto first_t, uint32_t slot = 0) {
         constexpr bool first = decltype(first_t)::value;
+        if constexpr (RS && first) {
+            // a new super-block: acc into units of its d (slot: its scale slot)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float dn = sd[slot][0][wn * 64 + j * 16 + (lane & 15u)];
+                const bool nz = dn != 0.f;
+                const float f = nz ? unit[j] / dn : 1.f;
+                unit[j] = nz ? dn : unit[j];
+#pragma unroll
+                for (int i = 0; i < TM; i++) acc[i][j] *= f;
+            }
+        }
 #pragma unroll
         for (int ks = 0; ks < GSK / 32; ks++) {
             half8 a[TM], bw[4];
@@ -662,6 +687,11 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
                         tmp[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b2, tmp[i][j], 0, 0, 0);
                     }
                 }
+            } else if constexpr (RS) {
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], bw[j], acc[i][j], 0, 0, 0);
             } else {
 #pragma unroll
                 for (int i = 0; i < TM; i++)
@@ -712,7 +742,7 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
     // the loop head instead of only for the stage about to be dequantized.
     if constexpr (SBP) {
         for (uint32_t s = 0; s < S; s += 4) {
-            compute(0, opens);
+            compute(0, opens, (s >> 2) & 1u);
             dequant_stage(s + 1, R1, 1, std::integral_constant<int, 1>{});
             load_stage(s + 3 < S ? s + 3 : S - 1, R1, std::integral_constant<int, 3>{});
             __syncthreads();
@@ -725,7 +755,7 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
             load_stage(s + 5 < S ? s + 5 : S - 1, R1, std::integral_constant<int, 1>{});
             __syncthreads();
             compute(1, cont);
-            block_done(s >> 2);
+            if constexpr (!RS) block_done(s >> 2);
             dequant_stage(s + 4, R0, 0, std::integral_constant<int, 0>{});
             load_stage(s + 6 < S ? s + 6 : S - 1, R0, std::integral_constant<int, 2>{});
             __syncthreads();
@@ -760,18 +790,28 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
         xcur = xl;
         sweep();
     }
+    if constexpr (RS) {   // back to absolute units
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) acc[i][j] *= unit[j];
+    }
 
     // the row scales of this lane's output rows, loaded now so that the
     // stores below wait on nothing (a load issued after stores would wait
     // for them too: loads and stores share one counter)
+    // (the 256-row tile loads them at the stores instead: registers)
+    constexpr bool RS_EARLY = BM < 256;
     float rs[TM][4];
+    if constexpr (RS_EARLY) {
 #pragma unroll
-    for (int i = 0; i < TM; i++)
+        for (int i = 0; i < TM; i++)
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const uint32_t m = m0 + wm * (BM / 2) + i * 16 + 4 * (lane >> 4) + e;
-            rs[i][e] = rowscale[m < M ? m : M - 1u];
-        }
+            for (int e = 0; e < 4; e++) {
+                const uint32_t m = m0 + wm * (BM / 2) + i * 16 + 4 * (lane >> 4) + e;
+                rs[i][e] = rowscale[m < M ? m : M - 1u];
+            }
+    }
     if (Q4 && xs_hi) {   // (no sums: the second, lo, product of an f32 X)
         // min term: acc -= sum_j xsum[m][j] * (dmin*mn)[r][j] over the K/32
         // sub-blocks.  In chunks of four super-blocks the workgroup stages
@@ -861,7 +901,8 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
                 const uint32_t m = m0 + wm * (BM / 2) + i * 16 + 4 * (lane >> 4) + e;
                 if (m < M && r < N) {
                     float *const y = ysplit;
-                    const float v = acc[i][j][e] * rs[i][e];   // the row's power of two back out: exact
+                    const float sc = RS_EARLY ? rs[i][e] : rowscale[m];
+                    const float v = acc[i][j][e] * sc;   // the row's power of two back out: exact
                     if (halves) unsafeAtomicAdd(y + (size_t)m * N + r, v);
                     else if (accumulate && splits == 1) y[(size_t)m * N + r] += v;
                     else y[(size_t)m * N + r] = v;
@@ -917,8 +958,15 @@ uint32_t gemm_bn(uint32_t m, uint32_t dtype) {
 // sweeps make the 128-row tile spill; the 64-row one keeps three
 // workgroups per CU and twice the workgroups); 128 otherwise.
 // YULE_GEMM_F32_BM64 sets that f32 bound.
-uint32_t gemm_bm(uint32_t m, bool f32x) {
+// Q4_K with bf16 X from M = YULE_GEMM_BM256 (default 1024) on: 256-row
+// tiles of 256-wide ones, each wave a 128 x 64 sub-tile (its accumulators
+// fit beside the stage registers because they need no second set), which
+// halves the LDS bytes each wave reads per MFMA against 64 x 64 sub-tiles:
+// M = 2048 +12-14% (14336 x 4096 and 4096 x 14336).
+uint32_t gemm_bm(uint32_t m, bool f32x, uint32_t dtype, uint32_t bn) {
     static const int env = env_int("YULE_GEMM_F32_BM64", 128);
+    static const int big = env_int("YULE_GEMM_BM256", 1024);
+    if ((uint32_t)big <= m && !f32x && bn == 256 && dtype == YULE_DTYPE_Q4_K) return 256u;
     return m <= 64 || (f32x && m <= (uint32_t)env) ? 64u : 128u;
 }
 
@@ -985,6 +1033,9 @@ void launch_gemm_bn(hipStream_t s, const GemmPass &p) {
             hipLaunchKernelGGL((gemm_kernel<DT, 128, BN, 2>), dim3(grid), dim3(2 * BN), 0, s, YULE_GEMM_ARGS);
     } else if (bm == 64) {
         hipLaunchKernelGGL((gemm_kernel<DT, 64, BN, 1>), dim3(grid), dim3(2 * BN), 0, s, YULE_GEMM_ARGS);
+    } else if (bm == 256) {   // 128 x 64 wave tiles (Q4_K, 256-wide tiles; chosen by gemm_bm)
+        if constexpr (DT == YULE_DTYPE_Q4_K && BN == 256)
+            hipLaunchKernelGGL((gemm_kernel<DT, 256, BN, 1>), dim3(grid), dim3(2 * BN), 0, s, YULE_GEMM_ARGS);
     } else {
         hipLaunchKernelGGL((gemm_kernel<DT, 128, BN, 1>), dim3(grid), dim3(2 * BN), 0, s, YULE_GEMM_ARGS);
     }
@@ -1030,7 +1081,7 @@ static GemmWork gemm_work(uint32_t m, uint32_t n_rows, uint32_t n_cols, uint32_t
     GemmWork g;
     g.q4 = dtype == YULE_DTYPE_Q4_K || dtype == YULE_DTYPE_Q5_K;   // min term: X sub-block sums
     g.bn = gemm_bn(m, dtype);
-    g.bm = gemm_bm(m, f32x);
+    g.bm = gemm_bm(m, f32x, dtype, g.bn);
     g.ks = gemm_splits(m, n_rows, n_cols, g.bn, g.bm, gemm_wgs_per_cu(dtype, g.bm, g.bn, f32x));
     g.tail = gemm_tail(m, n_rows, n_cols, g.bn, g.bm, g.ks);
     g.n_x = (size_t)m * n_cols;

@@ -344,6 +344,54 @@ __global__ __launch_bounds__(256) void read_probe_var_kernel(const uint4 *__rest
     if (threadIdx.x == 0) part[blockIdx.x] = red[0] ^ red[1] ^ red[2] ^ red[3];
 }
 
+// MFMA issue-rate probe: CH independent accumulator chains per wave, no
+// memory traffic inside the loop (operands come from `in`, so nothing folds),
+// one result per lane to `out`.  SHAPE 0: v_mfma_f32_16x16x32_f16 (16384
+// flops), 1: v_mfma_f32_32x32x16_f16 (32768 flops).
+typedef _Float16 probe_half8 __attribute__((ext_vector_type(8)));
+typedef float probe_f4 __attribute__((ext_vector_type(4)));
+typedef float probe_f16v __attribute__((ext_vector_type(16)));
+template <int SHAPE, int CH>
+__global__ __launch_bounds__(256) void mfma_probe_kernel(const uint4 *__restrict__ in, float *__restrict__ out,
+                                                         uint32_t iters) {
+    const uint4 av = in[threadIdx.x & 63u], bv = in[64 + (threadIdx.x & 63u)];
+    const probe_half8 a = __builtin_bit_cast(probe_half8, av), b = __builtin_bit_cast(probe_half8, bv);
+    float s = 0.f;
+    if constexpr (SHAPE == 0) {
+        // chains as separate variables (an array of them made the compiler
+        // rotate accumulators through copies inside the loop)
+        // distinct starting values, so that no two chains are the same computation
+        const float z = __builtin_bit_cast(float, av.x) * 0.f;
+        probe_f4 c0 = {z, z, z, z}, c1 = c0 + 1.f, c2 = c0 + 2.f, c3 = c0 + 3.f, c4 = c0 + 4.f, c5 = c0 + 5.f,
+                 c6 = c0 + 6.f, c7 = c0 + 7.f;
+        for (uint32_t it = 0; it < iters; it++) {
+            c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c0, 0, 0, 0);
+            if (CH > 1) c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c1, 0, 0, 0);
+            if (CH > 2) c2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c2, 0, 0, 0);
+            if (CH > 2) c3 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c3, 0, 0, 0);
+            if (CH > 4) c4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c4, 0, 0, 0);
+            if (CH > 4) c5 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c5, 0, 0, 0);
+            if (CH > 4) c6 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c6, 0, 0, 0);
+            if (CH > 4) c7 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c7, 0, 0, 0);
+        }
+        const probe_f4 t = ((c0 + c1) + (c2 + c3)) + ((c4 + c5) + (c6 + c7));
+        s = t[0] + t[3];
+    } else {
+        probe_f16v acc[CH];
+        const float z = __builtin_bit_cast(float, av.x) * 0.f;
+#pragma unroll
+        for (int j = 0; j < CH; j++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[j][e] = z + (float)j;
+        for (uint32_t it = 0; it < iters; it++)
+#pragma unroll
+            for (int j = 0; j < CH; j++) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[j], 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < CH; j++) s += acc[j][0] + acc[j][15];
+    }
+    out[(size_t)blockIdx.x * 256 + threadIdx.x] = s;
+}
+
 namespace yule {
 __global__ __launch_bounds__(64) void empty_kernel() {}
 
@@ -547,6 +595,26 @@ int yule_hip_read_probe_variant(yule_hip_backend *be, yule_buffer src, uint64_t 
     hipLaunchKernelGGL(k[pattern][li], dim3(n_partials), dim3(256), 0, be->stream, (const uint4 *)ps, bytes / 16,
                        (uint32_t *)pp, n_partials);
     return check_launch("read_probe_variant");
+}
+
+int yule_hip_mfma_probe(yule_hip_backend *be, yule_buffer in, yule_buffer out, uint32_t shape, uint32_t chains,
+                        uint32_t n_wg, uint32_t iters) {
+    BE_OR_FAIL(be);
+    if (shape > 1 || (chains != 1 && chains != 2 && chains != 4 && chains != 8) || n_wg == 0 || n_wg > 65536 ||
+        iters == 0)
+        return set_error(YULE_ERR_INVALID, "mfma_probe: shape 0 or 1, chains 1, 2, 4 or 8, n_wg in 1..65536, iters > 0");
+    void *pi, *po;
+    int rc;
+    if ((rc = get_buffer(be, in, 128 * 16, &pi, "mfma_probe (in)")) ||
+        (rc = get_buffer(be, out, (size_t)n_wg * 256 * 4, &po, "mfma_probe (out)")))
+        return rc;
+    typedef void (*Kern)(const uint4 *, float *, uint32_t);
+    static const Kern k[2][4] = {
+        {mfma_probe_kernel<0, 1>, mfma_probe_kernel<0, 2>, mfma_probe_kernel<0, 4>, mfma_probe_kernel<0, 8>},
+        {mfma_probe_kernel<1, 1>, mfma_probe_kernel<1, 2>, mfma_probe_kernel<1, 4>, mfma_probe_kernel<1, 8>}};
+    const int ci = chains == 1 ? 0 : chains == 2 ? 1 : chains == 4 ? 2 : 3;
+    hipLaunchKernelGGL(k[shape][ci], dim3(n_wg), dim3(256), 0, be->stream, (const uint4 *)pi, (float *)po, iters);
+    return check_launch("mfma_probe");
 }
 
 int yule_hip_argmax(yule_hip_backend *be, yule_buffer in, uint32_t n, yule_buffer out) {
