@@ -660,6 +660,8 @@ def main():
                 "kernel": f"{dominant_kernel_name()} 14336x4096", "avg_launch_us": round(us, 3),
                 "avg_launch_us_passes": [round(u, 3) for u in dom_runs],
                 "algo_bytes_per_launch": dom_bytes, "profile_avg_us": profile_avg_us()}
+    if roofline["profile_avg_us"]:   # the committed rocprofv3 trace of this same loop
+        roofline["frac_trace"] = round(dom_bytes / (roofline["profile_avg_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
     log(f"dominant kernel Q4_K 14336x4096: {us:.2f} us/launch, {gbs:.1f} GB/s")
     roofline["read_probe"] = read_probe(hip, dom, "ffn_gate", n_dom)
     # the fastest single-launch read pattern of the variant sweep (bench.py --probe-variants)
