@@ -315,10 +315,16 @@ struct GemmW {
 // Split-K: split z of `splits` takes super-blocks [kb_lo, kb_hi) and,
 // when splits > 1, writes its partial tile to y + z*M*N (summed in a
 // fixed order by gemm_reduce_kernel, so results do not depend on timing).
-// Q4_K, Q8_0 and Q4_0 run two waves per SIMD (Q4_K's register budget holds
-// with a few spilled bytes); Q6_K's larger dequant state keeps it at one.
+// Two waves per SIMD, except the Q6_K kernels with f32 X (two sweeps) or a
+// 128 x 128 tile, whose dequant state does not fit that register budget
+// (the 64-row two-sweep one would, but measured slower in the runner's
+// batched prefill: 3.53 against 3.39 ms): one wave per SIMD there.
+constexpr int gemm_waves_per_simd(uint32_t dt, int bm, int bn, int sweeps) {
+    return dt == YULE_DTYPE_Q6_K && (sweeps == 2 || (bm == 128 && bn == 128)) ? 1 : 2;
+}
+
 template <uint32_t DT, int BM, int BN, int SWEEPS>
-__global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YULE_DTYPE_Q6_K ? 1 : 2))) void gemm_kernel(
+__global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(gemm_waves_per_simd(DT, BM, BN, SWEEPS)))) void gemm_kernel(
     // the first 14 dwords (what the first loads need) arrive preloaded in
     // SGPRs: no kernel-argument load delays them
     const _Float16 *__restrict__ xh, const uint8_t *w0, const uint8_t *w1, const uint8_t *w2, uint32_t s1,
@@ -397,15 +403,17 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
     // the load of y is not waited for ahead of the first stage's loads)
     const size_t y_off = splits > 1 && !tail ? (size_t)zs * M * N : 0;
 
-    // RS (Q4_K, Q5_K): the accumulators are kept in units of the current
-    // super-block's d of their column (u): before each super-block the
-    // column's acc is rescaled by u / d_new, then the block's integer-exact
-    // products accumulate straight into acc, with no second accumulator set
-    // (one f32 rounding per super-block, ~2^-24 of the partial sum).  A
-    // super-block with d = 0 keeps the unit, and its B operand is zero.
-    // Other formats accumulate each super-block (or block) into tmp and add
-    // d * tmp.
-    constexpr bool RS = Q4;
+    // RS (Q4_K, Q5_K, and Q6_K with bf16 X): the accumulators
+    // are kept in units of the current super-block's d of their column (u):
+    // before each super-block the column's acc is rescaled by u / d_new, then
+    // the block's products accumulate straight into acc, with no second
+    // accumulator set (one f32 rounding per super-block, ~2^-24 of the
+    // partial sum).  A super-block with d = 0 keeps the unit, and its B
+    // operand is zero.  Q8_0 / Q4_0 (d per 32-weight block) accumulate each
+    // block into tmp and add d * tmp; so do Q8_K, whose kernel measured
+    // 10-15% slower rescaled (M = 64-2048), and Q6_K with f32 X (the
+    // runner's batched prefill 2% slower rescaled).
+    constexpr bool RS = !B32 && !Q8K && !(DT == YULE_DTYPE_Q6_K && SWEEPS == 2);
     floatx4 acc[TM][4], tmp[TM][4];
     float unit[4] = {1.f, 1.f, 1.f, 1.f};
 #pragma unroll
@@ -593,7 +601,8 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
             align_raw<4>(R.sc, R.msc, scw);
             align_raw<4>(R.d, R.md, dw);
             const uint32_t g = 2u * (st & 1u) + part, nib = 4u * (st & 1u), qsh = 2u * g;
-            const int isc0 = (int8_t)(scw[0] & 0xFFu), isc1 = (int8_t)((scw[0] >> 8) & 0xFFu);
+            const int dnz = !RS || (dw[0] & 0x7FFFu) ? 1 : 0;   // RS: d = 0 zeroes B
+            const int isc0 = dnz * (int8_t)(scw[0] & 0xFFu), isc1 = dnz * (int8_t)((scw[0] >> 8) & 0xFFu);
             const _Float16 sc0 = (_Float16)(float)isc0, sc1 = (_Float16)(float)isc1;
             const h2v S0 = {sc0, sc0}, S1 = {sc1, sc1};
             if constexpr (X6) {   // the stage's sub-blocks 2 part and 2 part + 1 of this row
@@ -627,22 +636,22 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
         }
     };
 
-    // first: this stage opens a super-block, so its first k-step starts
-    // each tile's partial from zero (no separate clearing of tmp)
+    // a new super-block: acc into units of its d (slot: its scale slot)
+    auto rescale = [&](uint32_t slot) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float dn = sd[slot][0][wn * 64 + j * 16 + (lane & 15u)];
+            const bool nz = dn != 0.f;
+            const float f = nz ? unit[j] / dn : 1.f;
+            unit[j] = nz ? dn : unit[j];
+#pragma unroll
+            for (int i = 0; i < TM; i++) acc[i][j] *= f;
+        }
+    };
+    // first: this stage opens a super-block (RS: rescale first)
     auto compute = [&](int b, auto first_t, uint32_t slot = 0) {
         constexpr bool first = decltype(first_t)::value;
-        if constexpr (RS && first) {
-            // a new super-block: acc into units of its d (slot: its scale slot)
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const float dn = sd[slot][0][wn * 64 + j * 16 + (lane & 15u)];
-                const bool nz = dn != 0.f;
-                const float f = nz ? unit[j] / dn : 1.f;
-                unit[j] = nz ? dn : unit[j];
-#pragma unroll
-                for (int i = 0; i < TM; i++) acc[i][j] *= f;
-            }
-        }
+        if constexpr (RS && first) rescale(slot);
 #pragma unroll
         for (int ks = 0; ks < GSK / 32; ks++) {
             half8 a[TM], bw[4];
@@ -682,7 +691,7 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
                         b2[2 * e] = p2.x; b2[2 * e + 1] = p2.y;
                     }
 #pragma unroll
-                    for (int i = 0; i < TM; i++) {
+                    for (int i = 0; i < TM; i++) {   // (X6 is never RS)
                         tmp[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b1, tmp[i][j], 0, 0, 0);
                         tmp[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b2, tmp[i][j], 0, 0, 0);
                     }
@@ -692,7 +701,7 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
                 for (int i = 0; i < TM; i++)
 #pragma unroll
                     for (int j = 0; j < 4; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], bw[j], acc[i][j], 0, 0, 0);
-            } else {
+            } else {   // not RS (Q8_K, Q6_K with f32 X): the super-block into tmp (SBP: its first k-step from zero)
 #pragma unroll
                 for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -702,7 +711,7 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
             }
         }
     };
-    auto block_done = [&](uint32_t kb) {   // final += d[r] * super-block partial
+    auto block_done = [&](uint32_t kb) {   // not RS: acc += d[r] * super-block partial
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const float dr = sd[kb & 1u][0][wn * 64 + j * 16 + (lane & 15u)];
@@ -732,9 +741,9 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
     // Q4_K, Q5_K, Q8_K: one super-block (four stages) per pass; stage t computes out of
     // LDS buffer t & 1 while stage t + 1 is dequantized into the other and
     // the bytes of stage t + 3 load into the register set stage t + 1 freed.
-    // The pass's first stage starts every tile's partial from zero.  Q6_K,
-    // whose dequant state is larger, keeps a two-stage pass (the longer one
-    // spills) and clears the partials in block_done.
+    // The pass's first stage rescales the accumulators to the super-block's
+    // d (compute(first)).  Q6_K, whose dequant state is larger, keeps a
+    // two-stage pass (the longer one spills) and rescales every other pass.
     // The last pass's final dequant and load are unconditional (stage S does
     // not exist: its dequant writes LDS buffer 0 and scale slot (S/4) & 1,
     // which nothing reads any more, and the load re-reads stage S - 1): a
@@ -773,12 +782,15 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(DT == YU
         }
     } else {
         for (uint32_t s = 0; s < S; s += 2) {
+            if constexpr (RS)
+                if ((s & 3u) == 0u) rescale((s >> 2) & 1u);   // stage s opens a super-block
             compute(0, cont);
             dequant_stage(s + 1, R1, 1, rt);
             load_stage(s + 3 < S ? s + 3 : S - 1, R1, rt);
             __syncthreads();
             compute(1, cont);
-            if (((s + 1) & 3u) == 3u) block_done((s + 1) >> 2);
+            if constexpr (!RS)
+                if (((s + 1) & 3u) == 3u) block_done((s + 1) >> 2);
             dequant_stage(s + 2, R0, 0, rt);
             load_stage(s + 4 < S ? s + 4 : S - 1, R0, rt);
             __syncthreads();
@@ -971,7 +983,7 @@ uint32_t gemm_bm(uint32_t m, bool f32x, uint32_t dtype, uint32_t bn) {
 }
 
 // Workgroups resident per CU: one for the 256-wide tiles and for Q6_K's
-// 128-row and two-sweep kernels (their registers), two otherwise.
+// 128-row and two-sweep kernels (one wave per SIMD), two otherwise.
 uint32_t gemm_wgs_per_cu(uint32_t dtype, uint32_t bm, uint32_t bn, bool f32x) {
     return bn == 256 || (dtype == YULE_DTYPE_Q6_K && (bm == 128 || f32x)) ? 1u : 2u;
 }
