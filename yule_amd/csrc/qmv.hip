@@ -128,7 +128,11 @@ struct RawPair {
 // PAIR: segments 0 and 1 are the gate and up matrices (equal row counts);
 // a team computes row r of both and stores silu(g)*u into segment 0's
 // output (model_runner.rs:963-972), so SwiGLU costs nothing extra.
-template <class F, int W, int D, int NT, bool PAIR, bool TWO>
+// PLAIN: no input transform and the plain store epilogue (quantized_matmul
+// itself): the kernel then has no residual load of y, whose wait would order
+// behind the next row's prefetch (loads complete in issue order), so the
+// compiler's wait before each row covers that row's loads only.
+template <class F, int W, int D, int NT, bool PAIR, bool TWO, bool PLAIN = false>
 __global__ __launch_bounds__(NT) void qmv_stream_kernel(const uint8_t *vb0, const uint8_t *vb1, const uint8_t *vb2,
                                                         const float *__restrict__ x, uint32_t st1, uint32_t st2,
                                                         uint32_t n_rows, uint32_t bpr_pf,
@@ -211,9 +215,9 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const uint8_t *vb0, cons
         float *yb = sg.y[0];
 #pragma unroll
         for (int i = 1; i < kStreamSegs; i++) yb = s == (uint32_t)i ? sg.y[i] - stv[i] : yb;
-        if (xf.epi == kEpiAdd) v = yb[row] + v;   // residual + projection (model_runner.rs:782-784)
+        if (!PLAIN && xf.epi == kEpiAdd) v = yb[row] + v;   // residual + projection (model_runner.rs:782-784)
         yb[row] = v;
-        if (xf.epi == kEpiArgmax) {
+        if (!PLAIN && xf.epi == kEpiArgmax) {
             const unsigned long long key = argmax_pack(v, row);
             best = key > best ? key : best;
         }
@@ -332,10 +336,22 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const uint8_t *vb0, cons
             }
         } else if (WPT == 1) {
             const uint32_t row = uni(rbase + team);
-            if (t == 0 && row < n_rows) store(row, acc);
+            if constexpr (PLAIN) {
+                // every lane of the team stores (the same value, one address),
+                // and a team past the last row stores the last row again: its
+                // clamped fetch computed that row, so the value is identical.
+                // No branch around the store, so the compiler's wait before
+                // the next row counts the memory operations exactly.
+                store(row < n_rows ? row : n_rows - 1, acc);
+            } else if (t == 0 && row < n_rows) {
+                store(row, acc);
+            }
         } else {
             if ((tid & 63) == 0) ring[it & 15][tid >> 6] = acc;
-            if ((it & 7) == 7 || last) {
+            // (PLAIN: at most 16 row iterations per team, checked on the host;
+            // the ring is flushed once after the loop, so the loop holds no
+            // barrier and no global store)
+            if (!PLAIN && ((it & 7) == 7 || last)) {
                 __syncthreads();
                 const uint32_t first = it & ~7u;
                 if (tid < 8 * RI) {
@@ -360,7 +376,9 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const uint8_t *vb0, cons
             const uint32_t r = base + j * stride;
             if (r >= n_rows) break;
             const uint32_t rn = r + (D - 1) * stride;
-            if (rn < n_rows) buf[(j + D - 1) % D] = fetch(rn);
+            // (PLAIN: unconditional, rows past the end re-read the last row, so
+            // that no branch merges before the next row's wait)
+            if (PLAIN || rn < n_rows) buf[(j + D - 1) % D] = fetch(rn);
             if constexpr (PAIR) {
                 float g = F::dot(buf[j].g, sub, xs, aux), u = F::dot(buf[j].u, sub, xs, aux);
                 g = team_sum<W>(active ? g : 0.f);
@@ -374,7 +392,20 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const uint8_t *vb0, cons
             }
         }
     }
-    if (xf.epi == kEpiArgmax) {   // uniform: the workgroup's best row into its own slot
+    if constexpr (PLAIN && WPT > 1) {   // the ring's iterations 0 .. it - 1 (it <= 16)
+        __syncthreads();
+        if (tid < 16 * RI) {
+            const uint32_t iter = tid / RI, tm = tid % RI;
+            const uint32_t row = r0 + iter * stride + tm;
+            if (iter < it && row < n_rows) {
+                float s = 0.f;
+#pragma unroll
+                for (uint32_t i = 0; i < WPT; i++) s += ring[iter][tm * WPT + i];
+                store(row, s);
+            }
+        }
+    }
+    if (!PLAIN && xf.epi == kEpiArgmax) {   // uniform: the workgroup's best row into its own slot
         __shared__ unsigned long long wbest[NWV];
 #pragma unroll
         for (int off = 32; off >= 1; off >>= 1) {
@@ -410,8 +441,14 @@ static void launch_stream_d(hipStream_t s, const Segs &sg, const float *x, uint3
             return;
         }
     }
+    // YULE_QMV_PLAIN=0: the plain launches take the general kernel (comparison)
+    static const bool plain_on = env_flag("YULE_QMV_PLAIN", true);
     if (xf.mode != kXfNone)
         hipLaunchKernelGGL((qmv_stream_kernel<F, W, D, NT, false, true>), dim3(blocks), dim3(NT), lds, s,
+                           YULE_QMV_ARGS);
+    else if (xf.epi == kEpiStore && !xf.pf_wgs && plain_on &&
+             (W <= 64 || (n_rows + (size_t)blocks * (NT / W) - 1) / ((size_t)blocks * (NT / W)) <= 16))
+        hipLaunchKernelGGL((qmv_stream_kernel<F, W, D, NT, false, false, true>), dim3(blocks), dim3(NT), lds, s,
                            YULE_QMV_ARGS);
     else
         hipLaunchKernelGGL((qmv_stream_kernel<F, W, D, NT, false, false>), dim3(blocks), dim3(NT), lds, s,
