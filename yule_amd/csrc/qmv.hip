@@ -128,11 +128,20 @@ struct RawPair {
 // PAIR: segments 0 and 1 are the gate and up matrices (equal row counts);
 // a team computes row r of both and stores silu(g)*u into segment 0's
 // output (model_runner.rs:963-972), so SwiGLU costs nothing extra.
-// PLAIN: no input transform and the plain store epilogue (quantized_matmul
-// itself): the kernel then has no residual load of y, whose wait would order
-// behind the next row's prefetch (loads complete in issue order), so the
-// compiler's wait before each row covers that row's loads only.
-template <class F, int W, int D, int NT, bool PAIR, bool TWO, bool PLAIN = false>
+// EXACT: the row loop holds no branch around a memory operation, so the
+// compiler's wait before each row covers that row's loads only (with a
+// branch it waits for every load in flight, the next row's prefetch
+// included: loads complete in issue order).  The next row's fetch is
+// unconditional (rows past the end re-read the last row); a one-wave team
+// stores with every lane (the same value to one address; a team past the
+// last row stores that row's value again); teams wider than a wave flush
+// their LDS ring once after the loop, where the residual of kEpiAdd is
+// loaded too.  The host picks it for one-wave-or-narrower teams without an
+// input transform and with the store epilogue (decode's narrow fused
+// launches measured slower in this form: Q/K/V with RoPE 4.61 -> 4.96 us,
+// paired gate/up 5.78 -> 5.92, O + residual 3.27 -> 3.38), and for wider
+// teams with at most 16 row iterations each.
+template <class F, int W, int D, int NT, bool PAIR, bool TWO, bool EXACT = false>
 __global__ __launch_bounds__(NT) void qmv_stream_kernel(const uint8_t *vb0, const uint8_t *vb1, const uint8_t *vb2,
                                                         const float *__restrict__ x, uint32_t st1, uint32_t st2,
                                                         uint32_t n_rows, uint32_t bpr_pf,
@@ -215,9 +224,11 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const uint8_t *vb0, cons
         float *yb = sg.y[0];
 #pragma unroll
         for (int i = 1; i < kStreamSegs; i++) yb = s == (uint32_t)i ? sg.y[i] - stv[i] : yb;
-        if (!PLAIN && xf.epi == kEpiAdd) v = yb[row] + v;   // residual + projection (model_runner.rs:782-784)
+        // (the one-wave EXACT kernels run the store epilogue only: no branch)
+        constexpr bool STORE_ONLY = EXACT && WPT == 1;
+        if (!STORE_ONLY && xf.epi == kEpiAdd) v = yb[row] + v;   // residual + projection (model_runner.rs:782-784)
         yb[row] = v;
-        if (!PLAIN && xf.epi == kEpiArgmax) {
+        if (!STORE_ONLY && xf.epi == kEpiArgmax) {
             const unsigned long long key = argmax_pack(v, row);
             best = key > best ? key : best;
         }
@@ -256,7 +267,7 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const uint8_t *vb0, cons
         }
 #pragma unroll
         for (int j = 0; j < D - 1; j++)
-            if (r0 + j * stride < n_rows) buf[j] = fetch(r0 + j * stride);
+            if (EXACT || r0 + j * stride < n_rows) buf[j] = fetch(r0 + j * stride);
         // nothing below (the RoPE block's argument loads and their wait)
         // is scheduled ahead of the first rows' weight loads
         __builtin_amdgcn_sched_barrier(0);
@@ -336,22 +347,21 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const uint8_t *vb0, cons
             }
         } else if (WPT == 1) {
             const uint32_t row = uni(rbase + team);
-            if constexpr (PLAIN) {
-                // every lane of the team stores (the same value, one address),
-                // and a team past the last row stores the last row again: its
-                // clamped fetch computed that row, so the value is identical.
-                // No branch around the store, so the compiler's wait before
-                // the next row counts the memory operations exactly.
+            if constexpr (EXACT) {
+                // every lane of the team stores (the same value, one address);
+                // a team past the last row (store epilogue only) stores the
+                // last row again: its clamped fetch computed that row, so the
+                // value is identical
                 store(row < n_rows ? row : n_rows - 1, acc);
             } else if (t == 0 && row < n_rows) {
                 store(row, acc);
             }
         } else {
             if ((tid & 63) == 0) ring[it & 15][tid >> 6] = acc;
-            // (PLAIN: at most 16 row iterations per team, checked on the host;
+            // (EXACT: at most 16 row iterations per team, checked on the host;
             // the ring is flushed once after the loop, so the loop holds no
             // barrier and no global store)
-            if (!PLAIN && ((it & 7) == 7 || last)) {
+            if (!EXACT && ((it & 7) == 7 || last)) {
                 __syncthreads();
                 const uint32_t first = it & ~7u;
                 if (tid < 8 * RI) {
@@ -376,9 +386,9 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const uint8_t *vb0, cons
             const uint32_t r = base + j * stride;
             if (r >= n_rows) break;
             const uint32_t rn = r + (D - 1) * stride;
-            // (PLAIN: unconditional, rows past the end re-read the last row, so
+            // (EXACT: unconditional, rows past the end re-read the last row, so
             // that no branch merges before the next row's wait)
-            if (PLAIN || rn < n_rows) buf[(j + D - 1) % D] = fetch(rn);
+            if (EXACT || rn < n_rows) buf[(j + D - 1) % D] = fetch(rn);
             if constexpr (PAIR) {
                 float g = F::dot(buf[j].g, sub, xs, aux), u = F::dot(buf[j].u, sub, xs, aux);
                 g = team_sum<W>(active ? g : 0.f);
@@ -392,7 +402,7 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const uint8_t *vb0, cons
             }
         }
     }
-    if constexpr (PLAIN && WPT > 1) {   // the ring's iterations 0 .. it - 1 (it <= 16)
+    if constexpr (EXACT && WPT > 1) {   // the ring's iterations 0 .. it - 1 (it <= 16)
         __syncthreads();
         if (tid < 16 * RI) {
             const uint32_t iter = tid / RI, tm = tid % RI;
@@ -405,7 +415,7 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const uint8_t *vb0, cons
             }
         }
     }
-    if (!PLAIN && xf.epi == kEpiArgmax) {   // uniform: the workgroup's best row into its own slot
+    if (!(EXACT && WPT == 1) && xf.epi == kEpiArgmax) {   // uniform: the workgroup's best row into its own slot
         __shared__ unsigned long long wbest[NWV];
 #pragma unroll
         for (int off = 32; off >= 1; off >>= 1) {
@@ -432,8 +442,24 @@ static void launch_stream_d(hipStream_t s, const Segs &sg, const float *x, uint3
     const uint32_t n_rows = xf.pair ? sg.start[1] : sg.total;
     const uint32_t *rope_ctl = xf.epi == kEpiRope ? xf.ctl : nullptr;
     const uint32_t bpr_pf = bpr | blocks << 16;
+    // EXACT kernel (see qmv_stream_kernel) when every computed row is real or
+    // a duplicate that stores the same value, and wide teams' rings hold all
+    // their row iterations; YULE_QMV_EXACT=0 turns it off (comparison)
+    static const bool exact_on = env_flag("YULE_QMV_EXACT", true);
+    constexpr uint32_t RI = NT / W;
+    const uint64_t iters = (n_rows + (uint64_t)blocks * RI - 1) / ((uint64_t)blocks * RI);
+    const bool exact = exact_on && (W > 64 ? iters <= 16 : xf.mode == kXfNone && xf.epi == kEpiStore);
     blocks += xf.pf_wgs;
 #define YULE_QMV_ARGS vb[0], vb[1], vb[2], x, sg.start[1], sg.start[2], n_rows, bpr_pf, rope_ctl, sg, xf
+#define YULE_QMV_LAUNCH(P, T)                                                                                        \
+    do {                                                                                                             \
+        if (exact)                                                                                                   \
+            hipLaunchKernelGGL((qmv_stream_kernel<F, W, D, NT, P, T, true>), dim3(blocks), dim3(NT), lds, s,         \
+                               YULE_QMV_ARGS);                                                                       \
+        else                                                                                                         \
+            hipLaunchKernelGGL((qmv_stream_kernel<F, W, D, NT, P, T, false>), dim3(blocks), dim3(NT), lds, s,        \
+                               YULE_QMV_ARGS);                                                                       \
+    } while (0)
     if constexpr (W <= 64) {
         if (xf.pair) {   // always with a transform (checked by launch_qmv_fused)
             hipLaunchKernelGGL((qmv_stream_kernel<F, W, D, NT, true, true>), dim3(blocks), dim3(NT), lds, s,
@@ -441,18 +467,15 @@ static void launch_stream_d(hipStream_t s, const Segs &sg, const float *x, uint3
             return;
         }
     }
-    // YULE_QMV_PLAIN=0: the plain launches take the general kernel (comparison)
-    static const bool plain_on = env_flag("YULE_QMV_PLAIN", true);
-    if (xf.mode != kXfNone)
-        hipLaunchKernelGGL((qmv_stream_kernel<F, W, D, NT, false, true>), dim3(blocks), dim3(NT), lds, s,
-                           YULE_QMV_ARGS);
-    else if (xf.epi == kEpiStore && !xf.pf_wgs && plain_on &&
-             (W <= 64 || (n_rows + (size_t)blocks * (NT / W) - 1) / ((size_t)blocks * (NT / W)) <= 16))
-        hipLaunchKernelGGL((qmv_stream_kernel<F, W, D, NT, false, false, true>), dim3(blocks), dim3(NT), lds, s,
-                           YULE_QMV_ARGS);
-    else
-        hipLaunchKernelGGL((qmv_stream_kernel<F, W, D, NT, false, false>), dim3(blocks), dim3(NT), lds, s,
-                           YULE_QMV_ARGS);
+    if (xf.mode != kXfNone) {
+        if constexpr (W > 64) YULE_QMV_LAUNCH(false, true);
+        else
+            hipLaunchKernelGGL((qmv_stream_kernel<F, W, D, NT, false, true>), dim3(blocks), dim3(NT), lds, s,
+                               YULE_QMV_ARGS);
+    } else {
+        YULE_QMV_LAUNCH(false, false);
+    }
+#undef YULE_QMV_LAUNCH
 #undef YULE_QMV_ARGS
 }
 
