@@ -104,6 +104,25 @@ def test_gemm_wide_tiles(hip, dt, M, N, K):
         hip.free(h)
 
 
+@pytest.mark.parametrize("M,N,K", [(1, 77, 1024), (5, 300, 3072), (16, 64, 2048), (17, 129, 1024),
+                                   (32, 200, 3072), (32, 1000, 2048), (8, 4096, 5120), (3, 2000, 14336),
+                                   (33, 1000, 2048)])
+def test_gemm_few_rows(hip, M, N, K):
+    """Q4_K, M <= 32 and K / 256 a multiple of 4: the streaming kernel for
+    few X rows (one or two 16-row X tiles; ragged N and M; K splits of one,
+    two, five and fourteen super-block groups), every row vs the oracle;
+    M = 33 is the tile kernel's again."""
+    dt = DType.Q4_K
+    say(f"[gemm] few rows Q4_K M={M} N={N} K={K}")
+    w = synth.gen_quant(dt, 110 + M, N, K)
+    xb = bf16_bits(synth.gauss(111 + K, (M, K)))
+    y = run_gemm(hip, dt, w, xb, M, N, K)
+    xf = bf16_to_f32(xb).reshape(M, K)
+    for m in range(M):
+        ref = oracle.qmv_f64(int(dt), w, xf[m], N, K)
+        assert np.max(np.abs(y[m] - ref)) <= tolerance_bar(ref), f"row {m}"
+
+
 @pytest.mark.parametrize("N,K", [(14336, 4096), (4096, 14336)])
 def test_gemm_config_shapes_m2048(hip, N, K):
     """BASELINE configs[3] at M=2048, on the 256 x 256 tiles (128 x 64 per

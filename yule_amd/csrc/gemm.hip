@@ -51,6 +51,7 @@ namespace yule {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // Tiling: a workgroup of 2*BN threads computes a BM (m) x BN (r) tile, BN
 // 128 or 256; its waves, two along m and BN/64 along r, each a BM/2 x 64
@@ -923,6 +924,262 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(gemm_wav
         }
 }
 
+// Q4_K with bf16 X for few rows of X (M <= 32): the weights stream once
+// from memory straight into MFMA operands, no LDS round trip, so the launch
+// runs at the weight stream's pace instead of the tile kernels' per-stage
+// barrier/dequant/MFMA chain.  A workgroup takes 128 weight rows over a
+// K range (blockIdx.y of gridDim.y equal ranges, partials summed by the
+// split-K reduction) with four compute waves, 32 rows each as two MFMA A
+// tiles: A = the weights (one row per lane group of 16, the quarter-block
+// 32q..32q+31 bytes of qs per lane quad q), B = X rows 16t..16t+15 (MT
+// tiles of 16), each B fragment read from LDS once for both A tiles: per
+// super-block a wave then reads as many LDS bytes (MT x 8 KB) as its MFMAs
+// take cycles at the CU's LDS rate, where one A tile per wave would leave
+// the MFMAs waiting on LDS half the time.  In a k-step j (h = j / 4,
+// u = j % 4) quad q supplies the weights 64q + 32h + 8u + {0,2,1,3,4,6,5,7}
+// (the nibble-pair order of two qs dwords, h the nibble half), and the f16 X
+// pre-pass stores each four k in that order, so a lane's X operand is one
+// 16-byte piece of a row.  Each super-block's product (sc*q*2^-14 exact
+// integers times f16 X) accumulates in f32 and is added times d*2^14, as in
+// gemm_kernel; the min term is the same hi/lo MFMA product over the X
+// sub-block sums, four super-blocks (one per quad) per MFMA.
+// A fifth wave only copies into LDS: X into a ring of XB buffers (XB - 1
+// super-blocks ahead) and, per group of four super-blocks, the X sub-block
+// sums into one of NSB buffers (global_load_lds).  A wave's loads complete
+// in issue order, so copies issued by the compute waves would hold each
+// weight load behind them and cap the weight stream at the X ring's depth;
+// alone in their waves the weight loads run D super-blocks ahead (D a
+// multiple of 4 that divides the range's super-block count), and the min
+// term's weight header is the ring's (each quad keeps the header of its
+// super-block of the group).  One barrier per super-block for all five waves.
+template <int MT, int D, int XB>
+__global__ __launch_bounds__(320) __attribute__((amdgpu_waves_per_eu(1, 2))) void gemm_q4k_skinny_kernel(
+    const _Float16 *__restrict__ xh, const uint8_t *w0, const uint8_t *w1, const uint8_t *w2, uint32_t s1,
+    uint32_t s2, uint32_t M, uint32_t N, uint32_t K, float *__restrict__ y, const _Float16 *__restrict__ xs_hi,
+    const _Float16 *__restrict__ xs_lo, const float *__restrict__ rowscale, uint32_t accumulate) {
+    static_assert(D % 4 == 0, "weight ring a whole number of min-term groups");
+    typedef __attribute__((address_space(3))) void *lds_p;
+    typedef __attribute__((address_space(1))) void *glb_p;
+    constexpr int RT = 2;                      // A tiles (16 weight rows each) per compute wave
+    constexpr uint32_t BB = 144, XROWS = 16 * MT;
+    constexpr uint32_t XP = XROWS * 32 / 64;   // X pieces (16 bytes) per producer lane per super-block
+    constexpr uint32_t SP = XROWS * 8 / 64;    // sub-block-sum pieces per producer lane per group
+    static_assert(XB >= 3, "X ring: at least 3 buffers");
+    // sums buffers: a group's copy goes out with its first super-block's, up
+    // to XB - 1 super-blocks before it is read, so while up to XB / 4 + 1
+    // other groups' buffers are still to be read
+    constexpr uint32_t NSB = XB <= 4 ? 2 : 4;
+    __shared__ __align__(16) _Float16 xbuf[XB][XROWS * 256];
+    __shared__ __align__(16) _Float16 sbuf[NSB][2 * XROWS * 32];   // [group % NSB][hi rows | lo rows][32 sums]
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t nsub = K / 32, bpr = K / 256;
+    const uint32_t S = bpr / gridDim.y, kb0 = blockIdx.y * S;   // this workgroup's super-blocks [kb0, kb0 + S)
+
+    if (wave == 4) {
+        // producer.  X: slot idx = lane + 64 i of a buffer is row idx / 32,
+        // 16-byte piece p = idx % 32, holding X piece p ^ (row & 7) of that
+        // row.  Sums: slot idx is part idx / (4 XROWS) (hi, lo), row
+        // (idx / 4) % XROWS, piece idx % 4 of the group's 32 sums.
+        uint32_t xoff[XP];
+#pragma unroll
+        for (uint32_t i = 0; i < XP; i++) {
+            const uint32_t idx = lane + 64u * i, row = idx >> 5, c = (idx & 31u) ^ (row & 7u);
+            xoff[i] = (row < M ? row : M - 1u) * K + 8u * c;
+        }
+        auto dma = [&](uint32_t sb) {
+            _Float16 *dst = xbuf[sb % XB];
+#pragma unroll
+            for (uint32_t i = 0; i < XP; i++)
+                __builtin_amdgcn_global_load_lds((glb_p)(xh + (kb0 + sb) * 256u + xoff[i]), (lds_p)(dst + 64u * i * 8u),
+                                                 16, 0, 0);
+            if ((sb & 3u) == 0) {
+                _Float16 *sd = sbuf[(sb >> 2) % NSB];
+#pragma unroll
+                for (uint32_t i = 0; i < SP; i++) {
+                    const uint32_t idx = lane + 64u * i, part = idx / (4u * XROWS), row = (idx >> 2) % XROWS;
+                    const _Float16 *src = (part ? xs_lo : xs_hi) + (size_t)(row < M ? row : M - 1u) * nsub +
+                                          (kb0 + sb) * 8u + 8u * (idx & 3u);
+                    __builtin_amdgcn_global_load_lds((glb_p)src, (lds_p)(sd + 64u * i * 8u), 16, 0, 0);
+                }
+            }
+        };
+        // before super-block sb's barrier: its copies landed; the XB - 2
+        // later super-blocks' copies (at least (XB - 2) XP operations) may be
+        // in flight
+        constexpr uint32_t VM = (XB - 2) * XP < 63u ? (XB - 2) * XP : 63u;
+        constexpr int WAIT = (int)((VM & 15u) | ((VM >> 4) << 14) | (7u << 4) | (15u << 8));
+        for (uint32_t i = 0; i < XB - 1; i++) dma(i < S ? i : S - 1u);
+        for (uint32_t sb = 0; sb < S; sb++) {
+            __builtin_amdgcn_s_waitcnt(WAIT);
+            asm volatile("s_barrier" ::: "memory");
+            // the X buffer of sb + XB - 1 was last read at sb - 1 and the
+            // sums buffer of its group (when it opens one) at sb - 2 or
+            // earlier, by every compute wave before this barrier; past the
+            // end, a copy of the last super-block (never a group's first) into
+            // an unread buffer keeps the count fixed
+            dma(sb + XB - 1 < S ? sb + XB - 1 : S - 1u);
+        }
+        __builtin_amdgcn_s_waitcnt((int)(0u | (7u << 4) | (15u << 8)));   // vmcnt(0): no copy left in flight
+        return;
+    }
+
+    const uint32_t q = lane >> 4, rl = lane & 15u;
+    const size_t row_bytes = (size_t)bpr * BB;
+    const uint32_t rbase = blockIdx.x * (64u * RT) + wave * (16u * RT);
+    const uint8_t *wrow[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) {
+        const uint32_t r = rbase + 16u * rt + rl, rr = r < N ? r : N - 1u;   // this lane's weight rows (clamped)
+        const uint32_t seg = rr >= s2 ? 2u : rr >= s1 ? 1u : 0u;
+        wrow[rt] = (seg == 2 ? w2 : seg == 1 ? w1 : w0) + (size_t)(rr - (seg == 2 ? s2 : seg == 1 ? s1 : 0u)) * row_bytes +
+                   (size_t)kb0 * BB;
+    }
+
+    struct WR { uint4 h, qa, qb; };
+    WR ring[D][RT];
+    auto load_w = [&](uint32_t sb, WR *R) {
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) {
+            const uint8_t *blk = wrow[rt] + (size_t)sb * BB;
+            R[rt].h = *reinterpret_cast<const uint4 *>(blk);
+            R[rt].qa = *reinterpret_cast<const uint4 *>(blk + 16u + 32u * q);
+            R[rt].qb = *reinterpret_cast<const uint4 *>(blk + 32u + 32u * q);
+        }
+    };
+
+    floatx4 acc[RT][MT];
+    uint4 hm[RT];   // headers of super-block 4g + q of the current group g
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) {
+        hm[rt] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < MT; t++) acc[rt][t] = floatx4{0, 0, 0, 0};
+    }
+
+    auto compute = [&](const WR *R, const _Float16 *xs, uint32_t u) {
+        // 6-bit scales of sub-blocks 2q and 2q+1 (get_scale_min_k4,
+        // dequant.rs:176-190) as f16 multipliers of the masked nibbles
+        const bool low = q < 2u;
+        const uint32_t sh = (q & 1u) << 4;
+        h2v S0[RT], S1[RT];
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) {
+            const uint4 hd = R[rt].h;
+            if (q == (u & 3u)) hm[rt] = hd;
+            const uint32_t A = low ? hd.y : hd.w;
+            const uint32_t scs = ((A >> sh) & (low ? 0x3F3Fu : 0x0F0Fu)) | ((hd.y >> (sh + 2u)) & (low ? 0u : 0x3030u));
+            const _Float16 f0 = (_Float16)(float)((scs & 0xFFu) * 1024u), f1 = (_Float16)(float)((scs >> 8) * 64u);
+            S0[rt] = h2v{f0, f0};
+            S1[rt] = h2v{f1, f1};
+        }
+        floatx4 tmp[RT][MT];
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+            for (int t = 0; t < MT; t++) tmp[rt][t] = floatx4{0, 0, 0, 0};
+#pragma unroll
+        for (uint32_t j = 0; j < 8; j++) {
+            const uint32_t h = j >> 2, uu = j & 3u;
+            const uint32_t mask = h ? 0x00F000F0u : 0x000F000Fu;
+            half8 a[RT];
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++) {
+                const h2v Sc = h ? S1[rt] : S0[rt];
+                const uint4 &qv = uu < 2 ? R[rt].qa : R[rt].qb;
+                const uint32_t v0 = (uu & 1u) ? qv.z : qv.x, v1 = (uu & 1u) ? qv.w : qv.y;
+                const u32x4 av = {pk_scale(v0 & mask, Sc), pk_scale((v0 >> 8) & mask, Sc), pk_scale(v1 & mask, Sc),
+                                  pk_scale((v1 >> 8) & mask, Sc)};
+                a[rt] = __builtin_bit_cast(half8, av);
+            }
+            const uint32_t c = 8u * q + 4u * h + uu;
+#pragma unroll
+            for (int t = 0; t < MT; t++) {
+                const uint32_t m = 16u * t + rl;
+                const half8 b = *reinterpret_cast<const half8 *>(xs + m * 256u + 8u * (c ^ (m & 7u)));
+#pragma unroll
+                for (int rt = 0; rt < RT; rt++)
+                    tmp[rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[rt], b, tmp[rt][t], 0, 0, 0);
+            }
+        }
+        // d of the output rows 4q + e of each A tile (their lanes' headers, quad 0)
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) {
+            float dd[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                dd[e] = f16_bits((uint32_t)__builtin_amdgcn_ds_bpermute((int)((4u * q + e) * 4u), (int)R[rt].h.x)) *
+                        16384.0f;
+#pragma unroll
+            for (int t = 0; t < MT; t++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc[rt][t][e] += dd[e] * tmp[rt][t][e];
+        }
+    };
+    auto min_term = [&](const _Float16 *sums) {
+        // -(dmin * mn) of this lane's super-block 4g + q, split hi + lo f16
+        half8 ah[RT], al[RT];
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) {
+            const float dmin = f16_bits(hm[rt].x >> 16);
+            const uint32_t hdw[3] = {hm[rt].y, hm[rt].z, hm[rt].w};
+            const uint8_t *qb = reinterpret_cast<const uint8_t *>(hdw);
+#pragma unroll
+            for (int sbi = 0; sbi < 8; sbi++) {
+                const uint32_t mn = sbi < 4 ? (qb[sbi + 4] & 63u) : ((uint32_t)(qb[sbi + 4] >> 4) | ((uint32_t)(qb[sbi] >> 6) << 4));
+                const float v = -(dmin * (float)mn);
+                const _Float16 vh = (_Float16)v;
+                ah[rt][sbi] = vh;
+                al[rt][sbi] = (_Float16)(v - (float)vh);
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+            const uint32_t m = 16u * t + rl;
+            const half8 bh = *reinterpret_cast<const half8 *>(sums + m * 32u + 8u * q);
+            const half8 bl = *reinterpret_cast<const half8 *>(sums + (XROWS + m) * 32u + 8u * q);
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++) {
+                acc[rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[rt], bh, acc[rt][t], 0, 0, 0);
+                acc[rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[rt], bl, acc[rt][t], 0, 0, 0);
+                acc[rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[rt], bh, acc[rt][t], 0, 0, 0);
+            }
+        }
+    };
+
+#pragma unroll
+    for (int u = 0; u < D; u++) load_w(u, ring[u]);
+    for (uint32_t sb0 = 0; sb0 < S; sb0 += D) {
+#pragma unroll
+        for (uint32_t u = 0; u < (uint32_t)D; u++) {
+            const uint32_t sb = sb0 + u;
+            asm volatile("s_barrier" ::: "memory");   // X(sb) (and its group's sums) in their buffers
+            compute(ring[u], xbuf[sb % XB], u);
+            load_w(sb + D < S ? sb + D : S - 1u, ring[u]);
+            if ((u & 3u) == 3u) min_term(sbuf[(sb >> 2) % NSB]);
+        }
+    }
+
+    // split z's partial into its own Y block (the split-K reduction sums them)
+    float *const ys = y + (gridDim.y > 1 ? (size_t)blockIdx.y * M * N : 0);
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
+        const uint32_t m = 16u * t + rl;
+        if (m >= M) continue;
+        const float rs = rowscale[m];
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const uint32_t r = rbase + 16u * rt + 4u * q + e;
+                if (r < N) {
+                    const float v = acc[rt][t][e] * rs;   // the row's power of two back out: exact
+                    if (accumulate && gridDim.y == 1) ys[(size_t)m * N + r] += v;
+                    else ys[(size_t)m * N + r] = v;
+                }
+            }
+    }
+}
+
 // zeroes the y blocks of tiles [first, first + gridDim.x / (bm / 8)): one
 // workgroup per 8 rows of a tile, 32 lanes per row storing consecutive
 // floats (bm is 64 or 128, bn 128 or 256)
@@ -999,6 +1256,28 @@ uint32_t gemm_splits(uint32_t m, uint32_t n, uint32_t k, uint32_t bn, uint32_t b
     return ks < 1 ? 1 : ks > bpr ? bpr : ks;
 }
 
+// Q4_K with bf16 X and M <= 32 runs gemm_q4k_skinny_kernel (no tail; its
+// own K splits) when each row's super-block count is a multiple of 4: 14-24%
+// faster per call than the tile kernel at M = 1..16 on 14336x4096,
+// 4096x14336 and 4096x4096, 9-13% at M = 32 (equal on 1024x4096).  At
+// M = 64 it loses or ties (its waves, one per SIMD, serialize dequant, MFMA
+// chain and four times the X bytes from LDS).  YULE_GEMM_SKINNY=0 turns it off.
+bool gemm_skinny(uint32_t m, uint32_t k, uint32_t dtype, bool f32x) {
+    static const bool env = env_flag("YULE_GEMM_SKINNY", true);
+    return env && !f32x && dtype == YULE_DTYPE_Q4_K && m <= 32 && (k / 256) % 4 == 0;
+}
+
+// K splits of the few-rows kernel: as many as keep its 128-row workgroups
+// (one per CU) within one round, each split a whole number of four-super-
+// block groups.
+uint32_t gemm_skinny_splits(uint32_t n, uint32_t k) {
+    const uint32_t wgs = (n + 127) / 128, groups = k / 1024, cus = (uint32_t)device_cus();
+    uint32_t best = 1;
+    for (uint32_t d = 2; d <= groups; d++)
+        if (groups % d == 0 && wgs * d <= cus) best = d;
+    return best;
+}
+
 // Tail tiles split in two K halves (zero: none).  Without splits, the tiles
 // past the last whole round of resident workgroups (one 256-wide or two
 // 128-wide per CU) form a partial round nearly as long as a full one (a
@@ -1072,6 +1351,20 @@ int launch_gemm_dt(hipStream_t s, uint32_t dtype, const GemmPass &p) {
     return check_launch("quantized_gemm");
 }
 
+template <int MT>
+void launch_skinny_mt(hipStream_t s, const GemmPass &p) {
+    const dim3 grid((p.n + 127) / 128, p.ks);
+    constexpr int XB = 8;   // X ring: MT x 8 KB per buffer
+    hipLaunchKernelGGL((gemm_q4k_skinny_kernel<MT, 4, XB>), grid, dim3(320), 0, s, p.xh, p.w.w[0], p.w.w[1], p.w.w[2],
+                       p.w.s1, p.w.s2, p.m, p.n, p.k, p.y, p.xs_hi, p.xs_lo, p.rowscale, p.accumulate);
+}
+
+int launch_gemm_skinny(hipStream_t s, const GemmPass &p) {
+    if (p.m <= 16) launch_skinny_mt<1>(s, p);
+    else launch_skinny_mt<2>(s, p);
+    return check_launch("quantized_gemm (few X rows)");
+}
+
 bool gemm_dtype_ok(uint32_t dtype) {
     return dtype == YULE_DTYPE_Q4_K || dtype == YULE_DTYPE_Q6_K || dtype == YULE_DTYPE_Q8_0 ||
            dtype == YULE_DTYPE_Q4_0 || dtype == YULE_DTYPE_Q5_K || dtype == YULE_DTYPE_Q8_K;
@@ -1086,7 +1379,7 @@ struct GemmWork {
     size_t part_bytes, total;
     size_t n_x, n_sub, n_y;
     uint32_t ks, bn, bm, tail;
-    bool q4;
+    bool q4, skinny;
 };
 
 static GemmWork gemm_work(uint32_t m, uint32_t n_rows, uint32_t n_cols, uint32_t dtype, bool f32x) {
@@ -1094,8 +1387,9 @@ static GemmWork gemm_work(uint32_t m, uint32_t n_rows, uint32_t n_cols, uint32_t
     g.q4 = dtype == YULE_DTYPE_Q4_K || dtype == YULE_DTYPE_Q5_K;   // min term: X sub-block sums
     g.bn = gemm_bn(m, dtype);
     g.bm = gemm_bm(m, f32x, dtype, g.bn);
-    g.ks = gemm_splits(m, n_rows, n_cols, g.bn, g.bm, gemm_wgs_per_cu(dtype, g.bm, g.bn, f32x));
-    g.tail = gemm_tail(m, n_rows, n_cols, g.bn, g.bm, g.ks);
+    g.skinny = gemm_skinny(m, n_cols, dtype, f32x);
+    g.ks = g.skinny ? gemm_skinny_splits(n_rows, n_cols) : gemm_splits(m, n_rows, n_cols, g.bn, g.bm, gemm_wgs_per_cu(dtype, g.bm, g.bn, f32x));
+    g.tail = g.skinny ? 0u : gemm_tail(m, n_rows, n_cols, g.bn, g.bm, g.ks);
     g.n_x = (size_t)m * n_cols;
     g.n_sub = (size_t)m * (n_cols / 32);
     g.n_y = (size_t)m * n_rows;
@@ -1135,7 +1429,7 @@ static int gemm_enqueue(hipStream_t s, const GemmW &w, const void *x, bool f32x,
     if (rc) return rc;
     const GemmPass p{w, xh, xl, xs_hi, xs_lo, rowscale, g.ks > 1 ? part : y, m, n_rows, n_cols, g.ks, g.bn, g.bm,
                      accumulate ? 0u : g.tail, accumulate ? 1u : 0u};
-    if ((rc = launch_gemm_dt(s, dtype, p))) return rc;
+    if ((rc = g.skinny ? launch_gemm_skinny(s, p) : launch_gemm_dt(s, dtype, p))) return rc;
     if (defer) *defer = GemmRed{part, y, g.ks > 1 ? g.ks : 0u, n_rows, m, accumulate};
     if (g.ks > 1 && defer) return YULE_OK;   // summed by the next product's pre-pass
     if (g.ks > 1) {
