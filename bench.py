@@ -586,8 +586,8 @@ def main():
                          "one 64 MiB device copy, for rocprofv3 --pmc runs; prints a JSON line")
     ap.add_argument("--profile-gemm", type=int, default=0, metavar="N",
                     help="only run N calls of the Q4_K 14336x4096 prefill GEMM (for rocprofv3)")
-    ap.add_argument("--gemm-m", type=int, default=2048, choices=(64, 512, 2048),
-                    help="tokens M of the --profile-gemm calls (default 2048)")
+    ap.add_argument("--gemm-m", type=int, default=2048, choices=(1, 16, 32, 64, 512, 2048),
+                    help="tokens M of the --profile-gemm calls (default 2048; M <= 32 runs the few-rows kernel)")
     ap.add_argument("--probe-curve", action="store_true",
                     help="only measure the single-launch streaming-read rate against launch size (JSON line)")
     ap.add_argument("--probe-variants", action="store_true",
@@ -701,6 +701,8 @@ def main():
 
     if not args.quick:
         extra["prefill_gemm_q4k"] = prefill_gemm(hip)
+        # a few X rows (M <= 32: the streaming few-rows kernel)
+        extra["prefill_gemm_q4k_few_rows"] = prefill_gemm(hip, DType.Q4_K, ((14336, 4096), (4096, 14336)), (1, 16, 32))
         extra["prefill_gemm_other_formats"] = {
             dt.name: prefill_gemm(hip, dt, ((14336, 4096),), (512, 2048))
             for dt in (DType.Q4_0, DType.Q5_K, DType.Q6_K, DType.Q8_0, DType.Q8_K)}
