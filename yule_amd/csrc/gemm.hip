@@ -347,7 +347,11 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(gemm_wav
     // load or store covers the eight chunk positions of a 128-byte bank line
     // once, and the 64 x 128 tile keeps three workgroups per CU.
     constexpr int GLD = GSK;
-    __shared__ __align__(16) _Float16 sx[2][BM * GLD];
+    // the two X buffers as two objects: a copy into one (XDMA below) then
+    // does not make the compiler wait before reads of the other
+    __shared__ __align__(16) _Float16 sxa[BM * GLD];
+    __shared__ __align__(16) _Float16 sxb[BM * GLD];
+    auto xbuf = [&](int b) -> _Float16 * { return b ? sxb : sxa; };
     __shared__ __align__(16) _Float16 sw[2][BN * GLD];
     __shared__ float sd[2][B32 ? 2 : 1][BN];   // d per weight row: super-block slot, or the stage's two blocks
     // Q6_K with f32 X: the weight tile holds q - 32 and each row's four
@@ -361,6 +365,10 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(gemm_wav
     __shared__ uint32_t ssc[X6 ? 2 : 1][X6 ? BN : 1][4];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t wm = wave / WNN, wn = wave % WNN;
+    // XDMA (the 256 x 256 Q4_K tile with bf16 X, whose registers are full):
+    // X goes from memory straight into LDS (global_load_lds) one stage
+    // ahead instead of through XCH staging registers per stage in flight
+    constexpr bool XDMA = DT == YULE_DTYPE_Q4_K && BM == 256 && BN == 256 && SWEEPS == 1;
     // Tile of this workgroup.  The grid is one-dimensional over
     // (split, m tile, n tile), n fastest, in id order: workgroups go to the
     // eight XCDs round-robin by id, so the ones resident together at any
@@ -444,11 +452,13 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(gemm_wav
     auto load_stage = [&](uint32_t s, GemmRegs<DT, XCH> &R, auto stc) {
         constexpr int STC = decltype(stc)::value;
         const uint32_t kb = kb_lo + (s >> 2), st = STC >= 0 ? (uint32_t)STC : (s & 3u), k0 = kb * 256u + st * GSK;
+        if constexpr (!XDMA) {
 #pragma unroll
-        for (int i = 0; i < XCH; i++) {
-            const uint32_t idx = tid + NTH * i, row = idx >> 3, c = idx & 7u;
-            const uint32_t m = m0 + row < M ? m0 + row : M - 1u;
-            R.x[i] = *reinterpret_cast<const uint4 *>(xcur + (size_t)m * K + k0 + 8u * c);
+            for (int i = 0; i < XCH; i++) {
+                const uint32_t idx = tid + NTH * i, row = idx >> 3, c = idx & 7u;
+                const uint32_t m = m0 + row < M ? m0 + row : M - 1u;
+                R.x[i] = *reinterpret_cast<const uint4 *>(xcur + (size_t)m * K + k0 + 8u * c);
+            }
         }
         if constexpr (B32) {
             // block 2 (kb*4 + st) + part of the row: k = 64 stage + 32 part
@@ -489,13 +499,15 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(gemm_wav
         constexpr int STC = decltype(stc)::value;
         // kb relative to the split (LDS slot parity only)
         const uint32_t kb = s >> 2, st = STC >= 0 ? (uint32_t)STC : (s & 3u);
+        if constexpr (!XDMA) {
 #pragma unroll
-        for (int i = 0; i < XCH; i++) {
-            const uint32_t idx = tid + NTH * i, row = idx >> 3, c = idx & 7u;
-            // copied element by element: storing R.x[i] whole kept the
-            // register staging in scratch memory (80-450 bytes per lane)
-            const uint4 v = R.x[i];
-            *reinterpret_cast<uint4 *>(sx[b] + swz<Q4>(row, c)) = make_uint4(v.x, v.y, v.z, v.w);
+            for (int i = 0; i < XCH; i++) {
+                const uint32_t idx = tid + NTH * i, row = idx >> 3, c = idx & 7u;
+                // copied element by element: storing R.x[i] whole kept the
+                // register staging in scratch memory (80-450 bytes per lane)
+                const uint4 v = R.x[i];
+                *reinterpret_cast<uint4 *>(xbuf(b) + swz<Q4>(row, c)) = make_uint4(v.x, v.y, v.z, v.w);
+            }
         }
         _Float16 *wt = sw[b];
         uint4 o[4];
@@ -659,7 +671,7 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(gemm_wav
 #pragma unroll
             for (int i = 0; i < TM; i++)
                 a[i] = *reinterpret_cast<const half8 *>(
-                    sx[b] + swz<Q4>(wm * (BM / 2) + i * 16 + (lane & 15u), ks * 4 + (lane >> 4)));
+                    xbuf(b) + swz<Q4>(wm * (BM / 2) + i * 16 + (lane & 15u), ks * 4 + (lane >> 4)));
 #pragma unroll
             for (int j = 0; j < 4; j++)
                 bw[j] = *reinterpret_cast<const half8 *>(sw[b] + swz<Q4>(wn * 64 + j * 16 + (lane & 15u), ks * 4 + (lane >> 4)));
@@ -724,6 +736,51 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(gemm_wav
         }
     };
 
+    // XDMA: stage s's X tile into buffer b.  Slot idx = tid + NTH i of the
+    // buffer (the 1 KB of wave w's copy i are slots 64 w + 512 i onwards) is
+    // row idx / 8, chunk position idx % 8, which swz<true> fills from X chunk
+    // (idx % 8) ^ f(row).
+    // The copy is issued as inline assembly, outside the compiler's memory
+    // model: with the builtin, the compiler could not tell a copy into one
+    // buffer from reads of the other (both live in the kernel's one LDS
+    // block) and waited for every load in flight, the copy just issued
+    // included, before every other stage's MFMAs.  Unseen by the compiler,
+    // the copies only make its own load waits count fewer operations than
+    // are in flight, i.e. stricter; none falls after a stage's copy, since
+    // the stage's weight registers were already covered by the previous
+    // stage's explicit wait, which the compiler does account for.
+    // Scheduling barriers keep the copies first in their stage, ahead of the
+    // weight loads whose count the waits rely on.
+    typedef __attribute__((address_space(3))) _Float16 *lds_h;
+    auto dma_x = [&](uint32_t s, int b) {
+        const uint32_t k0 = (kb_lo + (s >> 2)) * 256u + (s & 3u) * GSK;
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < XCH; i++) {
+            const uint32_t idx = tid + NTH * i, row = idx >> 3, r7 = row & 7u;
+            const uint32_t c = (idx & 7u) ^ ((r7 & 1u) | ((r7 >> 1) & 2u) | ((r7 << 1) & 4u));
+            const uint32_t m = m0 + row < M ? m0 + row : M - 1u;
+            const _Float16 *src = xcur + (size_t)m * K + k0 + 8u * c;
+            const uint32_t dst = __builtin_amdgcn_readfirstlane(
+                (uint32_t)reinterpret_cast<uintptr_t>((lds_h)(xbuf(b) + (64u * wave + NTH * i) * 8u)));
+            asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(dst) : "m0");
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // end of an XDMA stage: this thread's copy of the next stage's X landed
+    // (the stage's two weight loads, issued after it, may stay in flight:
+    // loads complete in issue order, so at most those two are outstanding
+    // once it has; a split weight load only makes the wait stricter), its
+    // LDS stores done, then the barrier.  No __syncthreads: its release
+    // fence waits for every load, the weight loads two stages ahead included.
+    auto stage_sync = [&]() {
+        if constexpr (XDMA) {
+            __builtin_amdgcn_s_waitcnt((int)(2u | (7u << 4)));   // vmcnt(2) lgkmcnt(0)
+            asm volatile("s_barrier" ::: "memory");
+        } else {
+            __syncthreads();
+        }
+    };
     const std::integral_constant<int, -1> rt{};   // stage index known only at run time
     const std::integral_constant<bool, true> opens{};
     const std::integral_constant<bool, false> cont{};
@@ -732,13 +789,21 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(gemm_wav
     auto sweep = [&]() {
     GemmRegs<DT, XCH> R0, R1;
     load_stage(0, R0, std::integral_constant<int, 0>{});
+    if constexpr (XDMA) dma_x(0, 0);
     load_stage(1, R1, std::integral_constant<int, 1>{});
     // argument loads the epilogue needs (y, ...) and their waits stay behind
     // the first two stages' loads
     __builtin_amdgcn_sched_barrier(0);
     dequant_stage(0, R0, 0, std::integral_constant<int, 0>{});
     load_stage(2, R0, std::integral_constant<int, 2>{});   // S >= 4
-    __syncthreads();
+    if constexpr (XDMA) {
+        // X of stage 0 landed (stage 1's and 2's weight loads, four or more
+        // operations, were issued after it)
+        __builtin_amdgcn_s_waitcnt((int)(4u | (7u << 4)));   // vmcnt(4) lgkmcnt(0)
+        asm volatile("s_barrier" ::: "memory");
+    } else {
+        __syncthreads();
+    }
     // Q4_K, Q5_K, Q8_K: one super-block (four stages) per pass; stage t computes out of
     // LDS buffer t & 1 while stage t + 1 is dequantized into the other and
     // the bytes of stage t + 3 load into the register set stage t + 1 freed.
@@ -752,23 +817,30 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(gemm_wav
     // the loop head instead of only for the stage about to be dequantized.
     if constexpr (SBP) {
         for (uint32_t s = 0; s < S; s += 4) {
+            // (XDMA: each stage first copies the next stage's X into the
+            // buffer the previous stage read; past the end, stage S - 1
+            // again, into a buffer nothing reads any more)
+            if constexpr (XDMA) dma_x(s + 1, 1);
             compute(0, opens, (s >> 2) & 1u);
             dequant_stage(s + 1, R1, 1, std::integral_constant<int, 1>{});
             load_stage(s + 3 < S ? s + 3 : S - 1, R1, std::integral_constant<int, 3>{});
-            __syncthreads();
+            stage_sync();
+            if constexpr (XDMA) dma_x(s + 2, 0);
             compute(1, cont);
             dequant_stage(s + 2, R0, 0, std::integral_constant<int, 2>{});
             load_stage(s + 4 < S ? s + 4 : S - 1, R0, std::integral_constant<int, 0>{});
-            __syncthreads();
+            stage_sync();
+            if constexpr (XDMA) dma_x(s + 3, 1);
             compute(0, cont);
             dequant_stage(s + 3, R1, 1, std::integral_constant<int, 3>{});
             load_stage(s + 5 < S ? s + 5 : S - 1, R1, std::integral_constant<int, 1>{});
-            __syncthreads();
+            stage_sync();
+            if constexpr (XDMA) dma_x(s + 4 < S ? s + 4 : S - 1, 0);
             compute(1, cont);
             if constexpr (!RS) block_done(s >> 2);
             dequant_stage(s + 4, R0, 0, std::integral_constant<int, 0>{});
             load_stage(s + 6 < S ? s + 6 : S - 1, R0, std::integral_constant<int, 2>{});
-            __syncthreads();
+            stage_sync();
         }
     } else if constexpr (B32) {
         for (uint32_t s = 0; s < S; s += 2) {
