@@ -136,8 +136,10 @@ struct RawPair {
 // stores with every lane (the same value to one address; a team past the
 // last row stores that row's value again); teams wider than a wave flush
 // their LDS ring once after the loop, where the residual of kEpiAdd is
-// loaded too.  The host picks it for one-wave-or-narrower teams without an
-// input transform and with the store epilogue (decode's narrow fused
+// loaded too; a duplicate last row leaves the argmax unchanged (same value,
+// same row).  The host picks it for one-wave-or-narrower teams without an
+// input transform and with the store epilogue, and for the argmax epilogue
+// behind a transform (the lm_head: several rows per team) (decode's narrow fused
 // launches measured slower in this form: Q/K/V with RoPE 4.61 -> 4.96 us,
 // paired gate/up 5.78 -> 5.92, O + residual 3.27 -> 3.38), and for wider
 // teams with at most 16 row iterations each.
@@ -224,11 +226,13 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const uint8_t *vb0, cons
         float *yb = sg.y[0];
 #pragma unroll
         for (int i = 1; i < kStreamSegs; i++) yb = s == (uint32_t)i ? sg.y[i] - stv[i] : yb;
-        // (the one-wave EXACT kernels run the store epilogue only: no branch)
+        // (the one-wave EXACT kernels run the store epilogue only, and with
+        // an input transform also the argmax one: no load under a branch;
+        // argmax adds register work alone)
         constexpr bool STORE_ONLY = EXACT && WPT == 1;
         if (!STORE_ONLY && xf.epi == kEpiAdd) v = yb[row] + v;   // residual + projection (model_runner.rs:782-784)
         yb[row] = v;
-        if (!STORE_ONLY && xf.epi == kEpiArgmax) {
+        if ((!STORE_ONLY || TWO) && xf.epi == kEpiArgmax) {
             const unsigned long long key = argmax_pack(v, row);
             best = key > best ? key : best;
         }
@@ -328,7 +332,7 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const uint8_t *vb0, cons
     __shared__ float ring[16][NWV];
     auto finish = [&](float acc, uint32_t rbase, uint32_t it, bool last) {
         acc = team_sum<(W < 64 ? W : 64)>(active ? acc : 0.f);
-        if (TWO && W < 64 && xf.epi == kEpiRope) {
+        if (TWO && W < 64 && !EXACT && xf.epi == kEpiRope) {   // (RoPE launches never run EXACT)
             // rows 2i and 2i + 1 of a head are teams 2j and 2j + 1 of one wave
             // (row bases are even): the pair meets across lane W
             const float other = __shfl_xor(acc, W, 64);
@@ -415,7 +419,7 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const uint8_t *vb0, cons
             }
         }
     }
-    if (!(EXACT && WPT == 1) && xf.epi == kEpiArgmax) {   // uniform: the workgroup's best row into its own slot
+    if ((!(EXACT && WPT == 1) || TWO) && xf.epi == kEpiArgmax) {   // uniform: the workgroup's best row into its own slot
         __shared__ unsigned long long wbest[NWV];
 #pragma unroll
         for (int off = 32; off >= 1; off >>= 1) {
@@ -448,7 +452,12 @@ static void launch_stream_d(hipStream_t s, const Segs &sg, const float *x, uint3
     static const bool exact_on = env_flag("YULE_QMV_EXACT", true);
     constexpr uint32_t RI = NT / W;
     const uint64_t iters = (n_rows + (uint64_t)blocks * RI - 1) / ((uint64_t)blocks * RI);
-    const bool exact = exact_on && (W > 64 ? iters <= 16 : xf.mode == kXfNone && xf.epi == kEpiStore);
+    // (narrow teams: the plain store epilogue, and the argmax one behind an
+    // input transform, the lm_head's, whose launches give each team several
+    // rows: decode 1762 -> 1828 tok/s)
+    const bool exact = exact_on && (W > 64 ? iters <= 16
+                                           : (xf.mode == kXfNone && xf.epi == kEpiStore) ||
+                                                 (xf.mode != kXfNone && xf.epi == kEpiArgmax));
     blocks += xf.pf_wgs;
 #define YULE_QMV_ARGS vb[0], vb[1], vb[2], x, sg.start[1], sg.start[2], n_rows, bpr_pf, rope_ctl, sg, xf
 #define YULE_QMV_LAUNCH(P, T)                                                                                        \
@@ -468,10 +477,7 @@ static void launch_stream_d(hipStream_t s, const Segs &sg, const float *x, uint3
         }
     }
     if (xf.mode != kXfNone) {
-        if constexpr (W > 64) YULE_QMV_LAUNCH(false, true);
-        else
-            hipLaunchKernelGGL((qmv_stream_kernel<F, W, D, NT, false, true>), dim3(blocks), dim3(NT), lds, s,
-                               YULE_QMV_ARGS);
+        YULE_QMV_LAUNCH(false, true);
     } else {
         YULE_QMV_LAUNCH(false, false);
     }
