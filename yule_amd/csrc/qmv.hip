@@ -143,7 +143,12 @@ struct RawPair {
 // launches measured slower in this form: Q/K/V with RoPE 4.61 -> 4.96 us,
 // paired gate/up 5.78 -> 5.92, O + residual 3.27 -> 3.38), and for wider
 // teams with at most 16 row iterations each.
-template <class F, int W, int D, int NT, bool PAIR, bool TWO, bool EXACT = false>
+// ADD (with EXACT, one-wave teams, no input transform): the residual-add
+// epilogue with its load of y[row] unconditional; the host picks it only
+// when the rows divide evenly over the workgroups' teams, so that no team
+// computes a duplicate of the last row (two read-modify-writes of one y
+// element would race).
+template <class F, int W, int D, int NT, bool PAIR, bool TWO, bool EXACT = false, bool ADD = false>
 __global__ __launch_bounds__(NT) void qmv_stream_kernel(const uint8_t *vb0, const uint8_t *vb1, const uint8_t *vb2,
                                                         const float *__restrict__ x, uint32_t st1, uint32_t st2,
                                                         uint32_t n_rows, uint32_t bpr_pf,
@@ -230,7 +235,7 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const uint8_t *vb0, cons
         // an input transform also the argmax one: no load under a branch;
         // argmax adds register work alone)
         constexpr bool STORE_ONLY = EXACT && WPT == 1;
-        if (!STORE_ONLY && xf.epi == kEpiAdd) v = yb[row] + v;   // residual + projection (model_runner.rs:782-784)
+        if (ADD || (!STORE_ONLY && xf.epi == kEpiAdd)) v = yb[row] + v;   // residual + projection (model_runner.rs:782-784)
         yb[row] = v;
         if ((!STORE_ONLY || TWO) && xf.epi == kEpiArgmax) {
             const unsigned long long key = argmax_pack(v, row);
@@ -478,6 +483,11 @@ static void launch_stream_d(hipStream_t s, const Segs &sg, const float *x, uint3
     }
     if (xf.mode != kXfNone) {
         YULE_QMV_LAUNCH(false, true);
+    } else if (W <= 64 && exact_on && xf.epi == kEpiAdd && n_rows % ((uint64_t)(blocks - xf.pf_wgs) * RI) == 0) {
+        // residual add with no duplicate rows: the EXACT loop with the add
+        // (decode's O + residual)
+        hipLaunchKernelGGL((qmv_stream_kernel<F, W, D, NT, false, false, true, W <= 64>), dim3(blocks), dim3(NT), lds,
+                           s, YULE_QMV_ARGS);
     } else {
         YULE_QMV_LAUNCH(false, false);
     }
