@@ -1122,17 +1122,23 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float *__restri
 // The cache rows of the chunk, q and the V rows are loaded before the
 // control block is read: every load is in flight at once, from clamped row
 // indices (rows past max_rows are never touched).
-constexpr uint32_t kChunkThreads = 256;
 constexpr uint32_t kChunkMaxCombine = 1024;   // chunks per head (the runner uses it below 16384 positions)
 
-template <uint32_t HD>
-__global__ __launch_bounds__(kChunkThreads) void attn_chunk_kernel(
+// threads per chunk workgroup (128, 256 or 512; YULE_ATTN_CHUNK_THREADS):
+// the chunk length follows, 16 NT / HD positions
+static uint32_t chunk_threads() {
+    static const int env = env_int("YULE_ATTN_CHUNK_THREADS", 256);
+    return env == 128 || env == 512 ? (uint32_t)env : 256u;
+}
+
+template <uint32_t HD, uint32_t NT>
+__global__ __launch_bounds__(NT) void attn_chunk_kernel(
     // the leading 14 dwords arrive preloaded in SGPRs
     const float *__restrict__ q, const float *__restrict__ kc, const float *__restrict__ vc,
     const uint32_t *__restrict__ ctl, uint32_t group, uint32_t n_kv, uint32_t seq_host, uint32_t max_rows,
     float *__restrict__ out, float *__restrict__ part, float2 *__restrict__ ml, uint32_t *__restrict__ ticket,
     uint32_t max_chunks) {
-    constexpr uint32_t NT = kChunkThreads, ND4 = HD / 4;
+    constexpr uint32_t ND4 = HD / 4, NW = NT / 64;
     constexpr uint32_t LPP = HD / 16;          // lanes per position in the scores, four float4 each
     constexpr uint32_t C = NT / LPP;           // positions per chunk
     constexpr uint32_t NG = NT / ND4;          // position groups in the output
@@ -1140,7 +1146,7 @@ __global__ __launch_bounds__(kChunkThreads) void attn_chunk_kernel(
     static_assert(C % NG == 0 && LPP >= 2 && LPP <= 8, "chunk geometry");
     __shared__ float ps[C];
     __shared__ float red[8];
-    __shared__ float4 ored[4][ND4];
+    __shared__ float4 ored[NW][ND4];
     __shared__ uint32_t last;
     __shared__ float fcs[kChunkMaxCombine], lcs[kChunkMaxCombine];
     const uint32_t h = blockIdx.x, ch = blockIdx.y, tid = threadIdx.x;
@@ -1188,7 +1194,7 @@ __global__ __launch_bounds__(kChunkThreads) void attn_chunk_kernel(
         const float p = ps[pg * PPG + u];
         o.x += p * vv[u].x; o.y += p * vv[u].y; o.z += p * vv[u].z; o.w += p * vv[u].w;
     }
-    // groups inside a wave (lanes d4 + ND4 * j), then the four waves
+    // groups inside a wave (lanes d4 + ND4 * j), then the waves
 #pragma unroll
     for (uint32_t off = ND4; off < 64; off <<= 1) {
         o.x += __shfl_xor(o.x, off, 64); o.y += __shfl_xor(o.y, off, 64);
@@ -1197,13 +1203,30 @@ __global__ __launch_bounds__(kChunkThreads) void attn_chunk_kernel(
     const uint32_t lane = tid & 63u, w = tid >> 6;
     if (lane < ND4) ored[w][lane] = o;
     __syncthreads();
+    // the waves' sums in a fixed order: pairwise for four waves, then on in
+    // wave order
+    auto wave_total = [&](uint32_t d) {
+        float4 t;
+        if constexpr (NW >= 4) {
+            const float4 a = ored[0][d], b = ored[1][d], c = ored[2][d], e = ored[3][d];
+            t = make_float4((a.x + b.x) + (c.x + e.x), (a.y + b.y) + (c.y + e.y), (a.z + b.z) + (c.z + e.z),
+                            (a.w + b.w) + (c.w + e.w));
+        } else {
+            const float4 a = ored[0][d], b = ored[1][d];
+            t = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+        }
+#pragma unroll
+        for (uint32_t i = 4; i < NW; i++) {
+            const float4 c = ored[i][d];
+            t.x += c.x; t.y += c.y; t.z += c.z; t.w += c.w;
+        }
+        return t;
+    };
     if (n_ch == 1) {   // the whole sequence in this chunk
         if (tid < ND4) {
             const float inv = 1.0f / l;
-            const float4 a = ored[0][tid], b = ored[1][tid], c = ored[2][tid], d = ored[3][tid];
-            reinterpret_cast<float4 *>(out)[(size_t)h * ND4 + tid] =
-                make_float4(((a.x + b.x) + (c.x + d.x)) * inv, ((a.y + b.y) + (c.y + d.y)) * inv,
-                            ((a.z + b.z) + (c.z + d.z)) * inv, ((a.w + b.w) + (c.w + d.w)) * inv);
+            const float4 a = wave_total(tid);
+            reinterpret_cast<float4 *>(out)[(size_t)h * ND4 + tid] = make_float4(a.x * inv, a.y * inv, a.z * inv, a.w * inv);
         }
         return;
     }
@@ -1220,12 +1243,12 @@ __global__ __launch_bounds__(kChunkThreads) void attn_chunk_kernel(
     auto st = [](float *p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
     auto ld = [](const float *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
     if (tid < ND4) {
-        const float4 a = ored[0][tid], b = ored[1][tid], c = ored[2][tid], d = ored[3][tid];
+        const float4 a = wave_total(tid);
         float *pp = part + ((size_t)h * max_chunks + ch) * HD + 4 * tid;
-        st(pp + 0, (a.x + b.x) + (c.x + d.x));
-        st(pp + 1, (a.y + b.y) + (c.y + d.y));
-        st(pp + 2, (a.z + b.z) + (c.z + d.z));
-        st(pp + 3, (a.w + b.w) + (c.w + d.w));
+        st(pp + 0, a.x);
+        st(pp + 1, a.y);
+        st(pp + 2, a.z);
+        st(pp + 3, a.w);
     }
     float *mlp = reinterpret_cast<float *>(ml + (size_t)h * max_chunks + ch);
     if (tid == 0) {
@@ -1282,7 +1305,7 @@ __global__ __launch_bounds__(kChunkThreads) void attn_chunk_kernel(
 }
 
 // chunk length of attn_chunk_kernel for a head size (0: not served)
-uint32_t attn_chunk_len(uint32_t hd) { return hd == 64 ? 64u : hd == 128 ? 32u : 0u; }
+uint32_t attn_chunk_len(uint32_t hd) { return hd == 64 || hd == 128 ? chunk_threads() * 16u / hd : 0u; }
 
 size_t attn_chunk_scratch_bytes(uint32_t n_heads, uint32_t hd, uint32_t max_rows) {
     const uint32_t C = attn_chunk_len(hd);
@@ -1305,12 +1328,20 @@ int launch_attn_chunks(hipStream_t s, const float *q, const float *kc, const flo
     float2 *ml = reinterpret_cast<float2 *>(part + (size_t)n_heads * mc * hd);
     uint32_t *ticket = reinterpret_cast<uint32_t *>(ml + (size_t)n_heads * mc);
     const dim3 grid(n_heads, mc);
-    if (hd == 64)
-        hipLaunchKernelGGL(attn_chunk_kernel<64>, grid, dim3(kChunkThreads), 0, s, q, kc, vc, ctl, n_heads / n_kv,
-                           n_kv, seq_host, max_rows, out, part, ml, ticket, mc);
-    else
-        hipLaunchKernelGGL(attn_chunk_kernel<128>, grid, dim3(kChunkThreads), 0, s, q, kc, vc, ctl, n_heads / n_kv,
-                           n_kv, seq_host, max_rows, out, part, ml, ticket, mc);
+#define YULE_CHUNK_LAUNCH(HD, NT)                                                                                  \
+    hipLaunchKernelGGL((attn_chunk_kernel<HD, NT>), grid, dim3(NT), 0, s, q, kc, vc, ctl, n_heads / n_kv, n_kv,   \
+                       seq_host, max_rows, out, part, ml, ticket, mc)
+    const uint32_t nt = chunk_threads();
+    if (hd == 64) {
+        if (nt == 128) YULE_CHUNK_LAUNCH(64, 128);
+        else if (nt == 512) YULE_CHUNK_LAUNCH(64, 512);
+        else YULE_CHUNK_LAUNCH(64, 256);
+    } else {
+        if (nt == 128) YULE_CHUNK_LAUNCH(128, 128);
+        else if (nt == 512) YULE_CHUNK_LAUNCH(128, 512);
+        else YULE_CHUNK_LAUNCH(128, 256);
+    }
+#undef YULE_CHUNK_LAUNCH
     return check_launch("attn_chunks");
 }
 
