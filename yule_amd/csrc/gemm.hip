@@ -1004,10 +1004,10 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(gemm_wav
 // split-K reduction) with four compute waves, 32 rows each as two MFMA A
 // tiles: A = the weights (one row per lane group of 16, the quarter-block
 // 32q..32q+31 bytes of qs per lane quad q), B = X rows 16t..16t+15 (MT
-// tiles of 16), each B fragment read from LDS once for both A tiles: per
-// super-block a wave then reads as many LDS bytes (MT x 8 KB) as its MFMAs
-// take cycles at the CU's LDS rate, where one A tile per wave would leave
-// the MFMAs waiting on LDS half the time.  In a k-step j (h = j / 4,
+// tiles of 16), each B fragment read from LDS once for both A tiles (half
+// the LDS bytes per weight row of one A tile per wave; the K splits, which
+// the wider workgroups need to fill the CUs, also shorten each
+// workgroup's serial super-block chain).  In a k-step j (h = j / 4,
 // u = j % 4) quad q supplies the weights 64q + 32h + 8u + {0,2,1,3,4,6,5,7}
 // (the nibble-pair order of two qs dwords, h the nibble half), and the f16 X
 // pre-pass stores each four k in that order, so a lane's X operand is one
