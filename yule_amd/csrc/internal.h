@@ -106,6 +106,9 @@ struct QmvXf {
     // half of a gate/up pair, same rows) into the L2 of the XCD whose
     // workgroups will read them: that launch's row group g (pf_gbytes bytes
     // of each matrix, pf_total bytes in all) belongs to XCD g % 8
+    // (pf_delay: sleep iterations before the reads; bit 31 set on a Q/K/V
+    // launch with the RoPE epilogue: the layer's K/V cache rows before the
+    // current position too, for the attention launch)
     const uint8_t *pf_w[2] = {nullptr, nullptr};
     uint32_t pf_wgs = 0, pf_gbytes = 0, pf_groups = 0, pf_delay = 0;
     size_t pf_total = 0;

@@ -178,7 +178,7 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const uint8_t *vb0, cons
         const uint32_t pfw = gridDim.x - nblk;
         // prefetch workgroup: one dword of every 128-byte line of the row
         // groups that the next launch runs on this workgroup's XCD
-        for (uint32_t i = 0; i < xf.pf_delay; i++) __builtin_amdgcn_s_sleep(8);
+        for (uint32_t i = 0; i < (xf.pf_delay & 0x7fffffffu); i++) __builtin_amdgcn_s_sleep(8);
         const uint32_t xcd = blockIdx.x & 7u, rank = (blockIdx.x - nblk) >> 3, nr = pfw >> 3;
         const uint32_t lpg = (xf.pf_gbytes + 127) / 128, nseg = xf.pf_w[1] ? 2u : 1u;
         const uint32_t mine = xf.pf_groups > xcd + 8 * rank ? (xf.pf_groups - xcd - 8 * rank + 8 * nr - 1) / (8 * nr) : 0;
@@ -187,6 +187,18 @@ __global__ __launch_bounds__(NT) void qmv_stream_kernel(const uint8_t *vb0, cons
             const uint32_t gi = j / (lpg * nseg), rem = j % (lpg * nseg), sgi = rem / lpg, line = rem % lpg;
             const size_t off = (size_t)(xcd + 8 * (rank + gi * nr)) * xf.pf_gbytes + (size_t)line * 128;
             if (off < xf.pf_total) acc ^= *reinterpret_cast<const uint32_t *>((sgi ? xf.pf_w[1] : xf.pf_w[0]) + off);
+        }
+        if ((xf.pf_delay >> 31) && rope_ctl) {
+            // (pf_delay bit 31, a Q/K/V launch with the RoPE epilogue) this
+            // layer's K and V cache rows before the current position, for the
+            // attention launch that follows: its workgroups on every XCD read
+            // all of them, so each XCD's prefetch workgroups read them all
+            const uint32_t pos = rope_ctl[0];
+            const uint32_t lines = (uint32_t)(((size_t)pos * (st2 - st1) * sizeof(float) + 127) / 128);
+            for (uint32_t j = rank * NT + tid; j < 2 * lines; j += nr * NT) {
+                const float *base = j < lines ? xf.kc : xf.vc;
+                acc ^= __builtin_bit_cast(uint32_t, base[(size_t)(j < lines ? j : j - lines) * 32]);
+            }
         }
         if (acc == 0x9E3779B9u && n_rows == 0) sg.y[0][0] = 0.f;   // keeps the loads; never true
         return;

@@ -74,7 +74,7 @@ struct yule_hip_runner {
     // experimental: launches carry extra workgroups that read the next
     // launch's weights into its XCDs' L2 (bit 1: O -> gate/up, 2: gate/up ->
     // down, 4: Q/K/V -> O)
-    uint32_t pf_mask = 4, pf_wgs = 256, pf_delay = 0;
+    uint32_t pf_mask = 4 | 8, pf_wgs = 256, pf_delay = 0;
     hipGraph_t graph_n[2] = {nullptr, nullptr};
     hipGraphExec_t exec_n[2] = {nullptr, nullptr};
     uint32_t pos = 0;  // host mirror of ctl[0]
@@ -219,6 +219,9 @@ int enqueue_step(yule_hip_runner *r, bool split) {
             norm.hd = r->hd;
         }
         if ((r->pf_mask & 4) && fuse) plan_prefetch(r, norm, L.to, L.wo, nullptr, r->dim, qd);
+        // bit 8: those prefetch workgroups also read the layer's K/V cache
+        // rows before the position, for the chunked attention launch
+        if ((r->pf_mask & 8) && chunked && norm.pf_wgs) norm.pf_delay |= 1u << 31;
         if (L.tq == L.tk && L.tk == L.tv) {
             const QmvSeg segs[3] = {{L.wq, r->q, qd}, {L.wk, r->k, kvd}, {L.wv, r->v, kvd}};
             if ((rc = launch_qmv_fused(s, L.tq, segs, 3, xin, r->dim, norm))) return rc;
@@ -595,7 +598,7 @@ int yule_hip_runner_create(yule_hip_backend *be, const yule_model_desc *d, yule_
         return v < lo ? lo : v > hi ? hi : v;
     };
     r->multi_steps = (uint32_t)knob("YULE_RUNNER_GRAPH_STEPS", 1, kMaxGraphSteps, r->multi_steps);
-    r->pf_mask = (uint32_t)knob("YULE_RUNNER_PREFETCH", 0, 7, r->pf_mask);
+    r->pf_mask = (uint32_t)knob("YULE_RUNNER_PREFETCH", 0, 15, r->pf_mask);
     r->pf_wgs = (uint32_t)knob("YULE_RUNNER_PREFETCH_WGS", 0, 2048, r->pf_wgs) & ~7u;
     r->pf_delay = (uint32_t)knob("YULE_RUNNER_PREFETCH_DELAY", 0, 4096, r->pf_delay);
     for (const auto &L : r->layers)
