@@ -1123,6 +1123,8 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float *__restri
 // control block is read: every load is in flight at once, from clamped row
 // indices (rows past max_rows are never touched).
 constexpr uint32_t kChunkMaxCombine = 1024;   // chunks per head (the runner uses it below 16384 positions)
+// one head's ticket per 128-byte line: the heads' atomics do not queue on one line
+constexpr uint32_t kTicketStride = 32;
 
 // threads per chunk workgroup (128, 256 or 512; YULE_ATTN_CHUNK_THREADS):
 // the chunk length follows, 16 NT / HD positions
@@ -1264,7 +1266,8 @@ __global__ __launch_bounds__(NT) void attn_chunk_kernel(
         __builtin_amdgcn_s_waitcnt(0);
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         if (tid == 0)
-            last = __hip_atomic_fetch_add(ticket + h, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == n_ch - 1;
+            last = __hip_atomic_fetch_add(ticket + h * kTicketStride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                   n_ch - 1;
     }
     __syncthreads();
     if (!last) return;
@@ -1301,7 +1304,7 @@ __global__ __launch_bounds__(NT) void attn_chunk_kernel(
         for (uint32_t c = kPre; c < n_ch; c++) a += fcs[c] * ld(ph + (size_t)c * HD + tid);
         out[(size_t)h * HD + tid] = a / L;
     }
-    if (tid == 0) __hip_atomic_store(ticket + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) __hip_atomic_store(ticket + h * kTicketStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // chunk length of attn_chunk_kernel for a head size (0: not served)
@@ -1312,7 +1315,7 @@ size_t attn_chunk_scratch_bytes(uint32_t n_heads, uint32_t hd, uint32_t max_rows
     if (!C) return 0;
     const size_t mc = (max_rows + C - 1) / C;
     return (size_t)n_heads * mc * hd * sizeof(float) + (size_t)n_heads * mc * sizeof(float2) +
-           (size_t)n_heads * sizeof(uint32_t) + 256;
+           (size_t)n_heads * kTicketStride * sizeof(uint32_t) + 256;
 }
 
 // scratch: partials, (m, l) pairs, then the per-head tickets, which must be
