@@ -1123,8 +1123,9 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float *__restri
 // control block is read: every load is in flight at once, from clamped row
 // indices (rows past max_rows are never touched).
 constexpr uint32_t kChunkMaxCombine = 1024;   // chunks per head (the runner uses it below 16384 positions)
-// one head's ticket per 128-byte line: the heads' atomics do not queue on one line
-constexpr uint32_t kTicketStride = 32;
+// one head's ticket per 128-byte line: the heads' atomics do not queue on one
+// line; likewise each chunk's (m, l) pair
+constexpr uint32_t kTicketStride = 32, kMlStride = 16;
 
 // threads per chunk workgroup (128, 256 or 512; YULE_ATTN_CHUNK_THREADS):
 // the chunk length follows, 16 NT / HD positions
@@ -1252,7 +1253,7 @@ __global__ __launch_bounds__(NT) void attn_chunk_kernel(
         st(pp + 2, a.z);
         st(pp + 3, a.w);
     }
-    float *mlp = reinterpret_cast<float *>(ml + (size_t)h * max_chunks + ch);
+    float *mlp = reinterpret_cast<float *>(ml + ((size_t)h * max_chunks + ch) * kMlStride);
     if (tid == 0) {
         st(mlp, m);
         st(mlp + 1, l);
@@ -1274,7 +1275,7 @@ __global__ __launch_bounds__(NT) void attn_chunk_kernel(
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     // combine: every (m, l) pair and, for up to kPre chunks, the thread's
     // partial outputs are loaded at once (one memory round trip)
-    const float *mh = reinterpret_cast<const float *>(ml + (size_t)h * max_chunks);
+    const float *mh = reinterpret_cast<const float *>(ml + (size_t)h * max_chunks * kMlStride);
     const float *ph = part + (size_t)h * max_chunks * HD;
     constexpr uint32_t kPre = 8;
     const uint32_t dd = tid < HD ? tid : 0u;
@@ -1283,7 +1284,7 @@ __global__ __launch_bounds__(NT) void attn_chunk_kernel(
     for (uint32_t c = 0; c < kPre; c++) pv[c] = ld(ph + (size_t)(c < n_ch ? c : 0u) * HD + dd);
     float mm = -INFINITY;
     for (uint32_t c = tid; c < n_ch; c += NT) {
-        const float mc = ld(mh + 2 * c), lc = ld(mh + 2 * c + 1);
+        const float mc = ld(mh + 2 * kMlStride * c), lc = ld(mh + 2 * kMlStride * c + 1);
         fcs[c] = mc;
         lcs[c] = lc;
         mm = fmaxf(mm, mc);
@@ -1314,7 +1315,7 @@ size_t attn_chunk_scratch_bytes(uint32_t n_heads, uint32_t hd, uint32_t max_rows
     const uint32_t C = attn_chunk_len(hd);
     if (!C) return 0;
     const size_t mc = (max_rows + C - 1) / C;
-    return (size_t)n_heads * mc * hd * sizeof(float) + (size_t)n_heads * mc * sizeof(float2) +
+    return (size_t)n_heads * mc * hd * sizeof(float) + (size_t)n_heads * mc * kMlStride * sizeof(float2) +
            (size_t)n_heads * kTicketStride * sizeof(uint32_t) + 256;
 }
 
@@ -1329,7 +1330,7 @@ int launch_attn_chunks(hipStream_t s, const float *q, const float *kc, const flo
     if (mc > kChunkMaxCombine) return set_error(YULE_ERR_INVALID, "chunked attention: sequence too long");
     float *part = static_cast<float *>(scratch);
     float2 *ml = reinterpret_cast<float2 *>(part + (size_t)n_heads * mc * hd);
-    uint32_t *ticket = reinterpret_cast<uint32_t *>(ml + (size_t)n_heads * mc);
+    uint32_t *ticket = reinterpret_cast<uint32_t *>(ml + (size_t)n_heads * mc * kMlStride);
     const dim3 grid(n_heads, mc);
 #define YULE_CHUNK_LAUNCH(HD, NT)                                                                                  \
     hipLaunchKernelGGL((attn_chunk_kernel<HD, NT>), grid, dim3(NT), 0, s, q, kc, vc, ctl, n_heads / n_kv, n_kv,   \
