@@ -536,6 +536,10 @@ static void launch_stream_nt(hipStream_t s, const Segs &sg, const float *x, uint
     // 1663 -> 1684 tok/s against 704 (4 or 6 waves: 1618)
     const uint32_t rows = xf.pair ? sg.start[1] : sg.total;
     const uint32_t blocks = stream_blocks(W, NT, F::BS, bpr, rows, xf.pair, xf.epi == kEpiArgmax);
+    // the argmax epilogue's launches (the lm_head: ~8 rows per team at
+    // 32000 rows) keep three rows in flight per team, the others two
+    static const bool deep = env_flag("YULE_QMV_ARGMAX_DEEP", true);
+    if (deep && xf.epi == kEpiArgmax) return launch_stream_d<F, W, 3, NT>(s, sg, x, bpr, blocks, xf);
     launch_stream_d<F, W, 2, NT>(s, sg, x, bpr, blocks, xf);
 }
 
